@@ -1,0 +1,198 @@
+# SPDX-License-Identifier: Apache-2.0
+"""Flat-search benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2] [--nq N]
+
+A step is one exact search of the configuration's whole query batch against the
+whole database, with queries, database and outputs already resident in HBM (the
+device-pointer C ABI entry point; the host-pointer entry adds PCIe copies and is
+not what `value` measures). Default workload: BASELINE.json configs[1] (C2):
+L2, nb = 1,000,000 x d = 128 GMM(1,024 centres, sigma 0.3), nq = 10,000, k = 100,
+seed 1. Prints ONE JSON line on stdout; progress goes to stderr.
+
+roofline: the dominant kernel is scan_filter (fused fp32 MFMA distance tile +
+threshold filter over the full database, one launch per step). achieved =
+2 * nq * nb * d algorithmic FLOP per launch / its mean duration, timed with HIP
+events on the launch stream over the timed steps.
+
+cpu_baseline: the oracle's restatement of the reference CPU path (cpuSearch,
+src/FlatIndex.mm:259-290; serial, as the reference) timed on a bounded prefix of
+the same query batch against the full database, on one host core.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "metal-flat_amd"), os.path.join(ROOT, "oracle")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+WORKLOADS = {
+    "C1": ("C1: flat L2, nb=100,000 x d=128 integer-valued U{0..255}, nq=1,000, k=10, seed 0", 0, 10),
+    "C2": ("C2: flat L2, nb=1,000,000 x d=128 GMM(1024 centres, sigma 0.3), nq=10,000, k=100, seed 1", 0, 100),
+    "C3": ("C3: flat inner product, nb=1,000,000 x d=768 unit N(0,I), nq=10,000, k=100, seed 2", 1, 100),
+    "C4": ("C4: flat L2, nb=10,000,000 x d=96 U[-1,1], nq={nq}, k=10, seed 3", 0, 10),
+    "C5": ("C5: k-means assignment (k=1), 2,000,000 points x d=128 GMM(4096, sigma 0.5) vs 65,536 centroids, seed 4", 0, 1),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_data(cfg, nq_override):
+    import datagen
+
+    if cfg == "C1":
+        return datagen.sift_like()
+    if cfg == "C2":
+        return datagen.gmm()
+    if cfg == "C3":
+        return datagen.unit_normal()
+    if cfg == "C4":
+        return datagen.uniform_pm1(nq=nq_override or 64)
+    if cfg == "C5":
+        return datagen.kmeans_assign()
+    raise SystemExit(f"unknown config {cfg}")
+
+
+def cpu_baseline(x, q, k, metric, gpu_ids, seconds_target=12.0):
+    """Times the oracle (one core) on a prefix of the queries sized to ~10-15 s."""
+    import numpy as np
+    import oracle
+
+    nb, d = x.shape
+    # per-query cost ~ nb*d sequential fp32 steps; calibrate on one query
+    t0 = time.perf_counter()
+    oracle.flat_search(x, q[:1], k, metric=metric, threads=1)
+    one = max(time.perf_counter() - t0, 1e-6)
+    n = int(max(1, min(q.shape[0], seconds_target / one)))
+    t0 = time.perf_counter()
+    oi, _ = oracle.flat_search(x, q[:n], k, metric=metric, threads=1)
+    dt = time.perf_counter() - t0
+    recall = float(np.mean([len(set(oi[r].tolist()) & set(gpu_ids[r].tolist())) / k for r in range(n)]))
+    return {
+        "value": n / dt,
+        "unit": "queries/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"first {n} of the {q.shape[0]} queries against all {nb} rows (d={d}, k={k}), "
+                  f"{dt:.1f} s on one host core; GPU/oracle id agreement on the sample {recall:.5f}",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", default="C2", choices=sorted(WORKLOADS))
+    ap.add_argument("--nq", type=int, default=0, help="query count override (C4: 1, 16 or 64)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the database would shard by rows with an all-gather merge of per-GPU top-k; "
+              "not built). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import hipmem
+    import mflat
+
+    mflat.load()
+    name, metric, k = WORKLOADS[args.config]
+    t0 = time.perf_counter()
+    x, q = make_data(args.config, args.nq)
+    if args.nq and args.config != "C4":
+        q = q[: args.nq]
+    nb, d = x.shape
+    nq = q.shape[0]
+    log(f"[bench] {args.config}: nb={nb} d={d} nq={nq} k={k} data in {time.perf_counter() - t0:.1f}s")
+
+    idx = mflat.FlatIndex(d, metric)
+    if not idx.ready():
+        raise SystemExit("no usable gfx950 device")
+    t0 = time.perf_counter()
+    idx.add(x)
+    log(f"[bench] add {time.perf_counter() - t0:.2f}s")
+    qd = hipmem.DeviceArray.from_numpy(q)
+    ids = hipmem.DeviceArray((nq, k), np.int32)
+    dist = hipmem.DeviceArray((nq, k), np.float32)
+
+    for i in range(args.warmup):
+        idx.search_device(qd, k, ids, dist)
+        log(f"[bench] warmup {i + 1}/{args.warmup} done")
+    hipmem.synchronize()
+
+    mflat.profile_reset()
+    mflat.profile_enable(True)
+    hipmem.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        idx.search_device(qd, k, ids, dist)
+    hipmem.synchronize()
+    elapsed = time.perf_counter() - t0
+    mflat.profile_enable(False)
+    log(f"[bench] {args.steps} steps in {elapsed:.3f}s")
+
+    kern = {}
+    for fam in ("scan_filter", "scan_sample", "select", "argmin", "norms", "prep"):
+        ms, n = mflat.profile_read(fam)
+        if n:
+            kern[fam] = {"total_ms": round(ms, 4), "launches": n, "mean_ms": round(ms / n, 4)}
+
+    gpu_ids = ids.numpy()
+    ms_per_step = elapsed * 1000.0 / args.steps
+    flop = 2.0 * nq * nb * d
+    scan = kern.get("scan_filter")
+    if args.config == "C4" and nq <= 16:
+        byts = nb * d * 4 + nq * d * 4 + nq * k * 8
+        mean_s = scan["total_ms"] / scan["launches"] / 1000.0
+        ach = byts / mean_s / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None}
+    else:
+        per_launch = flop * args.steps / scan["launches"]
+        mean_s = scan["total_ms"] / scan["launches"] / 1000.0
+        ach = per_launch / mean_s / 1e12
+        roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None}
+
+    out = {
+        "metric": "QPS + % of MFMA/HBM roofline, flat L2 d=128 nb=1M k=100 (1 GPU)",
+        "value": round(nq * args.steps / elapsed, 2),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": name.format(nq=nq), "nb": nb, "d": d, "nq": nq, "k": k,
+                   "metric": "L2" if metric == 0 else "IP", "parallelism": "single GPU"},
+        "roofline": roof,
+        "kernels": kern,
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline(x, q, k, metric, gpu_ids)
+        log("[bench] cpu baseline done")
+    idx.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

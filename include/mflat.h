@@ -1,0 +1,136 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/* mflat.h -- C ABI of the MI355X-native exact flat-search library (libmflat.so).
+ *
+ * Drop-in for the flat-search part of metal-flat's C ABI
+ * (reference: c/include/mflat.h:31-90, implementation c/mflat.cpp:32-129).
+ * Same opaque handle, same status codes, same caller-owned output buffers,
+ * same row-major nearest-first results with -1 id padding.
+ *
+ * Buffer contract for mflat_flat_search: out_ids and out_distances are
+ * caller-allocated, each holding at least m * k elements (either may be NULL).
+ * *out_k_used (nullable) receives the number of columns actually written;
+ * the row stride of both outputs is k_used (reference c/mflat.cpp:42-50).
+ *
+ * Divergences from the reference, all deliberate:
+ *  - MFLAT_MAX_K is 1024 (reference 64, include/metalflat/FlatIndex.h:43);
+ *    k above it is clamped with a one-time warning per index, as in the
+ *    reference (src/FlatIndex.mm:298-304).
+ *  - There is no CPU fallback. Without a usable HIP device an index can be
+ *    created and filled (mflat_flat_ready() == 0) but mflat_flat_search
+ *    returns MFLAT_ERR_NOT_READY (reference: exact CPU path,
+ *    src/FlatIndex.mm:317-321).
+ *  - The IVF / IVF-PQ entry points (reference c/include/mflat.h:92-129) are
+ *    not part of this library.
+ *  - Additive entry points (device-pointer search/add, kernel timing) follow
+ *    the flat block; they have no counterpart in the reference.
+ */
+#ifndef MFLAT_H
+#define MFLAT_H
+
+#include <stdint.h>
+
+#define MFLAT_API __attribute__((visibility("default")))
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MFLAT_VERSION_MAJOR 0
+#define MFLAT_VERSION_MINOR 1
+#define MFLAT_VERSION_PATCH 0
+#define MFLAT_MAX_K 1024        /* largest k one search returns (reference: 64) */
+
+/* value-stable; reference c/include/mflat.h:36-40 */
+typedef enum {
+    MFLAT_METRIC_L2            = 0,   /* squared Euclidean, smaller = nearer */
+    MFLAT_METRIC_INNER_PRODUCT = 1,   /* dot product, larger = nearer        */
+    MFLAT_METRIC_COSINE        = 2    /* dot of L2-normalised vectors        */
+} mflat_metric_t;
+
+/* value-stable; reference c/include/mflat.h:42-49 */
+typedef enum {
+    MFLAT_OK            = 0,
+    MFLAT_ERR_NULL_ARG  = 1,    /* a required pointer was NULL                     */
+    MFLAT_ERR_BAD_ARG   = 2,    /* dim/n/m/k out of range                          */
+    MFLAT_ERR_ALLOC     = 3,    /* host or device allocation failed                */
+    MFLAT_ERR_NOT_READY = 4,    /* no usable HIP device for this index             */
+    MFLAT_ERR_INTERNAL  = 5     /* unexpected exception or HIP runtime error       */
+} mflat_status_t;
+
+/* reference c/include/mflat.h:51-53, c/mflat.cpp:72-73,86-96 */
+MFLAT_API const char* mflat_version(void);               /* "0.1.0"             */
+MFLAT_API const char* mflat_status_str(mflat_status_t);  /* static; do not free */
+MFLAT_API int         mflat_max_k(void);                 /* MFLAT_MAX_K         */
+
+/* ---------------- Logging (reference c/include/mflat.h:55-74) ------------- */
+typedef enum {
+    MFLAT_LOG_INFO  = 0,
+    MFLAT_LOG_WARN  = 1,
+    MFLAT_LOG_ERROR = 2,
+    MFLAT_LOG_OFF   = 3          /* threshold only; never delivered to a handler */
+} mflat_log_level_t;
+
+/* msg: NUL-terminated, no "[mflat]" prefix, no newline; user round-trips. */
+typedef void (*mflat_log_handler_t)(mflat_log_level_t level, const char* msg, void* user);
+
+/* handler == NULL restores the built-in stderr sink (reference c/mflat.cpp:75-79). */
+MFLAT_API void              mflat_set_log_handler(mflat_log_handler_t handler, void* user);
+MFLAT_API void              mflat_set_log_level(mflat_log_level_t threshold);
+MFLAT_API mflat_log_level_t mflat_log_level(void);
+
+/* ---------------- FlatIndex (exact) -------------------------------------- */
+typedef struct mflat_flat_index mflat_flat_index_t;      /* opaque */
+
+/* reference c/mflat.cpp:99-104: dim <= 0 -> NULL + MFLAT_ERR_BAD_ARG;
+   an unknown metric value maps to L2 (c/mflat.cpp:32-38). */
+MFLAT_API mflat_flat_index_t*
+mflat_flat_create(int dim, mflat_metric_t metric, mflat_status_t* out_status);
+/* reference c/mflat.cpp:105; NULL is a no-op */
+MFLAT_API void mflat_flat_free(mflat_flat_index_t*);
+
+/* reference c/mflat.cpp:106-108: 1 = HIP device usable, 0 = none */
+MFLAT_API int mflat_flat_ready(const mflat_flat_index_t*);
+MFLAT_API int mflat_flat_size (const mflat_flat_index_t*);
+MFLAT_API int mflat_flat_dim  (const mflat_flat_index_t*);
+
+/* reference c/mflat.cpp:110-116: append n row-major vectors (n*dim floats,
+   host memory, borrowed for the call). NULL -> NULL_ARG, n < 0 -> BAD_ARG,
+   n == 0 -> OK. Cosine rows are stored L2-normalised. */
+MFLAT_API mflat_status_t mflat_flat_add(mflat_flat_index_t*, const float* vectors, int n);
+/* reference c/mflat.cpp:117-121 */
+MFLAT_API mflat_status_t mflat_flat_reset(mflat_flat_index_t*);
+/* reference c/mflat.cpp:122-129: m < 0 or k < 1 -> BAD_ARG; m == 0 -> OK with
+   *out_k_used = 0. queries: m*dim floats in host memory. */
+MFLAT_API mflat_status_t mflat_flat_search(mflat_flat_index_t*, const float* queries,
+        int m, int k, int32_t* out_ids, float* out_distances, int* out_k_used);
+
+/* ---------------- Additive: device-resident data ------------------------- */
+/* No counterpart in the reference (its buffers are unified memory,
+   src/FlatIndex.mm:163-171). For callers whose data already lives in HBM.
+   All pointers are device pointers of the index's device; `stream` is a
+   hipStream_t (NULL = the index's own stream). The call returns after the
+   results are complete on the device. Same argument checks and status codes
+   as mflat_flat_search / mflat_flat_add; out_ids / out_distances hold m*k
+   elements with row stride k_used. */
+MFLAT_API mflat_status_t mflat_flat_search_device(mflat_flat_index_t*, const float* d_queries,
+        int m, int k, int32_t* d_out_ids, float* d_out_distances, int* out_k_used,
+        void* stream);
+MFLAT_API mflat_status_t mflat_flat_add_device(mflat_flat_index_t*, const float* d_vectors,
+        int n, void* stream);
+
+/* ---------------- Additive: kernel timing -------------------------------- */
+/* No counterpart in the reference. When enabled, every launch of the library's
+   kernels is bracketed with HIP events on the stream it runs on; the per-kernel
+   totals accumulate process-wide until reset. name: kernel family, one of
+   "scan_filter" (fused distance + threshold filter over the database, the
+   hot kernel), "scan_sample" (the same kernel over the row sample that sets
+   the thresholds), "select" (per-query top-k select / merge), "argmin"
+   (fused k = 1), "norms", "prep". Returns 0 and fills the outputs, or -1 for an unknown name. */
+MFLAT_API void mflat_profile_enable(int on);
+MFLAT_API void mflat_profile_reset(void);
+MFLAT_API int  mflat_profile_read(const char* name, double* total_ms, long long* launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MFLAT_H */

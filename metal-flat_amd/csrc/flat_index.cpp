@@ -1,0 +1,471 @@
+// SPDX-License-Identifier: Apache-2.0
+// flat_index.cpp -- host side of the flat-search hot path on one MI355X.
+//
+// Search = threshold filtering on the GPU, in levels (reference loop it
+// replaces: src/FlatIndex.mm:294-421):
+//
+//   L0  sample:  exact top-k of every query over a strided sample of R0
+//                database rows (scan_filter with no bound, then select). Its
+//                k-th (key, id) is a GUARANTEED bound: the k-th best over any
+//                subset is never better than the k-th best over the whole
+//                database. Its j-th (j <= k, from a Poisson tail estimate) is a
+//                SPECULATIVE bound expected to admit ~j*nb/R0 rows.
+//   L1  full:    scan_filter over all rows with the speculative bound, then
+//                select. The result is exact iff no candidate region overflowed
+//                and at least k rows passed (every row that did not pass ranks
+//                after all k that did).
+//   retry:       queries failing that test rerun L1 alone, with the guaranteed
+//                bound (too few passed) or with the k-th best of what was stored
+//                (a region overflowed; regions hold >= 2k entries, so each
+//                retry admits at least k fewer rows). Exactness never depends on
+//                the estimate, only the amount of work does.
+//
+// Small databases (nb <= 2*R0) skip the levels: one unbounded pass.
+#include "flat_index.hpp"
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+#include "log.hpp"
+
+namespace mflat_amd {
+namespace {
+
+void hipCheck(hipError_t e, const char* what) {
+    if (e == hipSuccess) return;
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) throw std::bad_alloc();
+    throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+#define HIPC(x) hipCheck((x), #x)
+
+constexpr int64_t kTargetWG = 2048;             // scan workgroups wanted per launch
+constexpr size_t kCandBudget = size_t(1536) << 20;  // candidate workspace per batch
+constexpr size_t kStageBytes = size_t(256) << 20;   // host->device staging chunk
+
+int64_t roundUp(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    void ensure(size_t b) {
+        if (b <= bytes) return;
+        release();
+        const size_t want = std::max(b, bytes + bytes / 2);
+        HIPC(hipMalloc(&p, want));
+        bytes = want;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+    template <class T> T* as() const { return static_cast<T*>(p); }
+};
+
+// Smallest j in [1, k] with P(Poisson(lambda) >= j) <= 1e-3: the chance that a
+// speculative bound taken at the sample's j-th best admits fewer than k rows.
+int chooseJ(int k, double lambda) {
+    double term = std::exp(-lambda), cdf = term;
+    for (int j = 1; j <= k; ++j) {
+        if (1.0 - cdf <= 1e-3) return j;
+        term *= lambda / j;
+        cdf += term;
+    }
+    return k;
+}
+
+void splitPlan(int64_t nrows, int nqb, int64_t& rowsPerSplit, int& nsplit) {
+    const int64_t ntiles = std::max<int64_t>(1, (nrows + kBM - 1) / kBM);
+    int64_t want = std::max<int64_t>(1, (kTargetWG + nqb - 1) / nqb);
+    want = std::min(want, ntiles);
+    const int64_t tps = (ntiles + want - 1) / want;
+    nsplit = (int)((ntiles + tps - 1) / tps);
+    rowsPerSplit = tps * kBM;
+}
+
+int pow2ceil(int64_t x) {
+    int p = 1;
+    while (p < x) p <<= 1;
+    return p;
+}
+
+struct Plan {
+    bool direct = true;
+    int64_t R0 = 0;       // sample rows
+    int stride = 1;       // sample row r is database row r*stride
+    int j = 1;            // speculative rank
+    int64_t rps0 = 0;
+    int nsplit0 = 1, cap0 = 1;
+    int64_t rps1 = 0;
+    int nsplit1 = 1, cap1 = 1;
+    size_t perQuery = 0;  // candidate entries per query (max over levels)
+};
+
+}  // namespace
+
+struct FlatIndex::Impl {
+    int dim = 0, dpad = 0;
+    Metric metric = Metric::L2;
+    int device = -1;
+    bool ready = false;
+    bool warnedK = false;
+    hipStream_t stream = nullptr;
+
+    int64_t nb = 0;
+    int64_t capRows = 0;
+    DevBuf X, xn;
+
+    // strided sample of the database (L0)
+    int64_t sampleR = 0;
+    int sampleStride = 0;
+    int64_t sampleNb = -1;
+    DevBuf sX, sXn, sIdx;
+
+    // per-search workspace
+    DevBuf stage, qin, outIds, outVals;
+    DevBuf qbuf, qnorm, cand, cnt;
+    DevBuf tauSk, tauSi, tauGk, tauGi, tauKk, tauKi, status;
+    DevBuf cQ, cQn, cTk, cTi, cIdx, cSel;
+
+    int kernMetric() const { return metric == Metric::L2 ? 0 : 1; }
+    float emptyValue() const { return metric == Metric::L2 ? INFINITY : -INFINITY; }
+
+    void setDevice() const {
+        if (device >= 0) HIPC(hipSetDevice(device));
+    }
+
+    Plan plan(int64_t mb, int k) const {
+        Plan pl;
+        const int nqb = (int)((mb + kBN - 1) / kBN);
+        int64_t r = (int64_t)std::ceil(std::sqrt(16.0 * (double)nb));
+        r = std::max<int64_t>(r, std::max<int64_t>(4LL * k, 256));
+        r = roundUp(r, kBM);
+        if (nb <= 2 * r) {
+            pl.direct = true;
+            splitPlan(nb, nqb, pl.rps1, pl.nsplit1);
+            pl.cap1 = (int)pl.rps1;
+            pl.perQuery = (size_t)pl.nsplit1 * pl.cap1;
+            return pl;
+        }
+        pl.direct = false;
+        pl.R0 = r;
+        pl.stride = (int)(nb / r);
+        const double lambda = (double)k * (double)r / (double)nb;
+        pl.j = chooseJ(k, lambda);
+        splitPlan(r, nqb, pl.rps0, pl.nsplit0);
+        pl.cap0 = (int)pl.rps0;
+        splitPlan(nb, nqb, pl.rps1, pl.nsplit1);
+        const double e1 = (double)pl.j * (double)nb / (double)r;   // expected survivors
+        const int64_t perSplit = (int64_t)(2.0 * e1 / pl.nsplit1) + 64;
+        pl.cap1 = std::max<int>({2 * k, 64, pow2ceil(perSplit)});
+        pl.perQuery = std::max((size_t)pl.nsplit0 * pl.cap0, (size_t)pl.nsplit1 * pl.cap1);
+        return pl;
+    }
+
+    void growRows(int64_t need, hipStream_t s) {
+        if (need <= capRows) return;
+        const int64_t newCap = std::max(need, roundUp(capRows + capRows / 2, kBM));
+        void* nx = nullptr;
+        void* nn = nullptr;
+        HIPC(hipMalloc(&nx, (size_t)newCap * dpad * sizeof(float)));
+        hipError_t e = hipMalloc(&nn, (size_t)newCap * sizeof(float));
+        if (e != hipSuccess) { (void)hipFree(nx); hipCheck(e, "hipMalloc(norms)"); }
+        HIPC(hipMemsetAsync(nx, 0, (size_t)newCap * dpad * sizeof(float), s));
+        HIPC(hipMemsetAsync(nn, 0, (size_t)newCap * sizeof(float), s));
+        if (nb > 0) {
+            HIPC(hipMemcpyAsync(nx, X.p, (size_t)nb * dpad * sizeof(float), hipMemcpyDeviceToDevice, s));
+            HIPC(hipMemcpyAsync(nn, xn.p, (size_t)nb * sizeof(float), hipMemcpyDeviceToDevice, s));
+        }
+        HIPC(hipStreamSynchronize(s));
+        X.release();
+        xn.release();
+        X.p = nx; X.bytes = (size_t)newCap * dpad * sizeof(float);
+        xn.p = nn; xn.bytes = (size_t)newCap * sizeof(float);
+        capRows = newCap;
+    }
+
+    void append(const float* src, int n, hipMemcpyKind kind, hipStream_t s) {
+        if (n <= 0) return;
+        if (nb + (int64_t)n > (int64_t)INT_MAX) throw BadArg("database would exceed 2^31-1 rows");
+        if (!ready) { nb += n; return; }
+        setDevice();
+        growRows(roundUp(nb + n, kBM), s);
+        float* dst = X.as<float>() + nb * dpad;
+        if (dim == dpad) {
+            HIPC(hipMemcpyAsync(dst, src, (size_t)n * dim * sizeof(float), kind, s));
+        } else {
+            const int64_t chunk = std::max<int64_t>(1, (int64_t)(kStageBytes / (sizeof(float) * dim)));
+            for (int64_t r0 = 0; r0 < n; r0 += chunk) {
+                const int64_t rn = std::min<int64_t>(chunk, n - r0);
+                stage.ensure((size_t)rn * dim * sizeof(float));
+                HIPC(hipMemcpyAsync(stage.p, src + r0 * dim, (size_t)rn * dim * sizeof(float), kind, s));
+                launch_pack_rows(stage.as<float>(), rn, dim, dst + r0 * dpad, rn, dpad, s);
+            }
+        }
+        if (metric == Metric::Cosine) launch_normalize_rows(dst, n, dpad, s);
+        launch_row_norms(dst, n, dpad, xn.as<float>() + nb, s);
+        HIPC(hipStreamSynchronize(s));
+        nb += n;
+    }
+
+    void ensureSample(const Plan& pl, hipStream_t s) {
+        if (sampleNb == nb && sampleR == pl.R0 && sampleStride == pl.stride) return;
+        std::vector<int> idx((size_t)pl.R0);
+        for (int64_t r = 0; r < pl.R0; ++r) idx[(size_t)r] = (int)(r * pl.stride);
+        sIdx.ensure(idx.size() * sizeof(int));
+        sX.ensure((size_t)pl.R0 * dpad * sizeof(float));
+        sXn.ensure((size_t)pl.R0 * sizeof(float));
+        HIPC(hipMemcpyAsync(sIdx.p, idx.data(), idx.size() * sizeof(int), hipMemcpyHostToDevice, s));
+        launch_gather_rows(X.as<float>(), sIdx.as<int>(), (int)pl.R0, dpad, sX.as<float>(), pl.R0, s);
+        launch_gather_f32(xn.as<float>(), sIdx.as<int>(), (int)pl.R0, sXn.as<float>(), s);
+        HIPC(hipStreamSynchronize(s));
+        sampleNb = nb;
+        sampleR = pl.R0;
+        sampleStride = pl.stride;
+    }
+
+    void scan(const float* Xs, const float* xns, int64_t nrows, int64_t rps, int nsplit, int idStride,
+              const float* Q, const float* qn, int nq, const float* tk, const int* ti, int cap,
+              hipStream_t s, bool sample = false) {
+        const int nqb = (nq + kBN - 1) / kBN;
+        cand.ensure((size_t)nq * nsplit * cap * sizeof(uint2));
+        cnt.ensure((size_t)nq * nsplit * sizeof(int));
+        ScanParams p;
+        p.X = Xs; p.xnorm = xns; p.nrows = nrows; p.rows_per_split = rps; p.nsplit = nsplit;
+        p.id_stride = idStride;
+        p.Q = Q; p.qnorm = qn; p.nq = nq; p.nqb = nqb; p.dpad = dpad;
+        p.tau_key = tk; p.tau_id = ti;
+        p.cand = cand.as<uint2>(); p.cnt = cnt.as<int>(); p.cap = cap;
+        launch_scan_filter(p, kernMetric(), sample, s);
+    }
+
+    SelectParams selectParams(int nq, int nsplit, int cap, int k, int j) const {
+        SelectParams sp;
+        std::memset(&sp, 0, sizeof sp);
+        sp.cand = cand.as<uint2>(); sp.cnt = cnt.as<int>();
+        sp.nsplit = nsplit; sp.cap = cap; sp.nq = nq; sp.k = k; sp.j = j;
+        sp.metric = kernMetric();
+        sp.out_stride = k;
+        return sp;
+    }
+
+    // Search mb staged queries (qbuf/qnorm) and write rows [0, mb) of the outputs.
+    void searchBatch(int mb, int k, const Plan& pl, int32_t* oIds, float* oVals, hipStream_t s) {
+        const float* Q = qbuf.as<float>();
+        const float* qn = qnorm.as<float>();
+        tauSk.ensure((size_t)mb * 4); tauSi.ensure((size_t)mb * 4);
+        tauGk.ensure((size_t)mb * 4); tauGi.ensure((size_t)mb * 4);
+        tauKk.ensure((size_t)mb * 4); tauKi.ensure((size_t)mb * 4);
+        status.ensure((size_t)mb * 4);
+
+        if (pl.direct) {
+            launch_fill_tau_none(tauSk.as<float>(), tauSi.as<int>(), mb, s);
+            scan(X.as<float>(), xn.as<float>(), nb, pl.rps1, pl.nsplit1, 1, Q, qn, mb,
+                 tauSk.as<float>(), tauSi.as<int>(), pl.cap1, s);
+            SelectParams sp = selectParams(mb, pl.nsplit1, pl.cap1, k, 1);
+            sp.out_ids = oIds; sp.out_vals = oVals;
+            launch_select(sp, s);
+            return;
+        }
+
+        ensureSample(pl, s);
+        // L0: sample, no bound -> speculative (j-th) and guaranteed (k-th) bounds
+        launch_fill_tau_none(tauSk.as<float>(), tauSi.as<int>(), mb, s);
+        scan(sX.as<float>(), sXn.as<float>(), pl.R0, pl.rps0, pl.nsplit0, pl.stride, Q, qn, mb,
+             tauSk.as<float>(), tauSi.as<int>(), pl.cap0, s, /*sample=*/true);
+        {
+            SelectParams sp = selectParams(mb, pl.nsplit0, pl.cap0, k, pl.j);
+            sp.tau_j_key = tauSk.as<float>(); sp.tau_j_id = tauSi.as<int>();
+            sp.tau_k_key = tauGk.as<float>(); sp.tau_k_id = tauGi.as<int>();
+            launch_select(sp, s);
+        }
+        // L1: full database with the speculative bound
+        scan(X.as<float>(), xn.as<float>(), nb, pl.rps1, pl.nsplit1, 1, Q, qn, mb,
+             tauSk.as<float>(), tauSi.as<int>(), pl.cap1, s);
+        {
+            SelectParams sp = selectParams(mb, pl.nsplit1, pl.cap1, k, k);
+            sp.out_ids = oIds; sp.out_vals = oVals;
+            sp.tau_k_key = tauKk.as<float>(); sp.tau_k_id = tauKi.as<int>();
+            sp.status = status.as<int>();
+            launch_select(sp, s);
+        }
+
+        // verification and retries
+        std::vector<int> st((size_t)mb);
+        HIPC(hipMemcpyAsync(st.data(), status.p, (size_t)mb * 4, hipMemcpyDeviceToHost, s));
+        HIPC(hipStreamSynchronize(s));
+        bool spec = pl.j < k;
+        std::vector<int> live((size_t)mb);
+        for (int i = 0; i < mb; ++i) live[(size_t)i] = i;
+        for (int round = 0;; ++round) {
+            std::vector<int> idx, sel;
+            for (int i : live) {
+                const int v = st[(size_t)i];
+                if (v & 1) { idx.push_back(i); sel.push_back(1); }
+                else if (spec && (v & 2)) { idx.push_back(i); sel.push_back(0); }
+            }
+            if (idx.empty()) break;
+            if (round >= 24) throw std::runtime_error("flat search: bound refinement did not converge");
+            const int nf = (int)idx.size();
+            const int nfPad = (int)roundUp(nf, kBN);
+            cIdx.ensure((size_t)nf * 4); cSel.ensure((size_t)nf * 4);
+            cQ.ensure((size_t)nfPad * dpad * 4); cQn.ensure((size_t)nfPad * 4);
+            cTk.ensure((size_t)nf * 4); cTi.ensure((size_t)nf * 4);
+            HIPC(hipMemcpyAsync(cIdx.p, idx.data(), (size_t)nf * 4, hipMemcpyHostToDevice, s));
+            HIPC(hipMemcpyAsync(cSel.p, sel.data(), (size_t)nf * 4, hipMemcpyHostToDevice, s));
+            launch_gather_rows(Q, cIdx.as<int>(), nf, dpad, cQ.as<float>(), nfPad, s);
+            launch_gather_f32(qn, cIdx.as<int>(), nf, cQn.as<float>(), s);
+            launch_gather_tau(tauGk.as<float>(), tauGi.as<int>(), tauKk.as<float>(), tauKi.as<int>(),
+                              cIdx.as<int>(), cSel.as<int>(), nf, cTk.as<float>(), cTi.as<int>(), s);
+            int64_t rps;
+            int nsplit;
+            splitPlan(nb, (nf + kBN - 1) / kBN, rps, nsplit);
+            const int cap = std::max(2 * k, 64);
+            scan(X.as<float>(), xn.as<float>(), nb, rps, nsplit, 1, cQ.as<float>(), cQn.as<float>(), nf,
+                 cTk.as<float>(), cTi.as<int>(), cap, s);
+            SelectParams sp = selectParams(nf, nsplit, cap, k, k);
+            sp.qmap = cIdx.as<int>();
+            sp.out_ids = oIds; sp.out_vals = oVals;
+            sp.tau_k_key = tauKk.as<float>(); sp.tau_k_id = tauKi.as<int>();
+            sp.status = status.as<int>();
+            launch_select(sp, s);
+            HIPC(hipMemcpyAsync(st.data(), status.p, (size_t)mb * 4, hipMemcpyDeviceToHost, s));
+            HIPC(hipStreamSynchronize(s));
+            live = idx;
+            spec = false;
+        }
+    }
+
+    int searchDev(const float* dq, int m, int k, int32_t* ids, float* vals, hipStream_t s) {
+        if (!ready) throw NotReady("no usable HIP device: flat search needs a gfx950 GPU");
+        if (m <= 0) return 0;
+        if (k < 1) k = 1;
+        if (k > kMaxK) {
+            if (!warnedK) {
+                MFLAT_LOG_WARN("k=%d clamped to MFLAT_MAX_K=%d", k, kMaxK);
+                warnedK = true;
+            }
+            k = kMaxK;
+        }
+        setDevice();
+        if (nb == 0) {
+            launch_fill_empty(ids, vals, (int64_t)m * k, emptyValue(), s);
+            HIPC(hipStreamSynchronize(s));
+            return k;
+        }
+        // batch the queries so the candidate workspace stays bounded
+        int64_t mb = m;
+        Plan pl = plan(mb, k);
+        for (int it = 0; it < 4 && (size_t)mb * pl.perQuery * sizeof(uint2) > kCandBudget; ++it) {
+            mb = (int64_t)(kCandBudget / (pl.perQuery * sizeof(uint2)));
+            mb = std::max<int64_t>(kBN, mb / kBN * kBN);
+            pl = plan(mb, k);
+        }
+        for (int64_t b0 = 0; b0 < m; b0 += mb) {
+            const int n = (int)std::min<int64_t>(mb, m - b0);
+            const Plan pb = (n == mb) ? pl : plan(n, k);
+            const int64_t nPad = roundUp(n, kBN);
+            qbuf.ensure((size_t)nPad * dpad * sizeof(float));
+            qnorm.ensure((size_t)nPad * sizeof(float));
+            launch_pack_rows(dq + b0 * dim, n, dim, qbuf.as<float>(), nPad, dpad, s);
+            if (metric == Metric::Cosine) launch_normalize_rows(qbuf.as<float>(), n, dpad, s);
+            if (metric == Metric::L2) launch_row_norms(qbuf.as<float>(), n, dpad, qnorm.as<float>(), s);
+            searchBatch(n, k, pb, ids ? ids + b0 * k : nullptr, vals ? vals + b0 * k : nullptr, s);
+        }
+        HIPC(hipStreamSynchronize(s));
+        return k;
+    }
+};
+
+FlatIndex::FlatIndex(int dim, Metric metric) : d_(new Impl) {
+    d_->dim = dim;
+    d_->dpad = (int)roundUp(dim, kBK);
+    d_->metric = metric;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        (void)hipGetLastError();
+        MFLAT_LOG_INFO("no HIP device - flat search unavailable on this index");
+        return;
+    }
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        MFLAT_LOG_ERROR("device %d is %s; this build targets gfx950 only", dev, prop.gcnArchName);
+        return;
+    }
+    if (hipStreamCreateWithFlags(&d_->stream, hipStreamNonBlocking) != hipSuccess) {
+        MFLAT_LOG_ERROR("hipStreamCreate failed");
+        return;
+    }
+    d_->device = dev;
+    d_->ready = true;
+}
+
+FlatIndex::~FlatIndex() {
+    if (!d_) return;
+    if (d_->device >= 0) (void)hipSetDevice(d_->device);
+    if (d_->stream) (void)hipStreamSynchronize(d_->stream);
+    for (DevBuf* b : {&d_->X, &d_->xn, &d_->sX, &d_->sXn, &d_->sIdx, &d_->stage, &d_->qin, &d_->outIds,
+                      &d_->outVals, &d_->qbuf, &d_->qnorm, &d_->cand, &d_->cnt, &d_->tauSk, &d_->tauSi,
+                      &d_->tauGk, &d_->tauGi, &d_->tauKk, &d_->tauKi, &d_->status, &d_->cQ, &d_->cQn,
+                      &d_->cTk, &d_->cTi, &d_->cIdx, &d_->cSel})
+        b->release();
+    if (d_->stream) (void)hipStreamDestroy(d_->stream);
+}
+
+bool FlatIndex::ready() const { return d_->ready; }
+int FlatIndex::size() const { return (int)d_->nb; }
+int FlatIndex::dim() const { return d_->dim; }
+Metric FlatIndex::metric() const { return d_->metric; }
+
+void FlatIndex::add(const float* rows, int n) {
+    d_->append(rows, n, hipMemcpyHostToDevice, d_->stream);
+}
+
+void FlatIndex::addDevice(const float* rows, int n, hipStream_t s) {
+    d_->append(rows, n, hipMemcpyDeviceToDevice, s ? s : d_->stream);
+}
+
+void FlatIndex::reset() {
+    if (d_->ready) {
+        d_->setDevice();
+        HIPC(hipStreamSynchronize(d_->stream));
+    }
+    d_->X.release();
+    d_->xn.release();
+    d_->capRows = 0;
+    d_->nb = 0;
+    d_->sampleNb = -1;
+}
+
+int FlatIndex::search(const float* q, int m, int k, int32_t* ids, float* dists) {
+    Impl& I = *d_;
+    if (!I.ready) throw NotReady("no usable HIP device: flat search needs a gfx950 GPU");
+    if (m <= 0) return 0;
+    const int kk = std::min(std::max(k, 1), kMaxK);
+    I.setDevice();
+    hipStream_t s = I.stream;
+    I.qin.ensure((size_t)m * I.dim * sizeof(float));
+    I.outIds.ensure((size_t)m * kk * sizeof(int32_t));
+    I.outVals.ensure((size_t)m * kk * sizeof(float));
+    HIPC(hipMemcpyAsync(I.qin.p, q, (size_t)m * I.dim * sizeof(float), hipMemcpyHostToDevice, s));
+    const int used = I.searchDev(I.qin.as<float>(), m, k, I.outIds.as<int32_t>(), I.outVals.as<float>(), s);
+    if (ids) HIPC(hipMemcpyAsync(ids, I.outIds.p, (size_t)m * used * sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    if (dists) HIPC(hipMemcpyAsync(dists, I.outVals.p, (size_t)m * used * sizeof(float), hipMemcpyDeviceToHost, s));
+    HIPC(hipStreamSynchronize(s));
+    return used;
+}
+
+int FlatIndex::searchDevice(const float* q, int m, int k, int32_t* ids, float* dists, hipStream_t s) {
+    return d_->searchDev(q, m, k, ids, dists, s ? s : d_->stream);
+}
+
+}  // namespace mflat_amd

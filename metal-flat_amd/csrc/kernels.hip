@@ -1,0 +1,640 @@
+// SPDX-License-Identifier: Apache-2.0
+// kernels.hip -- hand-written gfx950 kernels for exact flat search.
+//
+//   scan_filter  fused distance + threshold filter. An fp32 MFMA GEMM tile
+//                (v_mfma_f32_32x32x2_f32) of kBM database rows x kBN queries,
+//                whose epilogue turns dots into ranking keys and keeps only
+//                candidates at or below the query's lexicographic (key, id)
+//                bound. The nq x nb distance matrix never reaches HBM: only the
+//                few surviving candidates are written. Replaces the reference's
+//                MPS GEMM + per-tile merge pair (src/GemmDistance.mm:15-60,
+//                src/FlatIndex.mm:63-107,375-402).
+//   select       per-query exact top-k of the surviving candidates: radix select
+//                on the 64-bit (key, id) composite, then a bitonic sort of the k
+//                winners in LDS. It is the cross-tile merge.
+//   row norms / normalisation / packing helpers.
+#include "kernels.hpp"
+
+#include <cmath>
+#include <cstdio>
+#include <stdexcept>
+#include <string>
+
+namespace mflat_amd {
+
+typedef float fx4 __attribute__((ext_vector_type(4)));
+typedef float fx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kLds = kBK + 4;   // LDS row stride in floats: 16-byte reads of 16
+                                // consecutive rows land in distinct banks
+
+static void check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        throw std::runtime_error(std::string(what) + " launch failed: " + hipGetErrorString(e));
+}
+
+// ---------------------------------------------------------------------------
+// helpers
+// ---------------------------------------------------------------------------
+
+// dst[r][c] = src[r*dim + c] for r < n, c < dim; zero elsewhere (r < n_pad, c < dpad)
+__global__ void pack_rows_kernel(const float* __restrict__ src, int64_t n, int dim,
+                                 float* __restrict__ dst, int64_t n_pad, int dpad) {
+    const int64_t total = n_pad * dpad;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / dpad;
+        const int c = (int)(i - r * dpad);
+        dst[i] = (r < n && c < dim) ? src[r * dim + c] : 0.0f;
+    }
+}
+
+// ||row||^2 with a sequential double sum, cast to float: the accumulation the
+// reference's rowSqNorms uses (src/Distance.h:40-47), so the norms match it
+// bit for bit. One thread per row.
+__global__ void row_norms_kernel(const float* __restrict__ v, int64_t n, int dpad,
+                                 float* __restrict__ out) {
+    const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (r >= n) return;
+    const float* row = v + r * dpad;
+    double s = 0.0;
+    for (int c = 0; c < dpad; c += 4) {
+        const fx4 x = *(const fx4*)(row + c);
+        s += (double)x.x * x.x;
+        s += (double)x.y * x.y;
+        s += (double)x.z * x.z;
+        s += (double)x.w * x.w;
+    }
+    out[r] = (float)s;
+}
+
+// In-place L2 normalisation (reference src/Distance.h:50-60): double sum,
+// inv = float(1 / sqrt(s)), x *= inv, zero rows unchanged.
+__global__ void normalize_rows_kernel(float* __restrict__ v, int64_t n, int dpad) {
+    const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (r >= n) return;
+    float* row = v + r * dpad;
+    double s = 0.0;
+    for (int c = 0; c < dpad; ++c) s += (double)row[c] * row[c];
+    if (s > 0.0) {
+        const float inv = (float)(1.0 / sqrt(s));
+        for (int c = 0; c < dpad; ++c) row[c] *= inv;
+    }
+}
+
+__global__ void gather_rows_kernel(const float* __restrict__ src, const int* __restrict__ idx,
+                                   int n, int dpad, float* __restrict__ dst, int64_t n_pad) {
+    const int64_t total = n_pad * dpad;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / dpad;
+        const int c = (int)(i - r * dpad);
+        dst[i] = r < n ? src[(int64_t)idx[r] * dpad + c] : 0.0f;
+    }
+}
+
+__global__ void gather_f32_kernel(const float* __restrict__ src, const int* __restrict__ idx,
+                                  int n, float* __restrict__ dst) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = src[idx[i]];
+}
+
+// tau_out[i] = sel[i] ? b[idx[i]] : a[idx[i]]
+__global__ void gather_tau_kernel(const float* __restrict__ ka, const int* __restrict__ ia,
+                                  const float* __restrict__ kb, const int* __restrict__ ib,
+                                  const int* __restrict__ idx, const int* __restrict__ sel, int n,
+                                  float* __restrict__ ko, int* __restrict__ io) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int q = idx[i];
+    if (sel[i]) { ko[i] = kb[q]; io[i] = ib[q]; }
+    else        { ko[i] = ka[q]; io[i] = ia[q]; }
+}
+
+// "No bound": (+inf, -1) admits every finite key and rejects +inf and NaN,
+// matching the reference, which never inserts a score of -inf or NaN.
+__global__ void fill_tau_none_kernel(float* __restrict__ key, int* __restrict__ id, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) { key[i] = INFINITY; id[i] = -1; }
+}
+
+__global__ void fill_empty_kernel(int32_t* __restrict__ ids, float* __restrict__ vals,
+                                  int64_t count, float empty) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < count;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        if (ids) ids[i] = -1;
+        if (vals) vals[i] = empty;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// scan_filter: fp32 MFMA distance tile + threshold filter
+// ---------------------------------------------------------------------------
+//
+// Workgroup: 256 threads = 4 waves in a 2 x 2 arrangement; each wave owns a
+// 64-row x 64-query quarter of the 128 x 128 tile as 2 x 2 blocks of
+// v_mfma_f32_32x32x2_f32. The operand roles: A = database rows (M), B = queries
+// (N), so accumulator register r of lane l holds
+//     row   = 8*(r/4) + 4*(l/32) + (r%4),   query = l%32
+// i.e. every lane sees 16 rows of ONE query per block, which keeps the
+// per-query threshold in a register during the epilogue.
+//
+// The K dimension is consumed in chunks of kBK = 32 staged through LDS, double
+// buffered; one barrier per chunk. Within a chunk the two lane halves read
+// float4s of 4 consecutive columns, and MFMA step j of group g pairs columns
+// (8g + j, 8g + 4 + j): the same permutation on both operands, so the dot is
+// unchanged while every LDS read is a single ds_read_b128.
+//
+// A workgroup owns one query block and one split (a contiguous range of
+// database rows) and walks the split's tiles in ascending row order. Linear
+// workgroup ids are remapped so that each XCD (ids are dealt round-robin over
+// the 8 XCDs) receives a contiguous run of (split, query block) pairs: the
+// workgroups resident on one XCD then stream the same database rows through
+// that XCD's L2.
+// SAMPLE only names the instantiation (the sample pass gets its own symbol so
+// profiles separate it from the full-database pass); the code is the same.
+template <int METRIC, int SAMPLE>
+__global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
+    __shared__ __attribute__((aligned(16))) float sX[2 * kBM * kLds];
+    __shared__ __attribute__((aligned(16))) float sQ[2 * kBN * kLds];
+    __shared__ int sCnt[kBN];
+
+    const int nwg = gridDim.x;
+    const int bid = blockIdx.x;
+    const int full = (nwg / 8) * 8;
+    const int v = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
+    const int split = v / p.nqb;
+    const int qb = v - split * p.nqb;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave & 1;
+    const int wn = wave >> 1;
+    const int r32 = lane & 31;
+    const int h = lane >> 5;
+
+    if (tid < kBN) sCnt[tid] = 0;
+
+    // per-lane query state for the two query blocks this lane sees
+    float tk[2], qn[2];
+    int ti[2];
+    bool qv[2];
+#pragma unroll
+    for (int bn = 0; bn < 2; ++bn) {
+        const int q = qb * kBN + wn * 64 + bn * 32 + r32;
+        qv[bn] = q < p.nq;
+        tk[bn] = qv[bn] ? p.tau_key[q] : 0.0f;
+        ti[bn] = qv[bn] ? p.tau_id[q] : -1;
+        qn[bn] = (METRIC == 0 && qv[bn]) ? p.qnorm[q] : 0.0f;
+    }
+
+    const int64_t rows_pad = (p.nrows + kBM - 1) / kBM * kBM;
+    const int64_t rowBeg = (int64_t)split * p.rows_per_split;
+    int64_t rowEnd = rowBeg + p.rows_per_split;
+    if (rowEnd > rows_pad) rowEnd = rows_pad;
+    const int ntiles = rowEnd > rowBeg ? (int)((rowEnd - rowBeg) / kBM) : 0;
+    const int nk = p.dpad / kBK;
+    const int total = ntiles * nk;
+
+    // global -> register staging: 4 float4 per thread per operand
+    const int ldRow = tid >> 3;         // + 32*i
+    const int ldCol = (tid & 7) * 4;
+    const float* Xb = p.X + rowBeg * p.dpad;
+    const float* Qb = p.Q + (int64_t)qb * kBN * p.dpad;
+    fx4 rx[4], rq[4];
+
+    auto gload = [&](int it) {
+        const int tile = it / nk;
+        const int kc = it - tile * nk;
+        const float* xs = Xb + ((int64_t)tile * kBM) * p.dpad + kc * kBK + ldCol;
+        const float* qs = Qb + kc * kBK + ldCol;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = ldRow + 32 * i;
+            rx[i] = *(const fx4*)(xs + (int64_t)row * p.dpad);
+            rq[i] = *(const fx4*)(qs + (int64_t)row * p.dpad);
+        }
+    };
+    auto lstore = [&](int buf) {
+        float* dx = sX + buf * (kBM * kLds);
+        float* dq = sQ + buf * (kBN * kLds);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = ldRow + 32 * i;
+            *(fx4*)(dx + row * kLds + ldCol) = rx[i];
+            *(fx4*)(dq + row * kLds + ldCol) = rq[i];
+        }
+    };
+
+    fx16 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+
+    if (total > 0) {
+        gload(0);
+        lstore(0);
+    }
+    __syncthreads();
+
+    const int aOff = (wm * 64 + r32) * kLds + h * 4;
+    const int bOff = (wn * 64 + r32) * kLds + h * 4;
+
+    for (int it = 0; it < total; ++it) {
+        const int buf = it & 1;
+        const int tile = it / nk;
+        const int kc = it - tile * nk;
+        if (it + 1 < total) gload(it + 1);
+
+        const float* sx = sX + buf * (kBM * kLds);
+        const float* sq = sQ + buf * (kBN * kLds);
+#pragma unroll
+        for (int g = 0; g < kBK / 8; ++g) {
+            fx4 a0 = *(const fx4*)(sx + aOff + g * 8);
+            fx4 a1 = *(const fx4*)(sx + aOff + 32 * kLds + g * 8);
+            fx4 b0 = *(const fx4*)(sq + bOff + g * 8);
+            fx4 b1 = *(const fx4*)(sq + bOff + 32 * kLds + g * 8);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], b0[j], acc[0][0], 0, 0, 0);
+                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], b1[j], acc[0][1], 0, 0, 0);
+                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[j], b0[j], acc[1][0], 0, 0, 0);
+                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[j], b1[j], acc[1][1], 0, 0, 0);
+            }
+        }
+
+        if (kc == nk - 1) {
+            // epilogue: keys, threshold test, append survivors
+            const int64_t tileRow0 = rowBeg + (int64_t)tile * kBM;
+#pragma unroll
+            for (int bm = 0; bm < 2; ++bm) {
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const int rl = wm * 64 + bm * 32 + g4 * 8 + h * 4;
+                    const int64_t r0 = tileRow0 + rl;
+                    fx4 xn4 = {0.0f, 0.0f, 0.0f, 0.0f};
+                    if (METRIC == 0) xn4 = *(const fx4*)(p.xnorm + r0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int64_t row = r0 + i;
+                        const bool rv = row < p.nrows;
+                        const int id = (int)(row * p.id_stride);
+#pragma unroll
+                        for (int bn = 0; bn < 2; ++bn) {
+                            const float dot = acc[bm][bn][g4 * 4 + i];
+                            float key;
+                            if (METRIC == 0) {
+                                const float t = fmaf(-2.0f, dot, qn[bn] + xn4[i]);
+                                key = (t < 0.0f ? 0.0f : t) + 0.0f;
+                            } else {
+                                key = -dot + 0.0f;
+                            }
+                            const bool pass = rv && qv[bn] &&
+                                              (key < tk[bn] || (key == tk[bn] && id <= ti[bn]));
+                            if (pass) {
+                                const int ql = wn * 64 + bn * 32 + r32;
+                                const int slot = atomicAdd(&sCnt[ql], 1);
+                                if (slot < p.cap) {
+                                    const int64_t q = (int64_t)qb * kBN + ql;
+                                    p.cand[(q * p.nsplit + split) * p.cap + slot] =
+                                        make_uint2(__float_as_uint(key), (unsigned)id);
+                                }
+                            }
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+        }
+
+        if (it + 1 < total) lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    __syncthreads();
+    if (tid < kBN) {
+        const int q = qb * kBN + tid;
+        if (q < p.nq) p.cnt[(int64_t)q * p.nsplit + split] = sCnt[tid];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// select: exact per-query top-k of the candidate regions
+// ---------------------------------------------------------------------------
+
+// Order-preserving map of a float key to uint32 (ascending float order ==
+// ascending unsigned order); NaN never reaches here (the filter rejects it).
+__device__ __forceinline__ uint32_t key_to_ord(uint32_t bits) {
+    return (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+}
+__device__ __forceinline__ float ord_to_key(uint32_t o) {
+    const uint32_t bits = (o & 0x80000000u) ? (o ^ 0x80000000u) : ~o;
+    return __uint_as_float(bits);
+}
+__device__ __forceinline__ uint64_t composite(uint2 c) {
+    return ((uint64_t)key_to_ord(c.x) << 32) | (uint64_t)c.y;
+}
+
+// One workgroup (256 threads) per query. The (key, id) composites are distinct
+// (an id appears at most once per query), so the k-th smallest composite T is
+// unique and the winners are exactly the composites <= T.
+__global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
+    __shared__ uint64_t sBuf[kSelLds];
+    __shared__ uint64_t sTop[kTopMax];
+    __shared__ unsigned sHist[256];
+    __shared__ unsigned sSel[3];
+    __shared__ uint64_t sT;
+    __shared__ int sN;
+
+    const int q = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int64_t qbase = (int64_t)q * p.nsplit;
+
+    int c = 0;
+    bool ovf = false;
+    for (int s = 0; s < p.nsplit; ++s) {
+        const int n = p.cnt[qbase + s];
+        ovf |= n > p.cap;
+        c += n < p.cap ? n : p.cap;
+    }
+    const bool inLds = c <= kSelLds;
+    if (inLds) {
+        int base = 0;
+        for (int s = 0; s < p.nsplit; ++s) {
+            int n = p.cnt[qbase + s];
+            n = n < p.cap ? n : p.cap;
+            const uint2* src = p.cand + (qbase + s) * p.cap;
+            for (int e = tid; e < n; e += 256) sBuf[base + e] = composite(src[e]);
+            base += n;
+        }
+    }
+    __syncthreads();
+
+    auto for_each = [&](auto&& f) {
+        if (inLds) {
+            for (int e = tid; e < c; e += 256) f(sBuf[e]);
+        } else {
+            for (int s = 0; s < p.nsplit; ++s) {
+                int n = p.cnt[qbase + s];
+                n = n < p.cap ? n : p.cap;
+                const uint2* src = p.cand + (qbase + s) * p.cap;
+                for (int e = tid; e < n; e += 256) f(composite(src[e]));
+            }
+        }
+    };
+
+    const int k = p.k;
+    uint64_t T = ~0ull;   // take everything when c <= k
+    if (c > k) {
+        uint64_t prefix = 0, mask = 0;
+        unsigned kr = (unsigned)k;
+        bool found = false;
+        for (int shift = 56; shift >= 0; shift -= 8) {
+            sHist[tid] = 0;
+            __syncthreads();
+            for_each([&](uint64_t x) {
+                if ((x & mask) == prefix) atomicAdd(&sHist[(unsigned)(x >> shift) & 255u], 1u);
+            });
+            __syncthreads();
+            if (tid < 64) {
+                const unsigned h0 = sHist[4 * tid], h1 = sHist[4 * tid + 1];
+                const unsigned h2 = sHist[4 * tid + 2], h3 = sHist[4 * tid + 3];
+                const unsigned s4 = h0 + h1 + h2 + h3;
+                unsigned incl = s4;
+                for (int off = 1; off < 64; off <<= 1) {
+                    const unsigned t = __shfl_up(incl, off, 64);
+                    if (tid >= off) incl += t;
+                }
+                const unsigned excl = incl - s4;
+                if (excl < kr && kr <= incl) {
+                    unsigned cum = excl;
+                    unsigned b = 4 * tid, hb = h0;
+                    if (cum + h0 < kr) {
+                        cum += h0; b += 1; hb = h1;
+                        if (cum + h1 < kr) {
+                            cum += h1; b += 1; hb = h2;
+                            if (cum + h2 < kr) { cum += h2; b += 1; hb = h3; }
+                        }
+                    }
+                    sSel[0] = b;
+                    sSel[1] = kr - cum;
+                    sSel[2] = hb;
+                }
+            }
+            __syncthreads();
+            const unsigned b = sSel[0];
+            kr = sSel[1];
+            const unsigned hb = sSel[2];
+            prefix |= (uint64_t)b << shift;
+            mask |= (uint64_t)0xFFu << shift;
+            __syncthreads();
+            if (hb == 1u) {
+                for_each([&](uint64_t x) {
+                    if ((x & mask) == prefix) sT = x;
+                });
+                __syncthreads();
+                T = sT;
+                found = true;
+                break;
+            }
+        }
+        if (!found) T = prefix;
+    }
+
+    if (tid == 0) sN = 0;
+    __syncthreads();
+    for_each([&](uint64_t x) {
+        if (x <= T) {
+            const int pos = atomicAdd(&sN, 1);
+            if (pos < kTopMax) sTop[pos] = x;
+        }
+    });
+    __syncthreads();
+    const int nsel = sN < kTopMax ? sN : kTopMax;
+    int P = 1;
+    while (P < nsel) P <<= 1;
+    for (int i = nsel + tid; i < P; i += 256) sTop[i] = ~0ull;
+    __syncthreads();
+
+    // bitonic sort, ascending
+    for (int size = 2; size <= P; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = tid; i < (P >> 1); i += 256) {
+                const int lo = 2 * i - (i & (stride - 1));
+                const int hi = lo + stride;
+                const bool asc = (lo & size) == 0;
+                const uint64_t a = sTop[lo], b = sTop[hi];
+                if ((a > b) == asc) { sTop[lo] = b; sTop[hi] = a; }
+            }
+            __syncthreads();
+        }
+    }
+
+    const int orow = p.qmap ? p.qmap[q] : q;
+    if (p.out_ids || p.out_vals) {
+        for (int i = tid; i < k; i += 256) {
+            int32_t id = -1;
+            float val = p.metric == 0 ? INFINITY : -INFINITY;
+            if (i < nsel) {
+                const uint64_t x = sTop[i];
+                id = (int32_t)(uint32_t)(x & 0xFFFFFFFFu);
+                const float key = ord_to_key((uint32_t)(x >> 32));
+                val = p.metric == 0 ? key : -key;
+            }
+            if (p.out_ids) p.out_ids[(int64_t)orow * p.out_stride + i] = id;
+            if (p.out_vals) p.out_vals[(int64_t)orow * p.out_stride + i] = val;
+        }
+    }
+    if (tid == 0) {
+        if (p.tau_j_key) {
+            if (nsel >= p.j) {
+                const uint64_t x = sTop[p.j - 1];
+                p.tau_j_key[orow] = ord_to_key((uint32_t)(x >> 32));
+                p.tau_j_id[orow] = (int)(uint32_t)(x & 0xFFFFFFFFu);
+            } else {
+                p.tau_j_key[orow] = INFINITY;
+                p.tau_j_id[orow] = -1;
+            }
+        }
+        if (p.tau_k_key) {
+            if (nsel >= k) {
+                const uint64_t x = sTop[k - 1];
+                p.tau_k_key[orow] = ord_to_key((uint32_t)(x >> 32));
+                p.tau_k_id[orow] = (int)(uint32_t)(x & 0xFFFFFFFFu);
+            } else {
+                p.tau_k_key[orow] = INFINITY;
+                p.tau_k_id[orow] = -1;
+            }
+        }
+        if (p.status) p.status[orow] = (ovf ? 1 : 0) | (c < k ? 2 : 0);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+
+static int grid_for(int64_t work, int block) {
+    int64_t g = (work + block - 1) / block;
+    if (g > 65536) g = 65536;
+    if (g < 1) g = 1;
+    return (int)g;
+}
+
+void launch_pack_rows(const float* src, int64_t n, int dim, float* dst, int64_t n_pad, int dpad,
+                      hipStream_t s) {
+    if (n_pad <= 0) return;
+    void* tok;
+    prof_begin(kFamPrep, s, &tok);
+    pack_rows_kernel<<<grid_for(n_pad * dpad, 256), 256, 0, s>>>(src, n, dim, dst, n_pad, dpad);
+    prof_end(tok, s);
+    check_launch("pack_rows");
+}
+
+void launch_row_norms(const float* v, int64_t n, int dpad, float* out, hipStream_t s) {
+    if (n <= 0) return;
+    void* tok;
+    prof_begin(kFamNorms, s, &tok);
+    row_norms_kernel<<<(int)((n + 255) / 256), 256, 0, s>>>(v, n, dpad, out);
+    prof_end(tok, s);
+    check_launch("row_norms");
+}
+
+void launch_normalize_rows(float* v, int64_t n, int dpad, hipStream_t s) {
+    if (n <= 0) return;
+    void* tok;
+    prof_begin(kFamNorms, s, &tok);
+    normalize_rows_kernel<<<(int)((n + 255) / 256), 256, 0, s>>>(v, n, dpad);
+    prof_end(tok, s);
+    check_launch("normalize_rows");
+}
+
+void launch_gather_rows(const float* src, const int* idx, int n, int dpad, float* dst,
+                        int64_t n_pad, hipStream_t s) {
+    if (n_pad <= 0) return;
+    void* tok;
+    prof_begin(kFamPrep, s, &tok);
+    gather_rows_kernel<<<grid_for(n_pad * dpad, 256), 256, 0, s>>>(src, idx, n, dpad, dst, n_pad);
+    prof_end(tok, s);
+    check_launch("gather_rows");
+}
+
+void launch_gather_f32(const float* src, const int* idx, int n, float* dst, hipStream_t s) {
+    if (n <= 0) return;
+    void* tok;
+    prof_begin(kFamPrep, s, &tok);
+    gather_f32_kernel<<<(n + 255) / 256, 256, 0, s>>>(src, idx, n, dst);
+    prof_end(tok, s);
+    check_launch("gather_f32");
+}
+
+void launch_gather_tau(const float* ka, const int* ia, const float* kb, const int* ib,
+                       const int* idx, const int* sel, int n, float* ko, int* io, hipStream_t s) {
+    if (n <= 0) return;
+    void* tok;
+    prof_begin(kFamPrep, s, &tok);
+    gather_tau_kernel<<<(n + 255) / 256, 256, 0, s>>>(ka, ia, kb, ib, idx, sel, n, ko, io);
+    prof_end(tok, s);
+    check_launch("gather_tau");
+}
+
+void launch_fill_tau_none(float* key, int* id, int n, hipStream_t s) {
+    if (n <= 0) return;
+    void* tok;
+    prof_begin(kFamPrep, s, &tok);
+    fill_tau_none_kernel<<<(n + 255) / 256, 256, 0, s>>>(key, id, n);
+    prof_end(tok, s);
+    check_launch("fill_tau_none");
+}
+
+void launch_fill_empty(int32_t* ids, float* vals, int64_t count, float empty, hipStream_t s) {
+    if (count <= 0) return;
+    void* tok;
+    prof_begin(kFamPrep, s, &tok);
+    fill_empty_kernel<<<grid_for(count, 256), 256, 0, s>>>(ids, vals, count, empty);
+    prof_end(tok, s);
+    check_launch("fill_empty");
+}
+
+void launch_scan_filter(const ScanParams& p, int metric, bool sample, hipStream_t s) {
+    const int64_t grid = (int64_t)p.nqb * p.nsplit;
+    if (grid <= 0) return;
+    if (grid > 0x7FFFFFFF) throw std::runtime_error("scan_filter grid too large");
+    if (p.dpad % kBK != 0 || p.rows_per_split % kBM != 0 || p.cap < 1)
+        throw std::runtime_error("scan_filter: bad tiling parameters");
+    void* tok;
+    prof_begin(sample ? kFamScanSample : kFamScan, s, &tok);
+    if (metric == 0 && !sample)
+        scan_filter_kernel<0, 0><<<(int)grid, 256, 0, s>>>(p);
+    else if (metric == 0)
+        scan_filter_kernel<0, 1><<<(int)grid, 256, 0, s>>>(p);
+    else if (!sample)
+        scan_filter_kernel<1, 0><<<(int)grid, 256, 0, s>>>(p);
+    else
+        scan_filter_kernel<1, 1><<<(int)grid, 256, 0, s>>>(p);
+    prof_end(tok, s);
+    check_launch("scan_filter");
+}
+
+void launch_select(const SelectParams& p, hipStream_t s) {
+    if (p.nq <= 0) return;
+    if (p.k < 1 || p.k > kTopMax || p.j < 1 || p.j > p.k)
+        throw std::runtime_error("select: bad k/j");
+    void* tok;
+    prof_begin(kFamSelect, s, &tok);
+    select_kernel<<<p.nq, 256, 0, s>>>(p);
+    prof_end(tok, s);
+    check_launch("select");
+}
+
+}  // namespace mflat_amd

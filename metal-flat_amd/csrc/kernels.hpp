@@ -1,0 +1,96 @@
+// SPDX-License-Identifier: Apache-2.0
+// kernels.hpp -- device kernels of the flat-search hot path and their launchers.
+//
+// Data layout in HBM (all fp32, row-major):
+//   database  X[rows_pad][dpad]   rows_pad = roundup(nb, kBM), dpad = roundup(dim, kBK);
+//                                 pad rows and pad columns are zero
+//   row norms xn[rows_pad]        ||x||^2, double-accumulated (reference
+//                                 src/Distance.h:40-47), pad entries zero
+//   queries   Q[nqb*kBN][dpad]    same padding rules, qn[] likewise
+//   candidates cand[nq][nsplit][cap] of (key bits, id), cnt[nq][nsplit]
+//
+// Ranking key (smaller = nearer), the value the reference's merge kernel ranks
+// on, negated (reference src/FlatIndex.mm:89-93):
+//   L2:  key = max(0, (||q||^2 + ||x||^2) - 2 q.x)     reported value = key
+//   IP:  key = -(q.x)                                 reported value = -key
+// Results are ordered by (key, id) ascending: ties keep the lowest id, exactly
+// the order the reference's strict '>' insertion produces
+// (src/FlatIndex.mm:272-281).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace mflat_amd {
+
+constexpr int kBM = 128;   // database rows per scan tile
+constexpr int kBN = 128;   // queries per scan tile
+constexpr int kBK = 32;    // dimension chunk staged through LDS
+constexpr int kSelLds = 4096;   // candidates a select block holds in LDS
+constexpr int kTopMax = 1024;   // largest k (== MFLAT_MAX_K)
+
+enum KernelFamily {
+    kFamScan = 0, kFamScanSample = 1, kFamSelect = 2, kFamArgmin = 3, kFamNorms = 4, kFamPrep = 5,
+    kFamCount = 6
+};
+
+struct ScanParams {
+    const float* X;          // database tile source (see layout above)
+    const float* xnorm;      // per-row ||x||^2 (L2 only)
+    int64_t nrows;           // valid rows; rows >= nrows are padding
+    int64_t rows_per_split;  // multiple of kBM
+    int nsplit;              // database splits (grid = nqb * nsplit)
+    int id_stride;           // reported id = row * id_stride (sample passes)
+    const float* Q;          // queries
+    const float* qnorm;      // per-query ||q||^2 (L2 only)
+    int nq;                  // valid queries
+    int nqb;                 // query blocks of kBN
+    int dpad;                // padded dimension, multiple of kBK
+    const float* tau_key;    // per-query threshold key
+    const int* tau_id;       // per-query threshold id (lexicographic bound)
+    uint2* cand;             // candidate regions
+    int* cnt;                // per (query, split) candidate counts (may exceed cap)
+    int cap;                 // entries per (query, split) region
+};
+
+struct SelectParams {
+    const uint2* cand;
+    const int* cnt;
+    int nsplit;
+    int cap;
+    int nq;
+    int k;                   // rank to select (1..kTopMax)
+    int j;                   // secondary rank for tau_j (1..k)
+    int metric;              // 0: value = key, otherwise value = -key
+    const int* qmap;         // nullable: output row of query i
+    int32_t* out_ids;        // nullable
+    float* out_vals;         // nullable
+    int out_stride;
+    float* tau_j_key;        // nullable: j-th smallest (key, id), or "no bound"
+    int* tau_j_id;
+    float* tau_k_key;        // nullable: k-th smallest (key, id), or "no bound"
+    int* tau_k_id;
+    int* status;             // nullable: bit0 = a region overflowed, bit1 = fewer than k stored
+};
+
+// Launchers (kernels.hip). All are asynchronous on `s` and bracket the launch
+// with the process-wide kernel timer when it is enabled.
+void launch_pack_rows(const float* src, int64_t n, int dim, float* dst, int64_t n_pad, int dpad,
+                      hipStream_t s);
+void launch_row_norms(const float* v, int64_t n, int dpad, float* out, hipStream_t s);
+void launch_normalize_rows(float* v, int64_t n, int dpad, hipStream_t s);
+void launch_gather_rows(const float* src, const int* idx, int n, int dpad, float* dst,
+                        int64_t n_pad, hipStream_t s);
+void launch_gather_f32(const float* src, const int* idx, int n, float* dst, hipStream_t s);
+void launch_gather_tau(const float* ka, const int* ia, const float* kb, const int* ib,
+                       const int* idx, const int* sel, int n, float* ko, int* io, hipStream_t s);
+void launch_fill_tau_none(float* key, int* id, int n, hipStream_t s);
+void launch_fill_empty(int32_t* ids, float* vals, int64_t count, float empty, hipStream_t s);
+void launch_scan_filter(const ScanParams& p, int metric, bool sample, hipStream_t s);
+void launch_select(const SelectParams& p, hipStream_t s);
+
+// Kernel timer (profile.cpp).
+void prof_begin(int fam, hipStream_t s, void** token);
+void prof_end(void* token, hipStream_t s);
+
+}  // namespace mflat_amd

@@ -1,0 +1,198 @@
+// SPDX-License-Identifier: Apache-2.0
+// mflat_abi.cpp -- the C ABI (include/mflat.h) over the engine.
+//
+// Same shell as the reference's c/mflat.cpp:32-129: an opaque handle wrapping
+// the engine plus a std::mutex that serialises add / reset / search per handle;
+// every entry point is a try/catch that maps exceptions to status codes;
+// results are copied into caller-owned buffers with row stride k_used.
+#include <atomic>
+#include <cstring>
+#include <mutex>
+#include <new>
+
+#include "../../include/mflat.h"
+#include "flat_index.hpp"
+#include "log.hpp"
+
+using mflat_amd::FlatIndex;
+using mflat_amd::Metric;
+
+namespace mflat_amd {
+void prof_enable(int on);
+void prof_reset();
+int prof_read(const char* name, double* ms, long long* n);
+}  // namespace mflat_amd
+
+namespace {
+
+// reference c/mflat.cpp:32-38: unknown values map to L2
+Metric conv(mflat_metric_t m) {
+    switch (m) {
+        case MFLAT_METRIC_INNER_PRODUCT: return Metric::InnerProduct;
+        case MFLAT_METRIC_COSINE: return Metric::Cosine;
+        default: return Metric::L2;
+    }
+}
+
+// reference c/mflat.cpp:52-59: the C handler type differs from the C++ one, so
+// calls go through a trampoline (never a function-pointer cast).
+std::atomic<mflat_log_handler_t> gCHandler{nullptr};
+std::atomic<void*> gCUser{nullptr};
+void cLogTrampoline(mflat_amd::LogLevel lvl, const char* msg, void*) {
+    if (auto h = gCHandler.load(std::memory_order_acquire))
+        h(static_cast<mflat_log_level_t>(lvl), msg, gCUser.load(std::memory_order_acquire));
+}
+
+template <class F>
+mflat_status_t guarded(F&& f) {
+    try {
+        return f();
+    } catch (const std::bad_alloc&) {
+        return MFLAT_ERR_ALLOC;
+    } catch (const mflat_amd::NotReady& e) {
+        MFLAT_LOG_ERROR("%s", e.what());
+        return MFLAT_ERR_NOT_READY;
+    } catch (const mflat_amd::BadArg& e) {
+        MFLAT_LOG_ERROR("%s", e.what());
+        return MFLAT_ERR_BAD_ARG;
+    } catch (const std::exception& e) {
+        MFLAT_LOG_ERROR("%s", e.what());
+        return MFLAT_ERR_INTERNAL;
+    } catch (...) {
+        return MFLAT_ERR_INTERNAL;
+    }
+}
+
+}  // namespace
+
+struct mflat_flat_index {
+    FlatIndex idx;
+    std::mutex mu;
+    mflat_flat_index(int d, Metric m) : idx(d, m) {}
+};
+
+extern "C" {
+
+MFLAT_API const char* mflat_version(void) { return "0.1.0"; }
+MFLAT_API int mflat_max_k(void) { return MFLAT_MAX_K; }
+
+MFLAT_API const char* mflat_status_str(mflat_status_t s) {
+    switch (s) {
+        case MFLAT_OK: return "ok";
+        case MFLAT_ERR_NULL_ARG: return "null argument";
+        case MFLAT_ERR_BAD_ARG: return "bad argument";
+        case MFLAT_ERR_ALLOC: return "allocation failed";
+        case MFLAT_ERR_NOT_READY: return "index not ready";
+        case MFLAT_ERR_INTERNAL: return "internal error";
+    }
+    return "unknown";
+}
+
+MFLAT_API void mflat_set_log_handler(mflat_log_handler_t h, void* user) {
+    gCUser.store(user, std::memory_order_release);
+    gCHandler.store(h, std::memory_order_release);
+    mflat_amd::setLogHandler(h ? &cLogTrampoline : nullptr, nullptr);
+}
+MFLAT_API void mflat_set_log_level(mflat_log_level_t l) {
+    int v = static_cast<int>(l);
+    if (v < 0) v = 0;
+    if (v > 3) v = 3;
+    mflat_amd::setLogLevel(static_cast<mflat_amd::LogLevel>(v));
+}
+MFLAT_API mflat_log_level_t mflat_log_level(void) {
+    return static_cast<mflat_log_level_t>(mflat_amd::logLevel());
+}
+
+MFLAT_API mflat_flat_index_t* mflat_flat_create(int dim, mflat_metric_t metric, mflat_status_t* st) {
+    if (dim <= 0) {
+        if (st) *st = MFLAT_ERR_BAD_ARG;
+        return nullptr;
+    }
+    try {
+        auto* h = new mflat_flat_index(dim, conv(metric));
+        if (st) *st = MFLAT_OK;
+        return h;
+    } catch (const std::bad_alloc&) {
+        if (st) *st = MFLAT_ERR_ALLOC;
+        return nullptr;
+    } catch (...) {
+        if (st) *st = MFLAT_ERR_INTERNAL;
+        return nullptr;
+    }
+}
+
+MFLAT_API void mflat_flat_free(mflat_flat_index_t* h) { delete h; }
+MFLAT_API int mflat_flat_ready(const mflat_flat_index_t* h) { return (h && h->idx.ready()) ? 1 : 0; }
+MFLAT_API int mflat_flat_size(const mflat_flat_index_t* h) { return h ? h->idx.size() : 0; }
+MFLAT_API int mflat_flat_dim(const mflat_flat_index_t* h) { return h ? h->idx.dim() : 0; }
+
+MFLAT_API mflat_status_t mflat_flat_add(mflat_flat_index_t* h, const float* v, int n) {
+    if (!h || !v) return MFLAT_ERR_NULL_ARG;
+    if (n < 0) return MFLAT_ERR_BAD_ARG;
+    return guarded([&] {
+        std::lock_guard<std::mutex> lk(h->mu);
+        h->idx.add(v, n);
+        return MFLAT_OK;
+    });
+}
+
+MFLAT_API mflat_status_t mflat_flat_reset(mflat_flat_index_t* h) {
+    if (!h) return MFLAT_ERR_NULL_ARG;
+    return guarded([&] {
+        std::lock_guard<std::mutex> lk(h->mu);
+        h->idx.reset();
+        return MFLAT_OK;
+    });
+}
+
+MFLAT_API mflat_status_t mflat_flat_search(mflat_flat_index_t* h, const float* q, int m, int k,
+                                           int32_t* oi, float* od, int* ok) {
+    if (!h || !q) return MFLAT_ERR_NULL_ARG;
+    if (m < 0 || k < 1) return MFLAT_ERR_BAD_ARG;
+    if (m == 0) {   // reference c/mflat.cpp:44: empty result, k_used = 0
+        if (ok) *ok = 0;
+        return MFLAT_OK;
+    }
+    return guarded([&] {
+        std::lock_guard<std::mutex> lk(h->mu);
+        const int used = h->idx.search(q, m, k, oi, od);
+        if (ok) *ok = used;
+        return MFLAT_OK;
+    });
+}
+
+MFLAT_API mflat_status_t mflat_flat_search_device(mflat_flat_index_t* h, const float* q, int m, int k,
+                                                  int32_t* oi, float* od, int* ok, void* stream) {
+    if (!h || !q) return MFLAT_ERR_NULL_ARG;
+    if (m < 0 || k < 1) return MFLAT_ERR_BAD_ARG;
+    if (m == 0) {
+        if (ok) *ok = 0;
+        return MFLAT_OK;
+    }
+    return guarded([&] {
+        std::lock_guard<std::mutex> lk(h->mu);
+        const int used = h->idx.searchDevice(q, m, k, oi, od, static_cast<hipStream_t>(stream));
+        if (ok) *ok = used;
+        return MFLAT_OK;
+    });
+}
+
+MFLAT_API mflat_status_t mflat_flat_add_device(mflat_flat_index_t* h, const float* v, int n, void* stream) {
+    if (!h || !v) return MFLAT_ERR_NULL_ARG;
+    if (n < 0) return MFLAT_ERR_BAD_ARG;
+    return guarded([&] {
+        std::lock_guard<std::mutex> lk(h->mu);
+        if (n > 0 && !h->idx.ready())
+            throw mflat_amd::NotReady("no usable HIP device: device-pointer add needs a gfx950 GPU");
+        h->idx.addDevice(v, n, static_cast<hipStream_t>(stream));
+        return MFLAT_OK;
+    });
+}
+
+MFLAT_API void mflat_profile_enable(int on) { mflat_amd::prof_enable(on); }
+MFLAT_API void mflat_profile_reset(void) { mflat_amd::prof_reset(); }
+MFLAT_API int mflat_profile_read(const char* name, double* total_ms, long long* launches) {
+    return mflat_amd::prof_read(name, total_ms, launches);
+}
+
+}  // extern "C"

@@ -1,0 +1,193 @@
+# SPDX-License-Identifier: Apache-2.0
+"""ctypes binding of libmflat.so (the C ABI declared in include/mflat.h).
+
+This is the binding a Python caller of the reference's C ABI
+(c/include/mflat.h) would write: opaque handle, status codes, caller-owned
+output arrays. It loads the in-tree build at metal-flat_amd/lib/libmflat.so and
+raises if it is missing -- there is no other implementation behind it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_longlong, c_void_p
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libmflat.so")
+
+MFLAT_METRIC_L2 = 0
+MFLAT_METRIC_INNER_PRODUCT = 1
+MFLAT_METRIC_COSINE = 2
+
+MFLAT_OK = 0
+MFLAT_ERR_NULL_ARG = 1
+MFLAT_ERR_BAD_ARG = 2
+MFLAT_ERR_ALLOC = 3
+MFLAT_ERR_NOT_READY = 4
+MFLAT_ERR_INTERNAL = 5
+
+MFLAT_LOG_INFO, MFLAT_LOG_WARN, MFLAT_LOG_ERROR, MFLAT_LOG_OFF = 0, 1, 2, 3
+
+LOG_HANDLER_T = ctypes.CFUNCTYPE(None, c_int, c_char_p, c_void_p)
+
+# Every symbol include/mflat.h declares, with its ctypes signature.
+SIGNATURES = {
+    "mflat_version": (c_char_p, []),
+    "mflat_status_str": (c_char_p, [c_int]),
+    "mflat_max_k": (c_int, []),
+    "mflat_set_log_handler": (None, [LOG_HANDLER_T, c_void_p]),
+    "mflat_set_log_level": (None, [c_int]),
+    "mflat_log_level": (c_int, []),
+    "mflat_flat_create": (c_void_p, [c_int, c_int, POINTER(c_int)]),
+    "mflat_flat_free": (None, [c_void_p]),
+    "mflat_flat_ready": (c_int, [c_void_p]),
+    "mflat_flat_size": (c_int, [c_void_p]),
+    "mflat_flat_dim": (c_int, [c_void_p]),
+    "mflat_flat_add": (c_int, [c_void_p, c_void_p, c_int]),
+    "mflat_flat_reset": (c_int, [c_void_p]),
+    "mflat_flat_search": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, POINTER(c_int)]),
+    "mflat_flat_search_device": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p,
+                                         POINTER(c_int), c_void_p]),
+    "mflat_flat_add_device": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
+    "mflat_profile_enable": (None, [c_int]),
+    "mflat_profile_reset": (None, []),
+    "mflat_profile_read": (c_int, [c_char_p, POINTER(c_double), POINTER(c_longlong)]),
+}
+
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load libmflat.so once; raises FileNotFoundError if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} not built: run `make -C metal-flat_amd` "
+                                "(or __graft_entry__.build())")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+class MflatError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        self.status = status
+        msg = load().mflat_status_str(status).decode()
+        super().__init__(f"{what}: status {status} ({msg})")
+
+
+def _check(status: int, what: str) -> None:
+    if status != MFLAT_OK:
+        raise MflatError(status, what)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class FlatIndex:
+    """Python view of one mflat_flat_index_t (reference FlatIndex.h:37-77)."""
+
+    def __init__(self, dim: int, metric: int = MFLAT_METRIC_L2):
+        lib = load()
+        st = c_int(-1)
+        self._h = lib.mflat_flat_create(int(dim), int(metric), ctypes.byref(st))
+        if not self._h:
+            raise MflatError(st.value, "mflat_flat_create")
+        self.dim = int(dim)
+        self.metric = int(metric)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            load().mflat_flat_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def handle(self):
+        return self._h
+
+    def ready(self) -> bool:
+        return load().mflat_flat_ready(self._h) == 1
+
+    def size(self) -> int:
+        return load().mflat_flat_size(self._h)
+
+    def add(self, vectors) -> None:
+        v = _f32(vectors).reshape(-1, self.dim)
+        _check(load().mflat_flat_add(self._h, v.ctypes.data, v.shape[0]), "mflat_flat_add")
+
+    def reset(self) -> None:
+        _check(load().mflat_flat_reset(self._h), "mflat_flat_reset")
+
+    def search(self, queries, k: int):
+        """Returns (ids int32 [m, k_used], distances float32 [m, k_used], k_used)."""
+        q = _f32(queries).reshape(-1, self.dim)
+        m = q.shape[0]
+        kk = max(1, min(int(k), load().mflat_max_k()))
+        ids = np.full((max(m, 1), kk), -7, dtype=np.int32)
+        dist = np.full((max(m, 1), kk), np.nan, dtype=np.float32)
+        used = c_int(-1)
+        _check(load().mflat_flat_search(self._h, q.ctypes.data, m, int(k), ids.ctypes.data,
+                                         dist.ctypes.data, ctypes.byref(used)), "mflat_flat_search")
+        ku = used.value
+        flat_i = ids.reshape(-1)[: m * ku].reshape(m, ku)
+        flat_d = dist.reshape(-1)[: m * ku].reshape(m, ku)
+        return flat_i.copy(), flat_d.copy(), ku
+
+    # ---- device-pointer entry points ----
+    # x / q / outputs: any object with .data_ptr() and .shape holding contiguous
+    # device memory of the index's GPU (hipmem.DeviceArray, or a torch tensor
+    # when torch shares the process -- see hipmem's note on runtimes).
+    def add_device(self, x, stream=None) -> None:
+        _check(load().mflat_flat_add_device(self._h, x.data_ptr(), x.shape[0],
+                                            _stream_ptr(stream)), "mflat_flat_add_device")
+
+    def search_device(self, q, k: int, out_ids, out_dist, stream=None) -> int:
+        used = c_int(-1)
+        _check(load().mflat_flat_search_device(
+            self._h, q.data_ptr(), q.shape[0], int(k),
+            out_ids.data_ptr() if out_ids is not None else None,
+            out_dist.data_ptr() if out_dist is not None else None,
+            ctypes.byref(used), _stream_ptr(stream)), "mflat_flat_search_device")
+        return used.value
+
+
+def _stream_ptr(stream):
+    if stream is None:
+        return None
+    return ctypes.c_void_p(int(getattr(stream, "cuda_stream", stream)))
+
+
+def profile_enable(on: bool) -> None:
+    load().mflat_profile_enable(1 if on else 0)
+
+
+def profile_reset() -> None:
+    load().mflat_profile_reset()
+
+
+def profile_read(name: str):
+    ms, n = c_double(0.0), c_longlong(0)
+    rc = load().mflat_profile_read(name.encode(), ctypes.byref(ms), ctypes.byref(n))
+    if rc != 0:
+        raise KeyError(name)
+    return ms.value, n.value

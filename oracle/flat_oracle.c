@@ -1,0 +1,223 @@
+/* SPDX-License-Identifier: Apache-2.0
+ *
+ * flat_oracle.c -- TEST INFRASTRUCTURE ONLY. CPU restatement of the reference's
+ * exact flat-search algorithm, used as the parity checker for the HIP library
+ * and as the CPU baseline timed by bench.py. Nothing in the product library
+ * (metal-flat_amd/) links, loads or calls this file.
+ *
+ * Every function follows a reference function line by line in semantics
+ * (loop order, accumulation type, comparison strictness), written from scratch:
+ *
+ *   orc_dot              src/Distance.h:26-30   float accumulation, c ascending
+ *   orc_sql2             src/Distance.h:33-37   float accumulation of (a-b)^2
+ *   orc_row_sq_norms     src/Distance.h:40-47   double accumulation, cast to float
+ *   orc_normalize_rows   src/Distance.h:50-60   double sum, inv = float(1/sqrt(s))
+ *   orc_cpu_search       src/FlatIndex.mm:259-290 (cpuSearch) with score()
+ *                        src/Distance.h:67-75: running top-k ascending, strict '>'
+ *                        insertion, reversal to nearest-first, -1 / +-inf padding
+ *   orc_flat_search      src/FlatIndex.mm:236-245 + 294-321: FlatIndex::add/search
+ *                        semantics (Cosine normalises db rows and a query copy)
+ *                        without the kMaxK clamp (k is generic in cpuSearch)
+ *   orc_argmin_l2        src/CoarseQuantizer.mm:122-131 strict '<' argmin
+ *                        (k = 1 assignment; must agree with orc_cpu_search k=1)
+ *   orc_brute_lex        bench/bench.mm:52-64 cpuTopkL2: partial sort of
+ *                        (dist, id) pairs -- an independent cross-check
+ *
+ * Build with -ffp-contract=off so no multiply-add is fused: the sums are the
+ * plain sequential fp32 sums the reference's C++ source spells out.
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define ORC_L2 0
+#define ORC_IP 1
+#define ORC_COS 2
+
+float orc_dot(const float* a, const float* b, int dim) {
+    float acc = 0.0f;
+    for (int c = 0; c < dim; ++c) acc += a[c] * b[c];
+    return acc;
+}
+
+float orc_sql2(const float* a, const float* b, int dim) {
+    float acc = 0.0f;
+    for (int c = 0; c < dim; ++c) {
+        float e = a[c] - b[c];
+        acc += e * e;
+    }
+    return acc;
+}
+
+void orc_row_sq_norms(const float* v, int64_t n, int dim, float* out) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float* row = v + i * dim;
+        double s = 0.0;
+        for (int c = 0; c < dim; ++c) s += (double)row[c] * row[c];
+        out[i] = (float)s;
+    }
+}
+
+void orc_normalize_rows(float* v, int64_t n, int dim) {
+    for (int64_t i = 0; i < n; ++i) {
+        float* row = v + i * dim;
+        double s = 0.0;
+        for (int c = 0; c < dim; ++c) s += (double)row[c] * row[c];
+        if (s > 0.0) {
+            const float inv = (float)(1.0 / sqrt(s));
+            for (int c = 0; c < dim; ++c) row[c] *= inv;
+        }
+    }
+}
+
+/* Ranking score, larger = nearer: L2 -> -sqL2, IP/Cosine -> dot. */
+static inline float orc_score(int metric, const float* q, const float* x, int dim) {
+    return metric == ORC_L2 ? -orc_sql2(q, x, dim) : orc_dot(q, x, dim);
+}
+static inline float orc_score_to_value(int metric, float s) {
+    return metric == ORC_L2 ? -s : s;
+}
+
+/* One query of cpuSearch. best_s/best_i: scratch of k entries. */
+static void orc_search_one(const float* db, int64_t nb, int dim, int metric,
+                           const float* q, int k, float* best_s, int32_t* best_i,
+                           int32_t* out_ids, float* out_vals) {
+    for (int i = 0; i < k; ++i) { best_s[i] = -INFINITY; best_i[i] = -1; }
+    for (int64_t j = 0; j < nb; ++j) {
+        const float s = orc_score(metric, q, db + j * dim, dim);
+        if (s > best_s[0]) {
+            int pos = 0;
+            while (pos + 1 < k && s > best_s[pos + 1]) {
+                best_s[pos] = best_s[pos + 1];
+                best_i[pos] = best_i[pos + 1];
+                ++pos;
+            }
+            best_s[pos] = s;
+            best_i[pos] = (int32_t)j;
+        }
+    }
+    for (int i = 0; i < k; ++i) {
+        const int src = k - 1 - i;
+        out_ids[i] = best_i[src];
+        /* unfilled slots keep -inf -> value +inf (L2) / -inf (IP), which is
+           emptyValue() of src/Distance.h:73-75 */
+        out_vals[i] = orc_score_to_value(metric, best_s[src]);
+    }
+}
+
+typedef struct {
+    const float* db; int64_t nb; int dim; int metric;
+    const float* q; int k; int32_t* ids; float* vals;
+    int64_t lo, hi; int status;
+} orc_job_t;
+
+static void* orc_worker(void* arg) {
+    orc_job_t* j = (orc_job_t*)arg;
+    float* bs = (float*)malloc(sizeof(float) * (size_t)j->k);
+    int32_t* bi = (int32_t*)malloc(sizeof(int32_t) * (size_t)j->k);
+    if (!bs || !bi) { free(bs); free(bi); j->status = -1; return NULL; }
+    for (int64_t qi = j->lo; qi < j->hi; ++qi)
+        orc_search_one(j->db, j->nb, j->dim, j->metric, j->q + qi * j->dim, j->k, bs, bi,
+                       j->ids + qi * j->k, j->vals + qi * j->k);
+    free(bs); free(bi);
+    j->status = 0;
+    return NULL;
+}
+
+/* cpuSearch over already-prepared rows (metric: 0 L2, 1 IP; Cosine callers pass
+   normalised rows with metric 1). threads <= 1 runs the reference's serial loop
+   on the calling thread; more threads split the queries in contiguous chunks
+   (as bench/bench.mm:134-156 does for its baseline). Returns 0 on success. */
+int orc_cpu_search(const float* db, int64_t nb, int dim, int metric, const float* q,
+                   int64_t m, int k, int32_t* out_ids, float* out_vals, int threads) {
+    if (k < 1 || m < 0 || dim <= 0) return -2;
+    const int sm = (metric == ORC_L2) ? ORC_L2 : ORC_IP;
+    if (threads <= 1 || m < 2) {
+        orc_job_t j = {db, nb, dim, sm, q, k, out_ids, out_vals, 0, m, 0};
+        orc_worker(&j);
+        return j.status;
+    }
+    if (threads > 256) threads = 256;
+    pthread_t tid[256];
+    orc_job_t jobs[256];
+    const int64_t chunk = (m + threads - 1) / threads;
+    int started = 0, rc = 0;
+    for (int t = 0; t < threads; ++t) {
+        const int64_t lo = (int64_t)t * chunk;
+        const int64_t hi = lo + chunk < m ? lo + chunk : m;
+        if (lo >= hi) break;
+        orc_job_t jj = {db, nb, dim, sm, q, k, out_ids, out_vals, lo, hi, 0};
+        jobs[t] = jj;
+        if (pthread_create(&tid[t], NULL, orc_worker, &jobs[t]) != 0) { rc = -1; break; }
+        ++started;
+    }
+    for (int t = 0; t < started; ++t) {
+        pthread_join(tid[t], NULL);
+        if (jobs[t].status != 0) rc = -1;
+    }
+    return rc;
+}
+
+/* FlatIndex::add + FlatIndex::search semantics (unclamped k): Cosine stores
+   normalised copies of the rows and normalises a copy of the queries, then
+   ranks by the dot product. Returns 0 on success. */
+int orc_flat_search(const float* db, int64_t nb, int dim, int metric, const float* q,
+                    int64_t m, int k, int32_t* out_ids, float* out_vals, int threads) {
+    if (metric != ORC_COS)
+        return orc_cpu_search(db, nb, dim, metric, q, m, k, out_ids, out_vals, threads);
+    float* dbn = (float*)malloc(sizeof(float) * (size_t)(nb > 0 ? nb : 1) * dim);
+    float* qn = (float*)malloc(sizeof(float) * (size_t)(m > 0 ? m : 1) * dim);
+    if (!dbn || !qn) { free(dbn); free(qn); return -1; }
+    memcpy(dbn, db, sizeof(float) * (size_t)nb * dim);
+    memcpy(qn, q, sizeof(float) * (size_t)m * dim);
+    orc_normalize_rows(dbn, nb, dim);
+    orc_normalize_rows(qn, m, dim);
+    const int rc = orc_cpu_search(dbn, nb, dim, ORC_IP, qn, m, k, out_ids, out_vals, threads);
+    free(dbn); free(qn);
+    return rc;
+}
+
+/* Strict '<' argmin of the squared L2 distance (lowest index wins ties). */
+void orc_argmin_l2(const float* pts, int64_t n, const float* cents, int64_t c, int dim,
+                   int32_t* out_ids, float* out_d) {
+    for (int64_t i = 0; i < n; ++i) {
+        float best = INFINITY;
+        int32_t bc = 0;
+        for (int64_t j = 0; j < c; ++j) {
+            const float d = orc_sql2(pts + i * dim, cents + j * dim, dim);
+            if (d < best) { best = d; bc = (int32_t)j; }
+        }
+        out_ids[i] = bc;
+        out_d[i] = best;
+    }
+}
+
+/* Independent cross-check: full lexicographic (dist, id) sort per query, L2. */
+typedef struct { float d; int32_t id; } orc_pair_t;
+static int orc_pair_cmp(const void* a, const void* b) {
+    const orc_pair_t* x = (const orc_pair_t*)a;
+    const orc_pair_t* y = (const orc_pair_t*)b;
+    if (x->d < y->d) return -1;
+    if (x->d > y->d) return 1;
+    return (x->id > y->id) - (x->id < y->id);
+}
+int orc_brute_lex(const float* db, int64_t nb, int dim, const float* q, int64_t m, int k,
+                  int32_t* out_ids, float* out_vals) {
+    orc_pair_t* all = (orc_pair_t*)malloc(sizeof(orc_pair_t) * (size_t)(nb > 0 ? nb : 1));
+    if (!all) return -1;
+    for (int64_t qi = 0; qi < m; ++qi) {
+        for (int64_t j = 0; j < nb; ++j) {
+            all[j].d = orc_sql2(q + qi * dim, db + j * dim, dim);
+            all[j].id = (int32_t)j;
+        }
+        qsort(all, (size_t)nb, sizeof(orc_pair_t), orc_pair_cmp);
+        for (int i = 0; i < k; ++i) {
+            out_ids[qi * k + i] = i < nb ? all[i].id : -1;
+            out_vals[qi * k + i] = i < nb ? all[i].d : INFINITY;
+        }
+    }
+    free(all);
+    return 0;
+}

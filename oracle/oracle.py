@@ -1,0 +1,127 @@
+# SPDX-License-Identifier: Apache-2.0
+"""TEST INFRASTRUCTURE ONLY: ctypes access to the CPU oracle (flat_oracle.c,
+built into oracle/_build/liboracle.so) and, where it was built, to the
+reference's own Distance.h primitives (oracle/_ref/libref_distance.so).
+
+Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use this
+module, as the checker or as the timed CPU baseline -- never as the product.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_float, c_int, c_int64, c_void_p
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(_HERE, "_build", "liboracle.so")
+REF_SO = os.path.join(_HERE, "_ref", "libref_distance.so")
+
+_o = None
+_r = None
+
+
+def lib():
+    global _o
+    if _o is None:
+        if not os.path.exists(ORACLE_SO):
+            raise FileNotFoundError(f"{ORACLE_SO} not built: run `make -C oracle`")
+        o = ctypes.CDLL(ORACLE_SO)
+        o.orc_dot.restype = c_float
+        o.orc_dot.argtypes = [c_void_p, c_void_p, c_int]
+        o.orc_sql2.restype = c_float
+        o.orc_sql2.argtypes = [c_void_p, c_void_p, c_int]
+        o.orc_row_sq_norms.restype = None
+        o.orc_row_sq_norms.argtypes = [c_void_p, c_int64, c_int, c_void_p]
+        o.orc_normalize_rows.restype = None
+        o.orc_normalize_rows.argtypes = [c_void_p, c_int64, c_int]
+        for name in ("orc_cpu_search", "orc_flat_search"):
+            f = getattr(o, name)
+            f.restype = c_int
+            f.argtypes = [c_void_p, c_int64, c_int, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_int]
+        o.orc_argmin_l2.restype = None
+        o.orc_argmin_l2.argtypes = [c_void_p, c_int64, c_void_p, c_int64, c_int, c_void_p, c_void_p]
+        o.orc_brute_lex.restype = c_int
+        o.orc_brute_lex.argtypes = [c_void_p, c_int64, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p]
+        _o = o
+    return _o
+
+
+def ref_lib():
+    """The reference's own primitives, or None when oracle/_ref was not built."""
+    global _r
+    if _r is None and os.path.exists(REF_SO):
+        r = ctypes.CDLL(REF_SO)
+        r.ref_dot.restype = c_float
+        r.ref_dot.argtypes = [c_void_p, c_void_p, c_int]
+        r.ref_sql2.restype = c_float
+        r.ref_sql2.argtypes = [c_void_p, c_void_p, c_int]
+        r.ref_row_sq_norms.restype = None
+        r.ref_row_sq_norms.argtypes = [c_void_p, c_int, c_int, c_void_p]
+        r.ref_normalize_rows.restype = None
+        r.ref_normalize_rows.argtypes = [c_void_p, c_int, c_int]
+        r.ref_score.restype = c_float
+        r.ref_score.argtypes = [c_int, c_void_p, c_void_p, c_int]
+        r.ref_score_to_value.restype = c_float
+        r.ref_score_to_value.argtypes = [c_int, c_float]
+        r.ref_empty_value.restype = c_float
+        r.ref_empty_value.argtypes = [c_int]
+        r.ref_l2_score_from_dot.restype = c_float
+        r.ref_l2_score_from_dot.argtypes = [c_float, c_float, c_float]
+        _r = r
+    return _r
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def flat_search(db, q, k, metric=0, threads=1):
+    """FlatIndex add+search semantics of the reference CPU path (unclamped k).
+    Returns (ids int32 [m, k], values float32 [m, k])."""
+    db = _f32(db)
+    q = _f32(q)
+    d = db.shape[1] if db.ndim == 2 and db.size else q.shape[1]
+    nb = db.shape[0] if db.size else 0
+    m = q.shape[0]
+    ids = np.empty((m, k), dtype=np.int32)
+    vals = np.empty((m, k), dtype=np.float32)
+    rc = lib().orc_flat_search(db.ctypes.data, nb, d, metric, q.ctypes.data, m, k,
+                               ids.ctypes.data, vals.ctypes.data, threads)
+    if rc != 0:
+        raise RuntimeError(f"orc_flat_search rc={rc}")
+    return ids, vals
+
+
+def row_sq_norms(v):
+    v = _f32(v)
+    out = np.empty(v.shape[0], dtype=np.float32)
+    lib().orc_row_sq_norms(v.ctypes.data, v.shape[0], v.shape[1], out.ctypes.data)
+    return out
+
+
+def normalize_rows(v):
+    v = _f32(v).copy()
+    lib().orc_normalize_rows(v.ctypes.data, v.shape[0], v.shape[1])
+    return v
+
+
+def argmin_l2(pts, cents):
+    pts = _f32(pts)
+    cents = _f32(cents)
+    ids = np.empty(pts.shape[0], dtype=np.int32)
+    d = np.empty(pts.shape[0], dtype=np.float32)
+    lib().orc_argmin_l2(pts.ctypes.data, pts.shape[0], cents.ctypes.data, cents.shape[0],
+                        pts.shape[1], ids.ctypes.data, d.ctypes.data)
+    return ids, d
+
+
+def brute_lex(db, q, k):
+    db = _f32(db)
+    q = _f32(q)
+    ids = np.empty((q.shape[0], k), dtype=np.int32)
+    vals = np.empty((q.shape[0], k), dtype=np.float32)
+    lib().orc_brute_lex(db.ctypes.data, db.shape[0], db.shape[1], q.ctypes.data, q.shape[0], k,
+                        ids.ctypes.data, vals.ctypes.data)
+    return ids, vals

@@ -1,0 +1,133 @@
+# SPDX-License-Identifier: Apache-2.0
+"""C ABI semantics that need no GPU (reference c/mflat.cpp:32-129 and
+c/include/mflat.h:31-90): the library loads, exports every symbol the header
+declares, and validates arguments exactly like the reference shell."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import mflat
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mflat.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"MFLAT_API[^;(]*?\b(mflat_\w+)\s*\(", text)))
+
+
+def test_loads_and_exports_every_declared_symbol():
+    lib = mflat.load()
+    syms = header_symbols()
+    assert len(syms) >= 19, syms
+    for s in syms:
+        assert hasattr(lib, s), s
+    assert set(syms) == set(mflat.SIGNATURES), set(syms) ^ set(mflat.SIGNATURES)
+
+
+def test_version_status_maxk():
+    lib = mflat.load()
+    assert lib.mflat_version() == b"0.1.0"
+    assert lib.mflat_max_k() == 1024
+    expect = {0: b"ok", 1: b"null argument", 2: b"bad argument", 3: b"allocation failed",
+              4: b"index not ready", 5: b"internal error"}
+    for k, v in expect.items():
+        assert lib.mflat_status_str(k) == v
+    assert lib.mflat_status_str(99) == b"unknown"
+
+
+def test_create_arguments():
+    lib = mflat.load()
+    st = ctypes.c_int(-1)
+    assert not lib.mflat_flat_create(0, 0, ctypes.byref(st)) and st.value == mflat.MFLAT_ERR_BAD_ARG
+    assert not lib.mflat_flat_create(-3, 0, None)
+    h = lib.mflat_flat_create(7, 42, ctypes.byref(st))   # unknown metric maps to L2
+    assert h and st.value == 0
+    assert lib.mflat_flat_dim(h) == 7 and lib.mflat_flat_size(h) == 0
+    lib.mflat_flat_free(h)
+    lib.mflat_flat_free(None)   # NULL is a no-op
+
+
+def test_null_handles_and_arguments():
+    lib = mflat.load()
+    x = np.zeros((2, 4), np.float32)
+    used = ctypes.c_int(-1)
+    assert lib.mflat_flat_add(None, x.ctypes.data, 2) == mflat.MFLAT_ERR_NULL_ARG
+    assert lib.mflat_flat_reset(None) == mflat.MFLAT_ERR_NULL_ARG
+    assert lib.mflat_flat_search(None, x.ctypes.data, 1, 1, None, None, None) == mflat.MFLAT_ERR_NULL_ARG
+    assert lib.mflat_flat_ready(None) == 0 and lib.mflat_flat_size(None) == 0 and lib.mflat_flat_dim(None) == 0
+    h = lib.mflat_flat_create(4, 0, None)
+    try:
+        assert lib.mflat_flat_add(h, None, 2) == mflat.MFLAT_ERR_NULL_ARG
+        assert lib.mflat_flat_add(h, x.ctypes.data, -1) == mflat.MFLAT_ERR_BAD_ARG
+        assert lib.mflat_flat_add(h, x.ctypes.data, 0) == mflat.MFLAT_OK
+        assert lib.mflat_flat_search(h, None, 1, 1, None, None, None) == mflat.MFLAT_ERR_NULL_ARG
+        assert lib.mflat_flat_search(h, x.ctypes.data, -1, 1, None, None, None) == mflat.MFLAT_ERR_BAD_ARG
+        assert lib.mflat_flat_search(h, x.ctypes.data, 1, 0, None, None, None) == mflat.MFLAT_ERR_BAD_ARG
+        # m == 0: OK with k_used = 0 (reference c/mflat.cpp:44), before any device use
+        assert lib.mflat_flat_search(h, x.ctypes.data, 0, 5, None, None, ctypes.byref(used)) == 0
+        assert used.value == 0
+        assert lib.mflat_flat_search_device(h, None, 1, 1, None, None, None, None) == mflat.MFLAT_ERR_NULL_ARG
+        assert lib.mflat_flat_search_device(h, x.ctypes.data, 1, 0, None, None, None, None) == mflat.MFLAT_ERR_BAD_ARG
+        assert lib.mflat_flat_add_device(h, x.ctypes.data, -2, None) == mflat.MFLAT_ERR_BAD_ARG
+    finally:
+        lib.mflat_flat_free(h)
+
+
+def test_log_level_roundtrip_and_handler():
+    lib = mflat.load()
+    got = []
+
+    @mflat.LOG_HANDLER_T
+    def handler(level, msg, user):
+        got.append((level, msg.decode()))
+
+    old = lib.mflat_log_level()
+    try:
+        lib.mflat_set_log_level(mflat.MFLAT_LOG_WARN)
+        assert lib.mflat_log_level() == mflat.MFLAT_LOG_WARN
+        lib.mflat_set_log_handler(handler, None)
+        idx = mflat.FlatIndex(8)
+        if idx.ready():
+            pytest.skip("a GPU is present; the no-device message is not emitted")
+        # no device: search fails loudly with NOT_READY and an error message
+        idx.add(np.ones((3, 8), np.float32))
+        assert idx.size() == 3
+        with pytest.raises(mflat.MflatError) as e:
+            idx.search(np.ones((1, 8), np.float32), 2)
+        assert e.value.status == mflat.MFLAT_ERR_NOT_READY
+        assert any(lv == mflat.MFLAT_LOG_ERROR and "HIP device" in m for lv, m in got), got
+        n = len(got)
+        lib.mflat_set_log_level(mflat.MFLAT_LOG_OFF)
+        with pytest.raises(mflat.MflatError):
+            idx.search(np.ones((1, 8), np.float32), 2)
+        assert len(got) == n            # Off silences everything
+        idx.close()
+    finally:
+        lib.mflat_set_log_handler(ctypes.cast(None, mflat.LOG_HANDLER_T), None)
+        lib.mflat_set_log_level(old)
+
+
+def test_no_device_is_not_ready():
+    idx = mflat.FlatIndex(16, mflat.MFLAT_METRIC_COSINE)
+    if idx.ready():
+        pytest.skip("a GPU is present")
+    assert idx.ready() is False
+    idx.add(np.ones((10, 16), np.float32))
+    idx.reset()
+    assert idx.size() == 0
+    idx.close()
+
+
+def test_profile_names():
+    mflat.profile_reset()
+    for name in ("scan_filter", "scan_sample", "select", "argmin", "norms", "prep"):
+        ms, n = mflat.profile_read(name)
+        assert ms == 0.0 and n == 0
+    with pytest.raises(KeyError):
+        mflat.profile_read("nope")

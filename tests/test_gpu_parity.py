@@ -1,0 +1,233 @@
+# SPDX-License-Identifier: Apache-2.0
+"""GPU parity: the HIP path through the C ABI vs the CPU oracle on the same
+seeded inputs (reduced sizes of the BASELINE.json configurations, plus the edge
+cases of the reference's flat-search semantics)."""
+import numpy as np
+import pytest
+
+import datagen
+import mflat
+import oracle
+import parity
+from conftest import oracle_threads
+
+pytestmark = pytest.mark.gpu
+
+L2, IP, COS = mflat.MFLAT_METRIC_L2, mflat.MFLAT_METRIC_INNER_PRODUCT, mflat.MFLAT_METRIC_COSINE
+
+
+def run(x, q, k, metric):
+    with mflat.FlatIndex(x.shape[1], metric) as idx:
+        assert idx.ready()
+        idx.add(x)
+        return idx.search(q, k)
+
+
+def orc(x, q, k, metric):
+    return oracle.flat_search(x, q, k, metric=metric, threads=oracle_threads())
+
+
+# ---- integer-valued data: bit-exact ------------------------------------------
+
+@pytest.mark.parametrize("nb,nq,k", [(20_000, 300, 10), (3_000, 129, 100), (100, 7, 10), (50_000, 257, 1)])
+def test_integer_exact(gpu_ok, nb, nq, k):
+    x, q = datagen.sift_like(nb=nb, nq=nq, seed=0)
+    gi, gd, ku = run(x, q, k, L2)
+    assert ku == k
+    oi, od = orc(x, q, k, L2)
+    parity.exact(gi, gd, oi, od)
+
+
+def test_c1_full_exact(gpu_ok):
+    """C1 at its full size: 100k x 128 integer-valued, 1k queries, k=10, seed 0."""
+    x, q = datagen.sift_like(seed=0)
+    gi, gd, ku = run(x, q, 10, L2)
+    oi, od = orc(x, q, 10, L2)
+    parity.exact(gi, gd, oi, od)
+
+
+def test_ties_duplicates_exact(gpu_ok):
+    """Massive exact ties: 40k rows drawn from 81 distinct vectors. Equal
+    distances must come out in ascending id order, and the bound refinement must
+    terminate with lexicographic (key, id) thresholds."""
+    rng = np.random.default_rng(7)
+    x = rng.integers(0, 3, size=(40_000, 4)).astype(np.float32)
+    q = rng.integers(0, 3, size=(130, 4)).astype(np.float32)
+    for k in (1, 10, 300):
+        gi, gd, _ = run(x, q, k, L2)
+        oi, od = orc(x, q, k, L2)
+        parity.exact(gi, gd, oi, od)
+
+
+def test_padding_and_small_db(gpu_ok):
+    x, q = datagen.sift_like(nb=37, nq=5, seed=3)
+    gi, gd, ku = run(x, q, 100, L2)
+    assert ku == 100
+    oi, od = orc(x, q, 100, L2)
+    parity.exact(gi, gd, oi, od)
+    assert np.all(gi[:, 37:] == -1) and np.all(np.isinf(gd[:, 37:]))
+
+
+def test_empty_db(gpu_ok):
+    with mflat.FlatIndex(16, IP) as idx:
+        gi, gd, ku = idx.search(np.ones((3, 16), np.float32), 5)
+    assert ku == 5 and np.all(gi == -1) and np.all(gd == -np.inf)
+    with mflat.FlatIndex(16, L2) as idx:
+        gi, gd, ku = idx.search(np.ones((3, 16), np.float32), 5)
+    assert np.all(gd == np.inf)
+
+
+def test_adversarial_order_retries(gpu_ok):
+    """Rows on the sample's stride are far away, so the first bounds are loose and
+    candidate regions overflow; the retry rounds must still give the exact answer."""
+    rng = np.random.default_rng(11)
+    nb = 60_000
+    x = rng.integers(0, 16, size=(nb, 32)).astype(np.float32)
+    x[::7] += 200.0
+    x[::13] += 200.0
+    q = rng.integers(0, 16, size=(150, 32)).astype(np.float32)
+    gi, gd, _ = run(x, q, 50, L2)
+    oi, od = orc(x, q, 50, L2)
+    parity.exact(gi, gd, oi, od)
+
+
+def test_clamp_k(gpu_ok):
+    x, q = datagen.sift_like(nb=3000, nq=4, seed=5)
+    gi, gd, ku = run(x, q, 5000, L2)
+    assert ku == mflat.load().mflat_max_k() == 1024
+    oi, od = orc(x, q, 1024, L2)
+    parity.exact(gi, gd, oi, od)
+
+
+# ---- floating-point data: north-star tolerances ------------------------------
+
+def test_gmm_l2_k100(gpu_ok):
+    """Reduced C2: GMM (1,024 centres, sigma 0.3), L2, k=100."""
+    x, q = datagen.gmm(nb=200_000, nq=400, seed=1)
+    gi, gd, _ = run(x, q, 100, L2)
+    oi, od = orc(x, q, 100, L2)
+    parity.sorted_lex(gi, gd, 0)
+    parity.tolerant(gi, gd, oi, od, x, q, 0)
+
+
+def test_unit_ip_d768(gpu_ok):
+    """Reduced C3: unit-normalised N(0, I), d=768, inner product, k=100."""
+    x, q = datagen.unit_normal(nb=40_000, nq=200, seed=2)
+    gi, gd, _ = run(x, q, 100, IP)
+    oi, od = orc(x, q, 100, IP)
+    parity.sorted_lex(gi, gd, 1)
+    parity.tolerant(gi, gd, oi, od, x, q, 1)
+
+
+def test_cosine(gpu_ok):
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal((30_000, 100)) * 3).astype(np.float32)
+    x[5] = 0.0   # zero rows stay zero (reference Distance.h:55)
+    q = rng.standard_normal((70, 100)).astype(np.float32)
+    gi, gd, _ = run(x, q, 20, COS)
+    oi, od = orc(x, q, 20, COS)
+    parity.tolerant(gi, gd, oi, od, oracle.normalize_rows(x), oracle.normalize_rows(q), 1)
+
+
+def test_uniform_small_batch(gpu_ok):
+    """Reduced C4: uniform [-1, 1], d=96, nq in {1, 16, 64}, k=10."""
+    x, q = datagen.uniform_pm1(nb=300_000, nq=64, seed=3)
+    for nq in (1, 16, 64):
+        gi, gd, _ = run(x, q[:nq], 10, L2)
+        oi, od = orc(x, q[:nq], 10, L2)
+        parity.tolerant(gi, gd, oi, od, x, q[:nq], 0)
+
+
+def test_kmeans_assign_k1(gpu_ok):
+    """Reduced C5: nearest centroid (k=1) with exact self-matches."""
+    cents, pts = datagen.kmeans_assign(npts=60_000, ncent=4096, seed=4)
+    gi, gd, _ = run(cents, pts, 1, L2)
+    oi, od = oracle.argmin_l2(pts, cents)
+    parity.tolerant(gi, gd, oi[:, None], od[:, None], cents, pts, 0)
+
+
+def test_odd_shapes(gpu_ok):
+    rng = np.random.default_rng(13)
+    for d, nb, nq in ((1, 5000, 3), (33, 12_345, 130), (129, 9_999, 257)):
+        x = rng.integers(-8, 8, size=(nb, d)).astype(np.float32)
+        q = rng.integers(-8, 8, size=(nq, d)).astype(np.float32)
+        for metric in (L2, IP):
+            gi, gd, _ = run(x, q, 17, metric)
+            oi, od = orc(x, q, 17, metric)
+            parity.exact(gi, gd, oi, od)
+
+
+def test_incremental_add_and_reset(gpu_ok):
+    x, q = datagen.sift_like(nb=30_000, nq=100, seed=21)
+    with mflat.FlatIndex(128, L2) as idx:
+        idx.add(x[:10_000])
+        a = idx.search(q, 10)
+        idx.add(x[10_000:])
+        gi, gd, _ = idx.search(q, 10)
+        assert idx.size() == 30_000
+        oi, od = orc(x, q, 10, L2)
+        parity.exact(gi, gd, oi, od)
+        oa, oad = orc(x[:10_000], q, 10, L2)
+        parity.exact(a[0], a[1], oa, oad)
+        idx.reset()
+        assert idx.size() == 0
+        ri, rd, _ = idx.search(q, 3)
+        assert np.all(ri == -1)
+
+
+def test_device_entry_matches_host(gpu_ok):
+    import hipmem
+
+    x, q = datagen.sift_like(nb=20_000, nq=200, seed=2)
+    with mflat.FlatIndex(128, L2) as idx:
+        xd = hipmem.DeviceArray.from_numpy(x)
+        idx.add_device(xd)
+        qd = hipmem.DeviceArray.from_numpy(q)
+        ids = hipmem.DeviceArray((200, 10), np.int32)
+        dist = hipmem.DeviceArray((200, 10), np.float32)
+        st = hipmem.Stream()
+        ku = idx.search_device(qd, 10, ids, dist, stream=st)
+        st.synchronize()
+        hi, hd, _ = idx.search(q, 10)
+        st.destroy()
+    assert ku == 10
+    assert np.array_equal(ids.numpy(), hi) and np.array_equal(dist.numpy(), hd)
+    oi, od = orc(x, q, 10, L2)
+    parity.exact(hi, hd, oi, od)
+
+
+TORCH_FIRST = r"""
+import sys, numpy as np, torch
+torch.zeros(1, device="cuda")          # torch's HIP runtime initialised first
+sys.path[:0] = [sys.argv[1], sys.argv[2]]
+import mflat, oracle
+rng = np.random.default_rng(1)
+x = rng.integers(0, 256, size=(9000, 64)).astype(np.float32)
+q = rng.integers(0, 256, size=(50, 64)).astype(np.float32)
+idx = mflat.FlatIndex(64)
+assert idx.ready()
+idx.add(torch.from_numpy(x).cuda().cpu().numpy())
+xd = torch.from_numpy(q).cuda()
+ids = torch.empty((50, 7), dtype=torch.int32, device="cuda")
+dd = torch.empty((50, 7), dtype=torch.float32, device="cuda")
+idx.search_device(xd, 7, ids, dd, stream=torch.cuda.current_stream())
+torch.cuda.synchronize()
+oi, od = oracle.flat_search(x, q, 7)
+assert np.array_equal(ids.cpu().numpy(), oi) and np.array_equal(dd.cpu().numpy(), od)
+print("torch-first ok")
+"""
+
+
+def test_shares_process_with_torch_when_torch_loads_first(gpu_ok):
+    """Single-runtime rule: with torch's GPU backend initialised before
+    libmflat.so loads, the library binds to torch's HIP runtime and interoperates
+    with torch tensors and streams (run in a fresh process)."""
+    import os
+    import subprocess
+    import sys
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    r = subprocess.run([sys.executable, "-c", TORCH_FIRST, os.path.join(root, "metal-flat_amd"),
+                        os.path.join(root, "oracle")], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and "torch-first ok" in r.stdout, r.stdout[-2000:] + r.stderr[-2000:]

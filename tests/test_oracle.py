@@ -1,0 +1,195 @@
+# SPDX-License-Identifier: Apache-2.0
+"""Pins the CPU oracle before it is trusted as the parity checker.
+
+The reference holds no golden vectors or known-answer tests for this path, so
+the oracle is pinned by:
+  * the reference's own primitives (src/Distance.h, compiled where it lies into
+    oracle/_ref by `make -C oracle ref`), bit for bit, live when built and via
+    the committed fixture tests/golden/distance_primitives.npz otherwise;
+  * closed forms (orthonormal bases, integer data whose fp32 sums are exact,
+    exact self-matches, duplicated rows);
+  * brute force: an independent lexicographic full sort and numpy float64;
+  * invariants (sortedness, prefix property, padding, cosine == IP on unit rows,
+    k = 1 == argmin).
+Each check is chosen so a plausible slip (reversed tie order, '>=' instead of
+'>', a dropped term, a wrong sign, float instead of double norms) fails it.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def rnd(shape, seed, lo=-3.0, hi=3.0):
+    return np.random.default_rng(seed).uniform(lo, hi, size=shape).astype(np.float32)
+
+
+def test_primitives_vs_reference_fixture():
+    g = np.load(os.path.join(GOLDEN, "distance_primitives.npz"))
+    a, b, v = g["a"], g["b"], g["v"]
+    o = oracle.lib()
+    d = a.shape[1]
+    dots = np.array([o.orc_dot(a[i].ctypes.data, b[i].ctypes.data, d) for i in range(a.shape[0])], np.float32)
+    sq = np.array([o.orc_sql2(a[i].ctypes.data, b[i].ctypes.data, d) for i in range(a.shape[0])], np.float32)
+    assert np.array_equal(dots.view(np.uint32), g["dot"].view(np.uint32))
+    assert np.array_equal(sq.view(np.uint32), g["sql2"].view(np.uint32))
+    assert np.array_equal(oracle.row_sq_norms(v).view(np.uint32), g["norms"].view(np.uint32))
+    assert np.array_equal(oracle.normalize_rows(v).view(np.uint32), g["normalized"].view(np.uint32))
+
+
+@pytest.mark.skipif(oracle.ref_lib() is None, reason="oracle/_ref not built (reference tree absent)")
+def test_primitives_vs_reference_live():
+    r = oracle.ref_lib()
+    o = oracle.lib()
+    for d in (1, 3, 96, 128, 767):
+        a = rnd((50, d), d)
+        b = rnd((50, d), d + 1)
+        for i in range(50):
+            pa, pb = a[i].ctypes.data, b[i].ctypes.data
+            assert np.float32(o.orc_dot(pa, pb, d)) == np.float32(r.ref_dot(pa, pb, d))
+            assert np.float32(o.orc_sql2(pa, pb, d)) == np.float32(r.ref_sql2(pa, pb, d))
+            assert np.float32(r.ref_score(0, pa, pb, d)) == -np.float32(o.orc_sql2(pa, pb, d))
+            assert np.float32(r.ref_score(1, pa, pb, d)) == np.float32(o.orc_dot(pa, pb, d))
+        ref_n = np.empty(50, np.float32)
+        r.ref_row_sq_norms(a.ctypes.data, 50, d, ref_n.ctypes.data)
+        assert np.array_equal(ref_n, oracle.row_sq_norms(a))
+        an = a.copy()
+        an[3] = 0.0
+        ref_v = an.copy()
+        r.ref_normalize_rows(ref_v.ctypes.data, 50, d)
+        assert np.array_equal(ref_v.view(np.uint32), oracle.normalize_rows(an).view(np.uint32))
+    assert r.ref_empty_value(0) == np.inf and r.ref_empty_value(1) == -np.inf
+    assert r.ref_score_to_value(0, -2.5) == 2.5 and r.ref_score_to_value(2, 1.5) == 1.5
+
+
+def test_norms_are_double_accumulated():
+    # A float accumulation of these squares loses the small terms; double keeps them.
+    v = np.array([[4096.0] + [1.0] * 127], np.float32)
+    got = oracle.row_sq_norms(v)[0]
+    assert got == np.float32(4096.0 ** 2 + 127)
+    assert got != np.float32(4096.0 ** 2)   # what a float accumulation returns
+
+
+def test_integer_data_matches_float64_brute_force():
+    rng = np.random.default_rng(0)
+    x = rng.integers(0, 256, size=(3000, 64)).astype(np.float32)
+    q = rng.integers(0, 256, size=(40, 64)).astype(np.float32)
+    ids, vals = oracle.flat_search(x, q, 25, metric=0)
+    d = ((q[:, None, :].astype(np.float64) - x[None, :, :]) ** 2).sum(-1)
+    for r in range(40):
+        order = np.lexsort((np.arange(3000), d[r]))[:25]
+        assert np.array_equal(ids[r], order)
+        assert np.array_equal(vals[r], d[r, order].astype(np.float32))
+
+
+def test_matches_independent_lexicographic_sort():
+    x = rnd((2000, 48), 1)
+    q = rnd((30, 48), 2)
+    a_ids, a_vals = oracle.flat_search(x, q, 40, metric=0)
+    b_ids, b_vals = oracle.brute_lex(x, q, 40)
+    assert np.array_equal(a_ids, b_ids) and np.array_equal(a_vals, b_vals)
+
+
+def test_ties_keep_lowest_id_first():
+    base = np.array([[1, 0, 0, 0], [0, 1, 0, 0], [0, 0, 1, 0]], np.float32)
+    x = np.concatenate([base, base, base, base])   # ids i, i+3, i+6, i+9 identical
+    q = np.array([[1, 0, 0, 0]], np.float32)
+    ids, vals = oracle.flat_search(x, q, 6, metric=0)
+    assert ids[0].tolist() == [0, 3, 6, 9, 1, 2]
+    assert vals[0].tolist() == [0, 0, 0, 0, 2, 2]
+    # the k-th slot among equals goes to the lowest id (strict '>' insertion)
+    ids, _ = oracle.flat_search(x, q, 2, metric=0)
+    assert ids[0].tolist() == [0, 3]
+    ids, vals = oracle.flat_search(x, q, 5, metric=1)
+    assert ids[0].tolist() == [0, 3, 6, 9, 1] and vals[0].tolist() == [1, 1, 1, 1, 0]
+
+
+def test_orthonormal_basis_inner_product():
+    d = 32
+    x = np.eye(d, dtype=np.float32)
+    q = rnd((10, d), 5)
+    ids, vals = oracle.flat_search(x, q, 8, metric=1)
+    for r in range(10):
+        order = np.lexsort((np.arange(d), -q[r]))[:8]
+        assert np.array_equal(ids[r], order)
+        assert np.array_equal(vals[r], q[r, order])
+
+
+def test_self_match_is_zero_and_first():
+    x = rnd((500, 20), 6)
+    ids, vals = oracle.flat_search(x, x[:50], 3, metric=0)
+    assert np.array_equal(ids[:, 0], np.arange(50)) and np.all(vals[:, 0] == 0)
+
+
+def test_padding_when_db_smaller_than_k():
+    x = rnd((5, 8), 7)
+    q = rnd((2, 8), 8)
+    for metric, empty in ((0, np.inf), (1, -np.inf), (2, -np.inf)):
+        ids, vals = oracle.flat_search(x, q, 9, metric=metric)
+        assert np.all(ids[:, 5:] == -1) and np.all(vals[:, 5:] == empty)
+        assert sorted(ids[0, :5].tolist()) == [0, 1, 2, 3, 4]
+    ids, vals = oracle.flat_search(np.zeros((0, 8), np.float32), q, 4, metric=0)
+    assert np.all(ids == -1) and np.all(vals == np.inf)
+
+
+def test_sorted_and_prefix_property():
+    x = rnd((4000, 16), 9)
+    q = rnd((20, 16), 10)
+    i10, v10 = oracle.flat_search(x, q, 10, metric=0)
+    i50, v50 = oracle.flat_search(x, q, 50, metric=0)
+    assert np.array_equal(i50[:, :10], i10) and np.array_equal(v50[:, :10], v10)
+    assert np.all(np.diff(v50, axis=1) >= 0)
+    j10, w10 = oracle.flat_search(x, q, 10, metric=1)
+    assert np.all(np.diff(w10, axis=1) <= 0)
+
+
+def test_cosine_equals_ip_on_normalised_rows():
+    x = rnd((1000, 24), 11)
+    q = rnd((15, 24), 12)
+    ci, cv = oracle.flat_search(x, q, 12, metric=2)
+    ii, iv = oracle.flat_search(oracle.normalize_rows(x), oracle.normalize_rows(q), 12, metric=1)
+    assert np.array_equal(ci, ii) and np.array_equal(cv, iv)
+    n = oracle.normalize_rows(np.vstack([x[:3], np.zeros((1, 24), np.float32)]))
+    assert np.all(n[3] == 0)
+    assert np.allclose(np.sum(n[:3].astype(np.float64) ** 2, axis=1), 1.0, atol=1e-6)
+
+
+def test_k1_equals_argmin():
+    x = rnd((3000, 12), 13)
+    q = rnd((100, 12), 14)
+    i1, v1 = oracle.flat_search(x, q, 1, metric=0)
+    ai, ad = oracle.argmin_l2(q, x)
+    assert np.array_equal(i1[:, 0], ai) and np.array_equal(v1[:, 0], ad)
+
+
+def test_nan_rows_never_inserted():
+    x = rnd((50, 8), 15)
+    x[7, 2] = np.nan
+    q = x[7:8].copy()
+    q[0, 2] = 0.0
+    ids, _ = oracle.flat_search(x, q, 50, metric=0)
+    assert 7 not in ids[0].tolist() and ids[0, -1] == -1
+
+
+def test_threaded_equals_serial():
+    x = rnd((3000, 32), 16)
+    q = rnd((64, 32), 17)
+    a = oracle.flat_search(x, q, 20, metric=0, threads=1)
+    b = oracle.flat_search(x, q, 20, metric=0, threads=8)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+def test_golden_flat_fixture():
+    """Regression fixture: oracle results on small fixed inputs (ties, padding,
+    every metric), generated by tests/golden/make_golden.py."""
+    g = np.load(os.path.join(GOLDEN, "flat_small.npz"))
+    for name in sorted({k.split("__")[0] for k in g.files}):
+        x, q = g[name + "__x"], g[name + "__q"]
+        metric, k = int(g[name + "__metric"]), int(g[name + "__k"])
+        ids, vals = oracle.flat_search(x, q, k, metric=metric)
+        assert np.array_equal(ids, g[name + "__ids"]), name
+        assert np.array_equal(vals.view(np.uint32), g[name + "__vals"].view(np.uint32)), name
