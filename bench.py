@@ -146,7 +146,7 @@ def main():
     log(f"[bench] {args.steps} steps in {elapsed:.3f}s")
 
     kern = {}
-    for fam in ("scan_filter", "scan_sample", "select", "argmin", "norms", "prep"):
+    for fam in ("scan_filter", "scan_sample", "scan_retry", "select", "argmin", "norms", "prep"):
         ms, n = mflat.profile_read(fam)
         if n:
             kern[fam] = {"total_ms": round(ms, 4), "launches": n, "mean_ms": round(ms / n, 4)}
@@ -162,9 +162,8 @@ def main():
         roof = {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None}
     else:
-        per_launch = flop * args.steps / scan["launches"]
         mean_s = scan["total_ms"] / scan["launches"] / 1000.0
-        ach = per_launch / mean_s / 1e12
+        ach = flop / mean_s / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None}
 

@@ -123,9 +123,11 @@ MFLAT_API mflat_status_t mflat_flat_add_device(mflat_flat_index_t*, const float*
    kernels is bracketed with HIP events on the stream it runs on; the per-kernel
    totals accumulate process-wide until reset. name: kernel family, one of
    "scan_filter" (fused distance + threshold filter over the database, the
-   hot kernel), "scan_sample" (the same kernel over the row sample that sets
-   the thresholds), "select" (per-query top-k select / merge), "argmin"
-   (fused k = 1), "norms", "prep". Returns 0 and fills the outputs, or -1 for an unknown name. */
+   hot kernel; one launch per search batch), "scan_sample" (the same kernel
+   over the row sample that sets the thresholds), "scan_retry" (the same
+   kernel re-run for the few queries whose threshold must be refined),
+   "select" (per-query top-k select / merge), "argmin" (fused k = 1),
+   "norms", "prep". Returns 0 and fills the outputs, or -1 for an unknown name. */
 MFLAT_API void mflat_profile_enable(int on);
 MFLAT_API void mflat_profile_reset(void);
 MFLAT_API int  mflat_profile_read(const char* name, double* total_ms, long long* launches);

@@ -25,6 +25,8 @@
 
 #include <algorithm>
 #include <climits>
+#include <cstdio>
+#include <cstdlib>
 #include <cmath>
 #include <cstring>
 #include <new>
@@ -36,6 +38,16 @@
 
 namespace mflat_amd {
 namespace {
+
+// MFLAT_TRACE=1 in the environment prints per-search plans and bound
+// refinements to stderr (diagnostics only; results are unaffected).
+bool traceOn() {
+    static const bool on = [] {
+        const char* v = std::getenv("MFLAT_TRACE");
+        return v && *v && *v != '0';
+    }();
+    return on;
+}
 
 void hipCheck(hipError_t e, const char* what) {
     if (e == hipSuccess) return;
@@ -68,12 +80,12 @@ struct DevBuf {
     template <class T> T* as() const { return static_cast<T*>(p); }
 };
 
-// Smallest j in [1, k] with P(Poisson(lambda) >= j) <= 1e-3: the chance that a
+// Smallest j in [1, k] with P(Poisson(lambda) >= j) <= tail: the chance that a
 // speculative bound taken at the sample's j-th best admits fewer than k rows.
-int chooseJ(int k, double lambda) {
+int chooseJ(int k, double lambda, double tail) {
     double term = std::exp(-lambda), cdf = term;
     for (int j = 1; j <= k; ++j) {
-        if (1.0 - cdf <= 1e-3) return j;
+        if (1.0 - cdf <= tail) return j;
         term *= lambda / j;
         cdf += term;
     }
@@ -100,6 +112,7 @@ struct Plan {
     int64_t R0 = 0;       // sample rows
     int stride = 1;       // sample row r is database row r*stride
     int j = 1;            // speculative rank
+    int j2 = 1;           // second, looser speculative rank (first retry)
     int64_t rps0 = 0;
     int nsplit0 = 1, cap0 = 1;
     int64_t rps1 = 0;
@@ -120,6 +133,8 @@ struct FlatIndex::Impl {
     int64_t nb = 0;
     int64_t capRows = 0;
     DevBuf X, xn;
+    float xnMax = 0.0f;   // max finite-or-inf ||x||^2 over the database
+    DevBuf maxBits;
 
     // strided sample of the database (L0)
     int64_t sampleR = 0;
@@ -130,7 +145,7 @@ struct FlatIndex::Impl {
     // per-search workspace
     DevBuf stage, qin, outIds, outVals;
     DevBuf qbuf, qnorm, cand, cnt;
-    DevBuf tauSk, tauSi, tauGk, tauGi, tauKk, tauKi, status;
+    DevBuf tauSk, tauSi, tauS2k, tauS2i, tauGk, tauGi, tauKk, tauKi, status;
     DevBuf cQ, cQn, cTk, cTi, cIdx, cSel;
 
     int kernMetric() const { return metric == Metric::L2 ? 0 : 1; }
@@ -157,7 +172,12 @@ struct FlatIndex::Impl {
         pl.R0 = r;
         pl.stride = (int)(nb / r);
         const double lambda = (double)k * (double)r / (double)nb;
-        pl.j = chooseJ(k, lambda);
+        // A tighter speculative rank means fewer survivors in the full pass
+        // (each costs an exact test and a store in the scan epilogue) at the
+        // price of more queries re-scanned (a retry batch costs the full pass's
+        // time per query block of kBN); ~1% misses balances the two.
+        pl.j = chooseJ(k, lambda, 0.01);
+        pl.j2 = chooseJ(k, lambda, 1e-9);
         splitPlan(r, nqb, pl.rps0, pl.nsplit0);
         pl.cap0 = (int)pl.rps0;
         splitPlan(nb, nqb, pl.rps1, pl.nsplit1);
@@ -210,7 +230,13 @@ struct FlatIndex::Impl {
         }
         if (metric == Metric::Cosine) launch_normalize_rows(dst, n, dpad, s);
         launch_row_norms(dst, n, dpad, xn.as<float>() + nb, s);
+        maxBits.ensure(sizeof(unsigned));
+        HIPC(hipMemsetAsync(maxBits.p, 0, sizeof(unsigned), s));
+        launch_max_norm(xn.as<float>() + nb, n, maxBits.as<unsigned>(), s);
+        float m = 0.0f;
+        HIPC(hipMemcpyAsync(&m, maxBits.p, sizeof(float), hipMemcpyDeviceToHost, s));
         HIPC(hipStreamSynchronize(s));
+        if (m > xnMax) xnMax = m;
         nb += n;
     }
 
@@ -232,24 +258,24 @@ struct FlatIndex::Impl {
 
     void scan(const float* Xs, const float* xns, int64_t nrows, int64_t rps, int nsplit, int idStride,
               const float* Q, const float* qn, int nq, const float* tk, const int* ti, int cap,
-              hipStream_t s, bool sample = false) {
+              hipStream_t s, int pass = kPassFull) {
         const int nqb = (nq + kBN - 1) / kBN;
         cand.ensure((size_t)nq * nsplit * cap * sizeof(uint2));
         cnt.ensure((size_t)nq * nsplit * sizeof(int));
         ScanParams p;
-        p.X = Xs; p.xnorm = xns; p.nrows = nrows; p.rows_per_split = rps; p.nsplit = nsplit;
+        p.X = Xs; p.xnorm = xns; p.xnorm_max = xnMax; p.nrows = nrows; p.rows_per_split = rps; p.nsplit = nsplit;
         p.id_stride = idStride;
         p.Q = Q; p.qnorm = qn; p.nq = nq; p.nqb = nqb; p.dpad = dpad;
         p.tau_key = tk; p.tau_id = ti;
         p.cand = cand.as<uint2>(); p.cnt = cnt.as<int>(); p.cap = cap;
-        launch_scan_filter(p, kernMetric(), sample, s);
+        launch_scan_filter(p, kernMetric(), pass, s);
     }
 
     SelectParams selectParams(int nq, int nsplit, int cap, int k, int j) const {
         SelectParams sp;
         std::memset(&sp, 0, sizeof sp);
         sp.cand = cand.as<uint2>(); sp.cnt = cnt.as<int>();
-        sp.nsplit = nsplit; sp.cap = cap; sp.nq = nq; sp.k = k; sp.j = j;
+        sp.nsplit = nsplit; sp.cap = cap; sp.nq = nq; sp.k = k; sp.j = j; sp.j2 = j;
         sp.metric = kernMetric();
         sp.out_stride = k;
         return sp;
@@ -260,6 +286,7 @@ struct FlatIndex::Impl {
         const float* Q = qbuf.as<float>();
         const float* qn = qnorm.as<float>();
         tauSk.ensure((size_t)mb * 4); tauSi.ensure((size_t)mb * 4);
+        tauS2k.ensure((size_t)mb * 4); tauS2i.ensure((size_t)mb * 4);
         tauGk.ensure((size_t)mb * 4); tauGi.ensure((size_t)mb * 4);
         tauKk.ensure((size_t)mb * 4); tauKi.ensure((size_t)mb * 4);
         status.ensure((size_t)mb * 4);
@@ -275,13 +302,19 @@ struct FlatIndex::Impl {
         }
 
         ensureSample(pl, s);
+        if (traceOn())
+            std::fprintf(stderr, "[mflat trace] mb=%d k=%d nb=%lld R0=%lld stride=%d j=%d j2=%d "
+                         "L0 %dx%d L1 splits=%d cap=%d\n", mb, k, (long long)nb, (long long)pl.R0,
+                         pl.stride, pl.j, pl.j2, pl.nsplit0, pl.cap0, pl.nsplit1, pl.cap1);
         // L0: sample, no bound -> speculative (j-th) and guaranteed (k-th) bounds
         launch_fill_tau_none(tauSk.as<float>(), tauSi.as<int>(), mb, s);
         scan(sX.as<float>(), sXn.as<float>(), pl.R0, pl.rps0, pl.nsplit0, pl.stride, Q, qn, mb,
-             tauSk.as<float>(), tauSi.as<int>(), pl.cap0, s, /*sample=*/true);
+             tauSk.as<float>(), tauSi.as<int>(), pl.cap0, s, kPassSample);
         {
             SelectParams sp = selectParams(mb, pl.nsplit0, pl.cap0, k, pl.j);
+            sp.j2 = pl.j2;
             sp.tau_j_key = tauSk.as<float>(); sp.tau_j_id = tauSi.as<int>();
+            sp.tau_j2_key = tauS2k.as<float>(); sp.tau_j2_id = tauS2i.as<int>();
             sp.tau_k_key = tauGk.as<float>(); sp.tau_k_id = tauGi.as<int>();
             launch_select(sp, s);
         }
@@ -296,19 +329,33 @@ struct FlatIndex::Impl {
             launch_select(sp, s);
         }
 
-        // verification and retries
+        // verification and retries. Per query, the bound used so far:
+        //   0 = speculative (j-th of the sample), 1 = looser speculative (j2-th),
+        //   2 = guaranteed (k-th of the sample or of a stored subset).
         std::vector<int> st((size_t)mb);
         HIPC(hipMemcpyAsync(st.data(), status.p, (size_t)mb * 4, hipMemcpyDeviceToHost, s));
         HIPC(hipStreamSynchronize(s));
-        bool spec = pl.j < k;
+        std::vector<int> level((size_t)mb, pl.j < k ? 0 : 2);
         std::vector<int> live((size_t)mb);
         for (int i = 0; i < mb; ++i) live[(size_t)i] = i;
         for (int round = 0;; ++round) {
+            // sel: 0 -> tau from tauS2 (j2-th), 1 -> tauK (k-th stored), 2 -> tauG (k-th of sample)
             std::vector<int> idx, sel;
             for (int i : live) {
                 const int v = st[(size_t)i];
-                if (v & 1) { idx.push_back(i); sel.push_back(1); }
-                else if (spec && (v & 2)) { idx.push_back(i); sel.push_back(0); }
+                int& lv = level[(size_t)i];
+                if (v & 1) {                       // a region overflowed: tighten from stored
+                    idx.push_back(i); sel.push_back(1); lv = 2;
+                } else if ((v & 2) && lv < 2) {    // speculative bound admitted < k rows
+                    const bool useJ2 = lv == 0 && pl.j2 > pl.j;
+                    idx.push_back(i); sel.push_back(useJ2 ? 0 : 2); lv = useJ2 ? 1 : 2;
+                }
+            }
+            if (traceOn()) {
+                int no = 0;
+                for (int t : sel) no += t == 1;
+                std::fprintf(stderr, "[mflat trace] round %d: %d of %d queries refined (%d overflow, %d under)\n",
+                             round, (int)idx.size(), mb, no, (int)idx.size() - no);
             }
             if (idx.empty()) break;
             if (round >= 24) throw std::runtime_error("flat search: bound refinement did not converge");
@@ -318,17 +365,20 @@ struct FlatIndex::Impl {
             cQ.ensure((size_t)nfPad * dpad * 4); cQn.ensure((size_t)nfPad * 4);
             cTk.ensure((size_t)nf * 4); cTi.ensure((size_t)nf * 4);
             HIPC(hipMemcpyAsync(cIdx.p, idx.data(), (size_t)nf * 4, hipMemcpyHostToDevice, s));
-            HIPC(hipMemcpyAsync(cSel.p, sel.data(), (size_t)nf * 4, hipMemcpyHostToDevice, s));
             launch_gather_rows(Q, cIdx.as<int>(), nf, dpad, cQ.as<float>(), nfPad, s);
             launch_gather_f32(qn, cIdx.as<int>(), nf, cQn.as<float>(), s);
-            launch_gather_tau(tauGk.as<float>(), tauGi.as<int>(), tauKk.as<float>(), tauKi.as<int>(),
-                              cIdx.as<int>(), cSel.as<int>(), nf, cTk.as<float>(), cTi.as<int>(), s);
+            HIPC(hipMemcpyAsync(cSel.p, sel.data(), (size_t)nf * 4, hipMemcpyHostToDevice, s));
+            TauSources ts;
+            ts.key[0] = tauS2k.as<float>(); ts.id[0] = tauS2i.as<int>();
+            ts.key[1] = tauKk.as<float>();  ts.id[1] = tauKi.as<int>();
+            ts.key[2] = tauGk.as<float>();  ts.id[2] = tauGi.as<int>();
+            launch_gather_tau(ts, cIdx.as<int>(), cSel.as<int>(), nf, cTk.as<float>(), cTi.as<int>(), s);
             int64_t rps;
             int nsplit;
             splitPlan(nb, (nf + kBN - 1) / kBN, rps, nsplit);
             const int cap = std::max(2 * k, 64);
             scan(X.as<float>(), xn.as<float>(), nb, rps, nsplit, 1, cQ.as<float>(), cQn.as<float>(), nf,
-                 cTk.as<float>(), cTi.as<int>(), cap, s);
+                 cTk.as<float>(), cTi.as<int>(), cap, s, kPassRetry);
             SelectParams sp = selectParams(nf, nsplit, cap, k, k);
             sp.qmap = cIdx.as<int>();
             sp.out_ids = oIds; sp.out_vals = oVals;
@@ -338,7 +388,6 @@ struct FlatIndex::Impl {
             HIPC(hipMemcpyAsync(st.data(), status.p, (size_t)mb * 4, hipMemcpyDeviceToHost, s));
             HIPC(hipStreamSynchronize(s));
             live = idx;
-            spec = false;
         }
     }
 
@@ -414,7 +463,7 @@ FlatIndex::~FlatIndex() {
     if (d_->device >= 0) (void)hipSetDevice(d_->device);
     if (d_->stream) (void)hipStreamSynchronize(d_->stream);
     for (DevBuf* b : {&d_->X, &d_->xn, &d_->sX, &d_->sXn, &d_->sIdx, &d_->stage, &d_->qin, &d_->outIds,
-                      &d_->outVals, &d_->qbuf, &d_->qnorm, &d_->cand, &d_->cnt, &d_->tauSk, &d_->tauSi,
+                      &d_->outVals, &d_->qbuf, &d_->qnorm, &d_->cand, &d_->cnt, &d_->tauSk, &d_->tauSi, &d_->tauS2k, &d_->tauS2i, &d_->maxBits,
                       &d_->tauGk, &d_->tauGi, &d_->tauKk, &d_->tauKi, &d_->status, &d_->cQ, &d_->cQn,
                       &d_->cTk, &d_->cTi, &d_->cIdx, &d_->cSel})
         b->release();
@@ -443,6 +492,7 @@ void FlatIndex::reset() {
     d_->xn.release();
     d_->capRows = 0;
     d_->nb = 0;
+    d_->xnMax = 0.0f;
     d_->sampleNb = -1;
 }
 

@@ -100,16 +100,16 @@ __global__ void gather_f32_kernel(const float* __restrict__ src, const int* __re
     if (i < n) dst[i] = src[idx[i]];
 }
 
-// tau_out[i] = sel[i] ? b[idx[i]] : a[idx[i]]
-__global__ void gather_tau_kernel(const float* __restrict__ ka, const int* __restrict__ ia,
-                                  const float* __restrict__ kb, const int* __restrict__ ib,
-                                  const int* __restrict__ idx, const int* __restrict__ sel, int n,
-                                  float* __restrict__ ko, int* __restrict__ io) {
+// tau_out[i] = source sel[i] (0, 1 or 2) at row idx[i]
+__global__ void gather_tau_kernel(TauSources src, const int* __restrict__ idx,
+                                  const int* __restrict__ sel, int n, float* __restrict__ ko,
+                                  int* __restrict__ io) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     const int q = idx[i];
-    if (sel[i]) { ko[i] = kb[q]; io[i] = ib[q]; }
-    else        { ko[i] = ka[q]; io[i] = ia[q]; }
+    const int w = sel[i];
+    ko[i] = src.key[w][q];
+    io[i] = src.id[w][q];
 }
 
 // "No bound": (+inf, -1) admits every finite key and rejects +inf and NaN,
@@ -126,6 +126,26 @@ __global__ void fill_empty_kernel(int32_t* __restrict__ ids, float* __restrict__
         if (ids) ids[i] = -1;
         if (vals) vals[i] = empty;
     }
+}
+
+// max over the finite-or-+inf norms (NaN skipped) -> *out as float bits.
+// Norms are >= 0, so their bit patterns order like their values.
+__global__ void max_norm_kernel(const float* __restrict__ xn, int64_t n, unsigned* __restrict__ out) {
+    __shared__ float sm[256];
+    float m = 0.0f;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const float v = xn[i];
+        if (v > m) m = v;          // false for NaN
+    }
+    sm[threadIdx.x] = m;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+        if ((int)threadIdx.x < off && sm[threadIdx.x + off] > sm[threadIdx.x])
+            sm[threadIdx.x] = sm[threadIdx.x + off];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) atomicMax(out, __float_as_uint(sm[0]));
 }
 
 // ---------------------------------------------------------------------------
@@ -152,12 +172,14 @@ __global__ void fill_empty_kernel(int32_t* __restrict__ ids, float* __restrict__
 // the 8 XCDs) receives a contiguous run of (split, query block) pairs: the
 // workgroups resident on one XCD then stream the same database rows through
 // that XCD's L2.
-// SAMPLE only names the instantiation (the sample pass gets its own symbol so
-// profiles separate it from the full-database pass); the code is the same.
-template <int METRIC, int SAMPLE>
+// PASS only names the instantiation (0 = full database, 1 = row sample,
+// 2 = retry of a few queries), so profiles separate the passes; the code is
+// the same.
+template <int METRIC, int PASS>
 __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     __shared__ __attribute__((aligned(16))) float sX[2 * kBM * kLds];
     __shared__ __attribute__((aligned(16))) float sQ[2 * kBN * kLds];
+    __shared__ __attribute__((aligned(16))) float sXn[2 * kBM];   // tile row norms, by tile parity
     __shared__ int sCnt[kBN];
 
     const int nwg = gridDim.x;
@@ -177,8 +199,17 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
 
     if (tid < kBN) sCnt[tid] = 0;
 
-    // per-lane query state for the two query blocks this lane sees
-    float tk[2], qn[2];
+    // Per-lane query state for the two query blocks this lane sees.
+    // ft is the fast-reject bound, a NECESSARY condition for key <= tau:
+    //   IP: key = -dot <= tau  <=>  dot >= -tau               (exact)
+    //   L2: key <= tau  ==>  fma(-2, dot, ||x||^2) <= tau - ||q||^2 + M,
+    //       M = 2^-20 (tau + 2||q||^2 + 2 max||x||^2). Both sides of the L2 key
+    //       (||q||^2 + ||x||^2) - 2 q.x and ||x||^2 - 2 q.x round at most once
+    //       per operation, so they differ from exact arithmetic by at most
+    //       2^-24 (2||q||^2 + 3||x||^2) + 2^-23 tau; M covers that sixteen-fold
+    //       together with the rounding of tau - ||q||^2 + M itself.
+    // Only candidates passing the fast test take the exact lexicographic test.
+    float tk[2], qn[2], ft[2];
     int ti[2];
     bool qv[2];
 #pragma unroll
@@ -188,6 +219,12 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
         tk[bn] = qv[bn] ? p.tau_key[q] : 0.0f;
         ti[bn] = qv[bn] ? p.tau_id[q] : -1;
         qn[bn] = (METRIC == 0 && qv[bn]) ? p.qnorm[q] : 0.0f;
+        if (METRIC == 0) {
+            const float m = 0x1p-20f * (tk[bn] + 2.0f * qn[bn] + 2.0f * p.xnorm_max);
+            ft[bn] = qv[bn] ? (tk[bn] - qn[bn]) + m : -INFINITY;
+        } else {
+            ft[bn] = qv[bn] ? -tk[bn] : INFINITY;
+        }
     }
 
     const int64_t rows_pad = (p.nrows + kBM - 1) / kBM * kBM;
@@ -203,8 +240,10 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     const int ldCol = (tid & 7) * 4;
     const float* Xb = p.X + rowBeg * p.dpad;
     const float* Qb = p.Q + (int64_t)qb * kBN * p.dpad;
-    fx4 rx[4], rq[4];
-
+    fx4 rx[4], rq[4], rn;
+    // The first chunk of every tile also brings the tile's 128 row norms
+    // (threads 0..31, one float4 each) into sXn[tile & 1]; the epilogue of
+    // that tile reads them from LDS instead of waiting on global memory.
     auto gload = [&](int it) {
         const int tile = it / nk;
         const int kc = it - tile * nk;
@@ -216,8 +255,10 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
             rx[i] = *(const fx4*)(xs + (int64_t)row * p.dpad);
             rq[i] = *(const fx4*)(qs + (int64_t)row * p.dpad);
         }
+        if (METRIC == 0 && kc == 0 && tid < kBM / 4)
+            rn = *(const fx4*)(p.xnorm + rowBeg + (int64_t)tile * kBM + tid * 4);
     };
-    auto lstore = [&](int buf) {
+    auto lstore = [&](int it, int buf) {
         float* dx = sX + buf * (kBM * kLds);
         float* dq = sQ + buf * (kBN * kLds);
 #pragma unroll
@@ -226,6 +267,9 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
             *(fx4*)(dx + row * kLds + ldCol) = rx[i];
             *(fx4*)(dq + row * kLds + ldCol) = rq[i];
         }
+        const int tile = it / nk;
+        if (METRIC == 0 && it - tile * nk == 0 && tid < kBM / 4)
+            *(fx4*)(sXn + (tile & 1) * kBM + tid * 4) = rn;
     };
 
     fx16 acc[2][2];
@@ -238,7 +282,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
 
     if (total > 0) {
         gload(0);
-        lstore(0);
+        lstore(0, 0);
     }
     __syncthreads();
 
@@ -253,6 +297,15 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
 
         const float* sx = sX + buf * (kBM * kLds);
         const float* sq = sQ + buf * (kBN * kLds);
+        // the epilogue's row norms, read before the last chunk's MFMAs
+        fx4 xnr[2][4];
+        if (METRIC == 0 && kc == nk - 1) {
+#pragma unroll
+            for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4)
+                    xnr[bm][g4] = *(const fx4*)(sXn + (tile & 1) * kBM + wm * 64 + bm * 32 + g4 * 8 + h * 4);
+        }
 #pragma unroll
         for (int g = 0; g < kBK / 8; ++g) {
             fx4 a0 = *(const fx4*)(sx + aOff + g * 8);
@@ -278,7 +331,20 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
                     const int rl = wm * 64 + bm * 32 + g4 * 8 + h * 4;
                     const int64_t r0 = tileRow0 + rl;
                     fx4 xn4 = {0.0f, 0.0f, 0.0f, 0.0f};
-                    if (METRIC == 0) xn4 = *(const fx4*)(p.xnorm + r0);
+                    if (METRIC == 0) xn4 = xnr[bm][g4];
+                    // 8 fast tests without branches, then one wave-level branch:
+                    // a group rarely holds a survivor in any of the 64 lanes.
+                    bool f[4][2];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int bn = 0; bn < 2; ++bn) {
+                            const float dot = acc[bm][bn][g4 * 4 + i];
+                            f[i][bn] = METRIC == 0 ? fmaf(-2.0f, dot, xn4[i]) <= ft[bn] : dot >= ft[bn];
+                        }
+                    const bool any = f[0][0] | f[0][1] | f[1][0] | f[1][1] | f[2][0] | f[2][1] |
+                                     f[3][0] | f[3][1];
+                    if (!any) continue;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int64_t row = r0 + i;
@@ -286,6 +352,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
                         const int id = (int)(row * p.id_stride);
 #pragma unroll
                         for (int bn = 0; bn < 2; ++bn) {
+                            if (!f[i][bn]) continue;
                             const float dot = acc[bm][bn][g4 * 4 + i];
                             float key;
                             if (METRIC == 0) {
@@ -317,7 +384,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
                     for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
         }
 
-        if (it + 1 < total) lstore(buf ^ 1);
+        if (it + 1 < total) lstore(it + 1, buf ^ 1);
         __syncthreads();
     }
 
@@ -351,32 +418,60 @@ __device__ __forceinline__ uint64_t composite(uint2 c) {
 __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
     __shared__ uint64_t sBuf[kSelLds];
     __shared__ uint64_t sTop[kTopMax];
+    __shared__ int sOff[kMaxSplit + 1];
     __shared__ unsigned sHist[256];
     __shared__ unsigned sSel[3];
+    __shared__ int sWave[4];
     __shared__ uint64_t sT;
     __shared__ int sN;
 
     const int q = blockIdx.x;
     const int tid = threadIdx.x;
-    const int64_t qbase = (int64_t)q * p.nsplit;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int ns = p.nsplit;
+    const int64_t qbase = (int64_t)q * ns;
 
-    int c = 0;
-    bool ovf = false;
-    for (int s = 0; s < p.nsplit; ++s) {
-        const int n = p.cnt[qbase + s];
-        ovf |= n > p.cap;
-        c += n < p.cap ? n : p.cap;
-    }
-    const bool inLds = c <= kSelLds;
-    if (inLds) {
-        int base = 0;
-        for (int s = 0; s < p.nsplit; ++s) {
-            int n = p.cnt[qbase + s];
-            n = n < p.cap ? n : p.cap;
-            const uint2* src = p.cand + (qbase + s) * p.cap;
-            for (int e = tid; e < n; e += 256) sBuf[base + e] = composite(src[e]);
-            base += n;
+    // exclusive prefix of the stored (clamped) counts: sOff[s] .. sOff[s+1]
+    int carry = 0;
+    bool ovfLocal = false;
+    for (int base = 0; base < ns; base += 256) {
+        const int sidx = base + tid;
+        int v = 0;
+        if (sidx < ns) {
+            const int n = p.cnt[qbase + sidx];
+            ovfLocal |= n > p.cap;
+            v = n < p.cap ? n : p.cap;
         }
+        int x = v;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int t = __shfl_up(x, off, 64);
+            if (lane >= off) x += t;
+        }
+        if (lane == 63) sWave[wave] = x;
+        __syncthreads();
+        int wpre = 0;
+        for (int w = 0; w < wave; ++w) wpre += sWave[w];
+        if (sidx < ns) sOff[sidx + 1] = carry + wpre + x;
+        carry += sWave[0] + sWave[1] + sWave[2] + sWave[3];
+        __syncthreads();
+    }
+    if (tid == 0) sOff[0] = 0;
+    const bool ovf = __syncthreads_or(ovfLocal);
+    const int c = carry;
+    const bool inLds = c <= kSelLds;
+
+    // flat index -> candidate (binary search over the split offsets)
+    auto fetch = [&](int e) -> uint64_t {
+        int lo = 0, hi = ns;   // find s with sOff[s] <= e < sOff[s+1]
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (sOff[mid] <= e) lo = mid; else hi = mid;
+        }
+        return composite(p.cand[(qbase + lo) * p.cap + (e - sOff[lo])]);
+    };
+    if (inLds) {
+        for (int e = tid; e < c; e += 256) sBuf[e] = fetch(e);
     }
     __syncthreads();
 
@@ -384,12 +479,7 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
         if (inLds) {
             for (int e = tid; e < c; e += 256) f(sBuf[e]);
         } else {
-            for (int s = 0; s < p.nsplit; ++s) {
-                int n = p.cnt[qbase + s];
-                n = n < p.cap ? n : p.cap;
-                const uint2* src = p.cand + (qbase + s) * p.cap;
-                for (int e = tid; e < n; e += 256) f(composite(src[e]));
-            }
+            for (int e = tid; e < c; e += 256) f(fetch(e));
         }
     };
 
@@ -506,6 +596,16 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
                 p.tau_j_id[orow] = -1;
             }
         }
+        if (p.tau_j2_key) {
+            if (nsel >= p.j2) {
+                const uint64_t x = sTop[p.j2 - 1];
+                p.tau_j2_key[orow] = ord_to_key((uint32_t)(x >> 32));
+                p.tau_j2_id[orow] = (int)(uint32_t)(x & 0xFFFFFFFFu);
+            } else {
+                p.tau_j2_key[orow] = INFINITY;
+                p.tau_j2_id[orow] = -1;
+            }
+        }
         if (p.tau_k_key) {
             if (nsel >= k) {
                 const uint64_t x = sTop[k - 1];
@@ -578,12 +678,12 @@ void launch_gather_f32(const float* src, const int* idx, int n, float* dst, hipS
     check_launch("gather_f32");
 }
 
-void launch_gather_tau(const float* ka, const int* ia, const float* kb, const int* ib,
-                       const int* idx, const int* sel, int n, float* ko, int* io, hipStream_t s) {
+void launch_gather_tau(const TauSources& src, const int* idx, const int* sel, int n, float* ko,
+                       int* io, hipStream_t s) {
     if (n <= 0) return;
     void* tok;
     prof_begin(kFamPrep, s, &tok);
-    gather_tau_kernel<<<(n + 255) / 256, 256, 0, s>>>(ka, ia, kb, ib, idx, sel, n, ko, io);
+    gather_tau_kernel<<<(n + 255) / 256, 256, 0, s>>>(src, idx, sel, n, ko, io);
     prof_end(tok, s);
     check_launch("gather_tau");
 }
@@ -606,30 +706,42 @@ void launch_fill_empty(int32_t* ids, float* vals, int64_t count, float empty, hi
     check_launch("fill_empty");
 }
 
-void launch_scan_filter(const ScanParams& p, int metric, bool sample, hipStream_t s) {
+void launch_max_norm(const float* xn, int64_t n, unsigned* out, hipStream_t s) {
+    if (n <= 0) return;
+    void* tok;
+    prof_begin(kFamNorms, s, &tok);
+    max_norm_kernel<<<grid_for(n, 256) < 1024 ? grid_for(n, 256) : 1024, 256, 0, s>>>(xn, n, out);
+    prof_end(tok, s);
+    check_launch("max_norm");
+}
+
+void launch_scan_filter(const ScanParams& p, int metric, int pass, hipStream_t s) {
     const int64_t grid = (int64_t)p.nqb * p.nsplit;
     if (grid <= 0) return;
     if (grid > 0x7FFFFFFF) throw std::runtime_error("scan_filter grid too large");
     if (p.dpad % kBK != 0 || p.rows_per_split % kBM != 0 || p.cap < 1)
         throw std::runtime_error("scan_filter: bad tiling parameters");
     void* tok;
-    prof_begin(sample ? kFamScanSample : kFamScan, s, &tok);
-    if (metric == 0 && !sample)
-        scan_filter_kernel<0, 0><<<(int)grid, 256, 0, s>>>(p);
-    else if (metric == 0)
-        scan_filter_kernel<0, 1><<<(int)grid, 256, 0, s>>>(p);
-    else if (!sample)
-        scan_filter_kernel<1, 0><<<(int)grid, 256, 0, s>>>(p);
-    else
-        scan_filter_kernel<1, 1><<<(int)grid, 256, 0, s>>>(p);
+    prof_begin(pass == kPassSample ? kFamScanSample : pass == kPassRetry ? kFamScanRetry : kFamScan, s, &tok);
+    const int g = (int)grid;
+    if (metric == 0) {
+        if (pass == kPassSample) scan_filter_kernel<0, kPassSample><<<g, 256, 0, s>>>(p);
+        else if (pass == kPassRetry) scan_filter_kernel<0, kPassRetry><<<g, 256, 0, s>>>(p);
+        else scan_filter_kernel<0, kPassFull><<<g, 256, 0, s>>>(p);
+    } else {
+        if (pass == kPassSample) scan_filter_kernel<1, kPassSample><<<g, 256, 0, s>>>(p);
+        else if (pass == kPassRetry) scan_filter_kernel<1, kPassRetry><<<g, 256, 0, s>>>(p);
+        else scan_filter_kernel<1, kPassFull><<<g, 256, 0, s>>>(p);
+    }
     prof_end(tok, s);
     check_launch("scan_filter");
 }
 
 void launch_select(const SelectParams& p, hipStream_t s) {
     if (p.nq <= 0) return;
-    if (p.k < 1 || p.k > kTopMax || p.j < 1 || p.j > p.k)
+    if (p.k < 1 || p.k > kTopMax || p.j < 1 || p.j > p.k || p.j2 < 1 || p.j2 > p.k)
         throw std::runtime_error("select: bad k/j");
+    if (p.nsplit < 1 || p.nsplit > kMaxSplit) throw std::runtime_error("select: bad nsplit");
     void* tok;
     prof_begin(kFamSelect, s, &tok);
     select_kernel<<<p.nq, 256, 0, s>>>(p);

@@ -28,15 +28,18 @@ constexpr int kBN = 128;   // queries per scan tile
 constexpr int kBK = 32;    // dimension chunk staged through LDS
 constexpr int kSelLds = 4096;   // candidates a select block holds in LDS
 constexpr int kTopMax = 1024;   // largest k (== MFLAT_MAX_K)
+constexpr int kMaxSplit = 2048; // most database splits one select block indexes
 
 enum KernelFamily {
-    kFamScan = 0, kFamScanSample = 1, kFamSelect = 2, kFamArgmin = 3, kFamNorms = 4, kFamPrep = 5,
-    kFamCount = 6
+    kFamScan = 0, kFamScanSample = 1, kFamScanRetry = 2, kFamSelect = 3, kFamArgmin = 4,
+    kFamNorms = 5, kFamPrep = 6, kFamCount = 7
 };
+enum ScanPass { kPassFull = 0, kPassSample = 1, kPassRetry = 2 };
 
 struct ScanParams {
     const float* X;          // database tile source (see layout above)
     const float* xnorm;      // per-row ||x||^2 (L2 only)
+    float xnorm_max;         // >= every finite ||x||^2 of the pass (L2 fast-reject margin)
     int64_t nrows;           // valid rows; rows >= nrows are padding
     int64_t rows_per_split;  // multiple of kBM
     int nsplit;              // database splits (grid = nqb * nsplit)
@@ -61,6 +64,7 @@ struct SelectParams {
     int nq;
     int k;                   // rank to select (1..kTopMax)
     int j;                   // secondary rank for tau_j (1..k)
+    int j2;                  // secondary rank for tau_j2 (1..k)
     int metric;              // 0: value = key, otherwise value = -key
     const int* qmap;         // nullable: output row of query i
     int32_t* out_ids;        // nullable
@@ -68,6 +72,8 @@ struct SelectParams {
     int out_stride;
     float* tau_j_key;        // nullable: j-th smallest (key, id), or "no bound"
     int* tau_j_id;
+    float* tau_j2_key;       // nullable: j2-th smallest (key, id), or "no bound"
+    int* tau_j2_id;
     float* tau_k_key;        // nullable: k-th smallest (key, id), or "no bound"
     int* tau_k_id;
     int* status;             // nullable: bit0 = a region overflowed, bit1 = fewer than k stored
@@ -82,11 +88,16 @@ void launch_normalize_rows(float* v, int64_t n, int dpad, hipStream_t s);
 void launch_gather_rows(const float* src, const int* idx, int n, int dpad, float* dst,
                         int64_t n_pad, hipStream_t s);
 void launch_gather_f32(const float* src, const int* idx, int n, float* dst, hipStream_t s);
-void launch_gather_tau(const float* ka, const int* ia, const float* kb, const int* ib,
-                       const int* idx, const int* sel, int n, float* ko, int* io, hipStream_t s);
+struct TauSources {   // three per-query bound arrays a retry can draw from
+    const float* key[3];
+    const int* id[3];
+};
+void launch_gather_tau(const TauSources& src, const int* idx, const int* sel, int n, float* ko,
+                       int* io, hipStream_t s);
 void launch_fill_tau_none(float* key, int* id, int n, hipStream_t s);
 void launch_fill_empty(int32_t* ids, float* vals, int64_t count, float empty, hipStream_t s);
-void launch_scan_filter(const ScanParams& p, int metric, bool sample, hipStream_t s);
+void launch_max_norm(const float* xn, int64_t n, unsigned* out, hipStream_t s);
+void launch_scan_filter(const ScanParams& p, int metric, int pass, hipStream_t s);
 void launch_select(const SelectParams& p, hipStream_t s);
 
 // Kernel timer (profile.cpp).
