@@ -97,7 +97,22 @@ def main():
     ap.add_argument("--config", default="C2", choices=sorted(WORKLOADS))
     ap.add_argument("--nq", type=int, default=0, help="query count override (C4: 1, 16 or 64)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run 3 device-to-device copies of MIB MiB (counter calibration)")
     args = ap.parse_args()
+
+    if args.copy_probe:
+        import hipmem
+
+        n = args.copy_probe << 20
+        src = hipmem.DeviceArray((n,), "uint8")
+        dst = hipmem.DeviceArray((n,), "uint8")
+        src.fill_bytes(1)
+        for _ in range(3):
+            hipmem.check(hipmem.hip().hipMemcpy(dst.ptr, src.ptr, n, hipmem.D2D), "hipMemcpy D2D")
+        hipmem.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "copies": 3}), flush=True)
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "

@@ -25,6 +25,7 @@ namespace mflat_amd {
 typedef float fx4 __attribute__((ext_vector_type(4)));
 typedef float fx16 __attribute__((ext_vector_type(16)));
 
+constexpr int kQGroup = 16;      // query blocks co-scheduled per XCD (see scan_filter)
 constexpr int kLds = kBK + 4;   // LDS row stride in floats: 16-byte reads of 16
                                 // consecutive rows land in distinct banks
 
@@ -182,12 +183,23 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     __shared__ __attribute__((aligned(16))) float sXn[2 * kBM];   // tile row norms, by tile parity
     __shared__ int sCnt[kBN];
 
+    // Workgroup -> (query block, split). Hardware deals consecutive ids
+    // round-robin over the 8 XCDs; v renumbers them so each XCD owns a
+    // contiguous range. Within it, query blocks go in groups of kQGroup,
+    // split-major inside a group: the ~64 workgroups resident on one XCD then
+    // cover kQGroup query blocks (1 MB of Q tiles at d = 128, kept in its 4 MB
+    // L2) times a few splits, and each database tile they stream is shared by
+    // kQGroup workgroups.
     const int nwg = gridDim.x;
     const int bid = blockIdx.x;
     const int full = (nwg / 8) * 8;
     const int v = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
-    const int split = v / p.nqb;
-    const int qb = v - split * p.nqb;
+    const int grpSize = p.nqb < kQGroup ? p.nqb : kQGroup;
+    const int grp = v / (grpSize * p.nsplit);
+    const int r = v - grp * grpSize * p.nsplit;
+    const int inGrp = p.nqb - grp * grpSize < grpSize ? p.nqb - grp * grpSize : grpSize;
+    const int split = r / inGrp;
+    const int qb = grp * grpSize + (r - split * inGrp);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
