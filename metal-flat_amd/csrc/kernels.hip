@@ -17,6 +17,7 @@
 
 #include <cmath>
 #include <cstdio>
+#include <type_traits>
 #include <stdexcept>
 #include <string>
 
@@ -256,9 +257,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     // The first chunk of every tile also brings the tile's 128 row norms
     // (threads 0..31, one float4 each) into sXn[tile & 1]; the epilogue of
     // that tile reads them from LDS instead of waiting on global memory.
-    auto gload = [&](int it) {
-        const int tile = it / nk;
-        const int kc = it - tile * nk;
+    auto gload = [&](int tile, int kc) {
         const float* xs = Xb + ((int64_t)tile * kBM) * p.dpad + kc * kBK + ldCol;
         const float* qs = Qb + kc * kBK + ldCol;
 #pragma unroll
@@ -270,7 +269,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
         if (METRIC == 0 && kc == 0 && tid < kBM / 4)
             rn = *(const fx4*)(p.xnorm + rowBeg + (int64_t)tile * kBM + tid * 4);
     };
-    auto lstore = [&](int it, int buf) {
+    auto lstore = [&](int tile, int kc, int buf) {
         float* dx = sX + buf * (kBM * kLds);
         float* dq = sQ + buf * (kBN * kLds);
 #pragma unroll
@@ -279,33 +278,28 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
             *(fx4*)(dx + row * kLds + ldCol) = rx[i];
             *(fx4*)(dq + row * kLds + ldCol) = rq[i];
         }
-        const int tile = it / nk;
-        if (METRIC == 0 && it - tile * nk == 0 && tid < kBM / 4)
+        if (METRIC == 0 && kc == 0 && tid < kBM / 4)
             *(fx4*)(sXn + (tile & 1) * kBM + tid * 4) = rn;
     };
 
     fx16 acc[2][2];
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
 
     if (total > 0) {
-        gload(0);
-        lstore(0, 0);
+        gload(0, 0);
+        lstore(0, 0, 0);
     }
     __syncthreads();
 
     const int aOff = (wm * 64 + r32) * kLds + h * 4;
     const int bOff = (wn * 64 + r32) * kLds + h * 4;
 
+    int tile = 0, kc = 0;   // position of chunk `it`, advanced without division
     for (int it = 0; it < total; ++it) {
         const int buf = it & 1;
-        const int tile = it / nk;
-        const int kc = it - tile * nk;
-        if (it + 1 < total) gload(it + 1);
+        const bool lastK = kc == nk - 1;
+        const int ntile = lastK ? tile + 1 : tile;
+        const int nkc = lastK ? 0 : kc + 1;
+        if (it + 1 < total) gload(ntile, nkc);
 
         const float* sx = sX + buf * (kBM * kLds);
         const float* sq = sQ + buf * (kBN * kLds);
@@ -318,20 +312,38 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
                 for (int g4 = 0; g4 < 4; ++g4)
                     xnr[bm][g4] = *(const fx4*)(sXn + (tile & 1) * kBM + wm * 64 + bm * 32 + g4 * 8 + h * 4);
         }
+        // A tile's first chunk starts every accumulator from an inline zero C
+        // operand, so no accumulator is ever cleared with moves.
+        auto mma = [&](auto zeroTag) {
+            constexpr bool ZERO = decltype(zeroTag)::value;
+            const fx16 z = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f,
+                            0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int g = 0; g < kBK / 8; ++g) {
-            fx4 a0 = *(const fx4*)(sx + aOff + g * 8);
-            fx4 a1 = *(const fx4*)(sx + aOff + 32 * kLds + g * 8);
-            fx4 b0 = *(const fx4*)(sq + bOff + g * 8);
-            fx4 b1 = *(const fx4*)(sq + bOff + 32 * kLds + g * 8);
+            for (int g = 0; g < kBK / 8; ++g) {
+                fx4 a0 = *(const fx4*)(sx + aOff + g * 8);
+                fx4 a1 = *(const fx4*)(sx + aOff + 32 * kLds + g * 8);
+                fx4 b0 = *(const fx4*)(sq + bOff + g * 8);
+                fx4 b1 = *(const fx4*)(sq + bOff + 32 * kLds + g * 8);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], b0[j], acc[0][0], 0, 0, 0);
-                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], b1[j], acc[0][1], 0, 0, 0);
-                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[j], b0[j], acc[1][0], 0, 0, 0);
-                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[j], b1[j], acc[1][1], 0, 0, 0);
+                for (int j = 0; j < 4; ++j) {
+                    if (ZERO && g == 0 && j == 0) {
+                        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], b0[j], z, 0, 0, 0);
+                        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], b1[j], z, 0, 0, 0);
+                        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[j], b0[j], z, 0, 0, 0);
+                        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[j], b1[j], z, 0, 0, 0);
+                    } else {
+                        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], b0[j], acc[0][0], 0, 0, 0);
+                        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], b1[j], acc[0][1], 0, 0, 0);
+                        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[j], b0[j], acc[1][0], 0, 0, 0);
+                        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[j], b1[j], acc[1][1], 0, 0, 0);
+                    }
+                }
             }
-        }
+        };
+        if (kc == 0)
+            mma(std::true_type{});
+        else
+            mma(std::false_type{});
 
         if (kc == nk - 1) {
             // epilogue: keys, threshold test, append survivors
@@ -388,16 +400,12 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
                     }
                 }
             }
-#pragma unroll
-            for (int a = 0; a < 2; ++a)
-#pragma unroll
-                for (int b = 0; b < 2; ++b)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
         }
 
-        if (it + 1 < total) lstore(it + 1, buf ^ 1);
+        if (it + 1 < total) lstore(ntile, nkc, buf ^ 1);
         __syncthreads();
+        tile = ntile;
+        kc = nkc;
     }
 
     __syncthreads();
