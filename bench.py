@@ -35,6 +35,11 @@ for p in (os.path.join(ROOT, "metal-flat_amd"), os.path.join(ROOT, "oracle")):
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 
+# HBM bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE + WRITE_SIZE
+# runs scaled by a plain-copy calibration (profiles/scan_filter_c2.md). Reported as
+# roofline.traffic for the configuration it was measured on; null otherwise.
+MEASURED_TRAFFIC_BYTES = {"C2": 5.69e9}
+
 WORKLOADS = {
     "C1": ("C1: flat L2, nb=100,000 x d=128 integer-valued U{0..255}, nq=1,000, k=10, seed 0", 0, 10),
     "C2": ("C2: flat L2, nb=1,000,000 x d=128 GMM(1024 centres, sigma 0.3), nq=10,000, k=100, seed 1", 0, 100),
@@ -180,7 +185,8 @@ def main():
         mean_s = scan["total_ms"] / scan["launches"] / 1000.0
         ach = flop / mean_s / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None}
+                "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4),
+                "traffic": MEASURED_TRAFFIC_BYTES.get(args.config) if args.nq == 0 else None}
 
     out = {
         "metric": "QPS + % of MFMA/HBM roofline, flat L2 d=128 nb=1M k=100 (1 GPU)",
