@@ -56,7 +56,8 @@ void hipCheck(hipError_t e, const char* what) {
 }
 #define HIPC(x) hipCheck((x), #x)
 
-constexpr int64_t kTargetWG = 2048;             // scan workgroups wanted per launch
+constexpr int64_t kTargetWG = 2048;             // scan_filter workgroups wanted per launch
+constexpr int64_t kTargetWGSmall = 4096;        // scan_small workgroups (HBM streaming)
 constexpr size_t kCandBudget = size_t(1536) << 20;  // candidate workspace per batch
 constexpr size_t kStageBytes = size_t(256) << 20;   // host->device staging chunk
 
@@ -92,9 +93,17 @@ int chooseJ(int k, double lambda, double tail) {
     return k;
 }
 
-void splitPlan(int64_t nrows, int nqb, int64_t& rowsPerSplit, int& nsplit) {
+// nq: queries of the launch (small batches go to scan_small, which streams the
+// database and wants many more, smaller workgroups).
+void splitPlan(int64_t nrows, int nq, int dpad, int64_t& rowsPerSplit, int& nsplit) {
+    const int nqb = (nq + kBN - 1) / kBN;
     const int64_t ntiles = std::max<int64_t>(1, (nrows + kBM - 1) / kBM);
-    int64_t want = std::max<int64_t>(1, (kTargetWG + nqb - 1) / nqb);
+    const int64_t target = small_scan_fits(nq, dpad) ? kTargetWGSmall : kTargetWG;
+    int64_t want = std::max<int64_t>(1, (target + nqb - 1) / nqb);
+    // keep a split's bytes addressable with 32-bit offsets
+    const int64_t maxTiles = std::max<int64_t>(1, ((int64_t)1 << 31) / ((int64_t)kBM * dpad * 4) - 1);
+    want = std::max(want, (ntiles + maxTiles - 1) / maxTiles);
+    want = std::min<int64_t>(want, kMaxSplit);
     want = std::min(want, ntiles);
     const int64_t tps = (ntiles + want - 1) / want;
     nsplit = (int)((ntiles + tps - 1) / tps);
@@ -157,13 +166,15 @@ struct FlatIndex::Impl {
 
     Plan plan(int64_t mb, int k) const {
         Plan pl;
-        const int nqb = (int)((mb + kBN - 1) / kBN);
         int64_t r = (int64_t)std::ceil(std::sqrt(16.0 * (double)nb));
+        // Small batches stream the database once whatever the bound; a sample of
+        // at most kSelLds rows keeps its per-query select inside LDS.
+        if (mb <= kSmallMaxQ) r = std::min<int64_t>(r, kSelLds);
         r = std::max<int64_t>(r, std::max<int64_t>(4LL * k, 256));
         r = roundUp(r, kBM);
         if (nb <= 2 * r) {
             pl.direct = true;
-            splitPlan(nb, nqb, pl.rps1, pl.nsplit1);
+            splitPlan(nb, (int)mb, dpad, pl.rps1, pl.nsplit1);
             pl.cap1 = (int)pl.rps1;
             pl.perQuery = (size_t)pl.nsplit1 * pl.cap1;
             return pl;
@@ -178,9 +189,9 @@ struct FlatIndex::Impl {
         // time per query block of kBN); ~1% misses balances the two.
         pl.j = chooseJ(k, lambda, 0.01);
         pl.j2 = chooseJ(k, lambda, 1e-9);
-        splitPlan(r, nqb, pl.rps0, pl.nsplit0);
+        splitPlan(r, (int)mb, dpad, pl.rps0, pl.nsplit0);
         pl.cap0 = (int)pl.rps0;
-        splitPlan(nb, nqb, pl.rps1, pl.nsplit1);
+        splitPlan(nb, (int)mb, dpad, pl.rps1, pl.nsplit1);
         const double e1 = (double)pl.j * (double)nb / (double)r;   // expected survivors
         const int64_t perSplit = (int64_t)(2.0 * e1 / pl.nsplit1) + 64;
         pl.cap1 = std::max<int>({2 * k, 64, pow2ceil(perSplit)});
@@ -199,7 +210,9 @@ struct FlatIndex::Impl {
         HIPC(hipMemsetAsync(nx, 0, (size_t)newCap * dpad * sizeof(float), s));
         HIPC(hipMemsetAsync(nn, 0, (size_t)newCap * sizeof(float), s));
         if (nb > 0) {
-            HIPC(hipMemcpyAsync(nx, X.p, (size_t)nb * dpad * sizeof(float), hipMemcpyDeviceToDevice, s));
+            // whole 32-row blocks: the chunked layout interleaves a block's rows
+            HIPC(hipMemcpyAsync(nx, X.p, (size_t)roundUp(nb, 32) * dpad * sizeof(float),
+                                hipMemcpyDeviceToDevice, s));
             HIPC(hipMemcpyAsync(nn, xn.p, (size_t)nb * sizeof(float), hipMemcpyDeviceToDevice, s));
         }
         HIPC(hipStreamSynchronize(s));
@@ -216,20 +229,20 @@ struct FlatIndex::Impl {
         if (!ready) { nb += n; return; }
         setDevice();
         growRows(roundUp(nb + n, kBM), s);
-        float* dst = X.as<float>() + nb * dpad;
-        if (dim == dpad) {
-            HIPC(hipMemcpyAsync(dst, src, (size_t)n * dim * sizeof(float), kind, s));
-        } else {
-            const int64_t chunk = std::max<int64_t>(1, (int64_t)(kStageBytes / (sizeof(float) * dim)));
-            for (int64_t r0 = 0; r0 < n; r0 += chunk) {
-                const int64_t rn = std::min<int64_t>(chunk, n - r0);
+        // rows go to the chunked database layout (kernels.hpp, blk_off)
+        const int64_t chunk = std::max<int64_t>(1, (int64_t)(kStageBytes / (sizeof(float) * dim)));
+        for (int64_t r0 = 0; r0 < n; r0 += chunk) {
+            const int64_t rn = std::min<int64_t>(chunk, n - r0);
+            const float* from = src + r0 * dim;
+            if (kind != hipMemcpyDeviceToDevice) {
                 stage.ensure((size_t)rn * dim * sizeof(float));
-                HIPC(hipMemcpyAsync(stage.p, src + r0 * dim, (size_t)rn * dim * sizeof(float), kind, s));
-                launch_pack_rows(stage.as<float>(), rn, dim, dst + r0 * dpad, rn, dpad, s);
+                HIPC(hipMemcpyAsync(stage.p, from, (size_t)rn * dim * sizeof(float), kind, s));
+                from = stage.as<float>();
             }
+            launch_store_rows_blk(from, rn, dim, X.as<float>(), nb + r0, dpad, s);
         }
-        if (metric == Metric::Cosine) launch_normalize_rows(dst, n, dpad, s);
-        launch_row_norms(dst, n, dpad, xn.as<float>() + nb, s);
+        if (metric == Metric::Cosine) launch_normalize_rows_blk(X.as<float>(), nb, n, dpad, s);
+        launch_row_norms_blk(X.as<float>(), nb, n, dpad, xn.as<float>() + nb, s);
         maxBits.ensure(sizeof(unsigned));
         HIPC(hipMemsetAsync(maxBits.p, 0, sizeof(unsigned), s));
         launch_max_norm(xn.as<float>() + nb, n, maxBits.as<unsigned>(), s);
@@ -248,7 +261,7 @@ struct FlatIndex::Impl {
         sX.ensure((size_t)pl.R0 * dpad * sizeof(float));
         sXn.ensure((size_t)pl.R0 * sizeof(float));
         HIPC(hipMemcpyAsync(sIdx.p, idx.data(), idx.size() * sizeof(int), hipMemcpyHostToDevice, s));
-        launch_gather_rows(X.as<float>(), sIdx.as<int>(), (int)pl.R0, dpad, sX.as<float>(), pl.R0, s);
+        launch_gather_rows_blk(X.as<float>(), sIdx.as<int>(), (int)pl.R0, dpad, sX.as<float>(), s);
         launch_gather_f32(xn.as<float>(), sIdx.as<int>(), (int)pl.R0, sXn.as<float>(), s);
         HIPC(hipStreamSynchronize(s));
         sampleNb = nb;
@@ -375,7 +388,7 @@ struct FlatIndex::Impl {
             launch_gather_tau(ts, cIdx.as<int>(), cSel.as<int>(), nf, cTk.as<float>(), cTi.as<int>(), s);
             int64_t rps;
             int nsplit;
-            splitPlan(nb, (nf + kBN - 1) / kBN, rps, nsplit);
+            splitPlan(nb, nf, dpad, rps, nsplit);
             const int cap = std::max(2 * k, 64);
             scan(X.as<float>(), xn.as<float>(), nb, rps, nsplit, 1, cQ.as<float>(), cQn.as<float>(), nf,
                  cTk.as<float>(), cTi.as<int>(), cap, s, kPassRetry);

@@ -85,6 +85,69 @@ __global__ void normalize_rows_kernel(float* __restrict__ v, int64_t n, int dpad
     }
 }
 
+// Database (chunked layout) helpers; see blk_off.
+__global__ void store_rows_blk_kernel(const float* __restrict__ src, int64_t n, int dim,
+                                      float* __restrict__ X, int64_t row0, int dpad) {
+    const int c4n = dpad / 4;
+    const int64_t total = n * c4n;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / c4n;
+        const int c = (int)(i - r * c4n) * 4;
+        fx4 v;
+        for (int j = 0; j < 4; ++j) v[j] = c + j < dim ? src[r * dim + c + j] : 0.0f;
+        *(fx4*)(X + blk_off(row0 + r, c, dpad)) = v;
+    }
+}
+
+// Sequential double sum over the row in column order (reference rowSqNorms).
+__global__ void row_norms_blk_kernel(const float* __restrict__ X, int64_t row0, int64_t n, int dpad,
+                                     float* __restrict__ out) {
+    const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (r >= n) return;
+    double s = 0.0;
+    for (int c = 0; c < dpad; c += 4) {
+        const fx4 x = *(const fx4*)(X + blk_off(row0 + r, c, dpad));
+        s += (double)x.x * x.x;
+        s += (double)x.y * x.y;
+        s += (double)x.z * x.z;
+        s += (double)x.w * x.w;
+    }
+    out[r] = (float)s;
+}
+
+__global__ void normalize_rows_blk_kernel(float* __restrict__ X, int64_t row0, int64_t n, int dpad) {
+    const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (r >= n) return;
+    double s = 0.0;
+    for (int c = 0; c < dpad; c += 4) {
+        const fx4 x = *(const fx4*)(X + blk_off(row0 + r, c, dpad));
+        for (int j = 0; j < 4; ++j) s += (double)x[j] * x[j];
+    }
+    if (s > 0.0) {
+        const float inv = (float)(1.0 / sqrt(s));
+        for (int c = 0; c < dpad; c += 4) {
+            fx4* px = (fx4*)(X + blk_off(row0 + r, c, dpad));
+            fx4 x = *px;
+            for (int j = 0; j < 4; ++j) x[j] *= inv;
+            *px = x;
+        }
+    }
+}
+
+// dst row r (chunked) = X row idx[r] (chunked), r < n
+__global__ void gather_rows_blk_kernel(const float* __restrict__ X, const int* __restrict__ idx, int n,
+                                       int dpad, float* __restrict__ dst) {
+    const int c4n = dpad / 4;
+    const int64_t total = (int64_t)n * c4n;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / c4n;
+        const int c = (int)(i - r * c4n) * 4;
+        *(fx4*)(dst + blk_off(r, c, dpad)) = *(const fx4*)(X + blk_off(idx[r], c, dpad));
+    }
+}
+
 __global__ void gather_rows_kernel(const float* __restrict__ src, const int* __restrict__ idx,
                                    int n, int dpad, float* __restrict__ dst, int64_t n_pad) {
     const int64_t total = n_pad * dpad;
@@ -257,14 +320,18 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     // The first chunk of every tile also brings the tile's 128 row norms
     // (threads 0..31, one float4 each) into sXn[tile & 1]; the epilogue of
     // that tile reads them from LDS instead of waiting on global memory.
+    // Database chunks are linear 4 KB pieces (one per 32-row block, chunked
+    // layout): thread t takes float4 t of each piece, i.e. row
+    // 32 i + 16 (t >> 7) + (t & 15), columns 8 ((t >> 4) & 3) + 4 ((t >> 6) & 1) .. +3.
+    const int xRow = 16 * (tid >> 7) + (tid & 15);
+    const int xCol = 8 * ((tid >> 4) & 3) + 4 * ((tid >> 6) & 1);
     auto gload = [&](int tile, int kc) {
-        const float* xs = Xb + ((int64_t)tile * kBM) * p.dpad + kc * kBK + ldCol;
+        const float* xs = Xb + ((int64_t)tile * kBM) * p.dpad + kc * 1024 + tid * 4;
         const float* qs = Qb + kc * kBK + ldCol;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int row = ldRow + 32 * i;
-            rx[i] = *(const fx4*)(xs + (int64_t)row * p.dpad);
-            rq[i] = *(const fx4*)(qs + (int64_t)row * p.dpad);
+            rx[i] = *(const fx4*)(xs + (int64_t)i * 32 * p.dpad);
+            rq[i] = *(const fx4*)(qs + (int64_t)(ldRow + 32 * i) * p.dpad);
         }
         if (METRIC == 0 && kc == 0 && tid < kBM / 4)
             rn = *(const fx4*)(p.xnorm + rowBeg + (int64_t)tile * kBM + tid * 4);
@@ -274,9 +341,8 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
         float* dq = sQ + buf * (kBN * kLds);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int row = ldRow + 32 * i;
-            *(fx4*)(dx + row * kLds + ldCol) = rx[i];
-            *(fx4*)(dq + row * kLds + ldCol) = rq[i];
+            *(fx4*)(dx + (32 * i + xRow) * kLds + xCol) = rx[i];
+            *(fx4*)(dq + (ldRow + 32 * i) * kLds + ldCol) = rq[i];
         }
         if (METRIC == 0 && kc == 0 && tid < kBM / 4)
             *(fx4*)(sXn + (tile & 1) * kBM + tid * 4) = rn;
@@ -416,6 +482,215 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// scan_small: the same filter for small batches (nq <= 64), HBM-streaming
+// ---------------------------------------------------------------------------
+//
+// With few queries every database byte is used by at most 64 queries, so the
+// pass is bound by reading the database once from HBM, not by MFMA. The
+// database rows go straight from global memory into the A operand of
+// v_mfma_f32_16x16x4_f32 (no LDS staging: each row is used by one wave only);
+// the queries, NQB blocks of 16, sit in LDS as the B operand. Output layout:
+// lane l holds query l%16 of the block and rows 4*(l/16) .. +3, so the
+// epilogue keeps the per-query bound in a register as in scan_filter.
+// K is consumed 16 columns at a time: lane quarter q = l/16 reads the float4 at
+// columns 16t + 4q .. +3 of its row and MFMA step j pairs columns
+// 16t + 4q + j across the quarters -- the same permutation on both operands.
+// One workgroup per split.
+// G > 0: dpad == 32 G, and a whole 32-row block is buffered in registers
+// (the next block's step t is fetched as soon as step t of the current block is
+// consumed), which keeps ~G KB per wave in flight. G == 0: any dpad, one step
+// of prefetch.
+template <int METRIC, int NQB, int PASS, int G>
+__global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
+    extern __shared__ __attribute__((aligned(16))) float sQs[];   // [16*NQB][dpad + 4]
+    __shared__ int sCnt[16 * NQB];
+
+    const int split = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int r16 = lane & 15;
+    const int quarter = lane >> 4;
+    const int ldq = p.dpad + 4;
+
+    for (int i = tid; i < 16 * NQB * (p.dpad / 4); i += 256) {
+        const int row = i / (p.dpad / 4);
+        const int c4 = i - row * (p.dpad / 4);
+        *(fx4*)(sQs + row * ldq + c4 * 4) = *(const fx4*)(p.Q + (int64_t)row * p.dpad + c4 * 4);
+    }
+    if (tid < 16 * NQB) sCnt[tid] = 0;
+
+    float tk[NQB], qn[NQB], ft[NQB];
+    int ti[NQB];
+    bool qv[NQB];
+#pragma unroll
+    for (int bq = 0; bq < NQB; ++bq) {
+        const int q = bq * 16 + r16;
+        qv[bq] = q < p.nq;
+        tk[bq] = qv[bq] ? p.tau_key[q] : 0.0f;
+        ti[bq] = qv[bq] ? p.tau_id[q] : -1;
+        qn[bq] = (METRIC == 0 && qv[bq]) ? p.qnorm[q] : 0.0f;
+        if (METRIC == 0) {
+            const float m = 0x1p-20f * (tk[bq] + 2.0f * qn[bq] + 2.0f * p.xnorm_max);
+            ft[bq] = qv[bq] ? (tk[bq] - qn[bq]) + m : -INFINITY;
+        } else {
+            ft[bq] = qv[bq] ? -tk[bq] : INFINITY;
+        }
+    }
+    __syncthreads();
+
+    const int64_t rows_pad = (p.nrows + kBM - 1) / kBM * kBM;
+    const int64_t rowBeg = (int64_t)split * p.rows_per_split;
+    int64_t rowEnd = rowBeg + p.rows_per_split;
+    if (rowEnd > rows_pad) rowEnd = rows_pad;
+    // Each wave takes 32-row blocks (two 16-row MFMA sets) round-robin. In the
+    // chunked layout, the operand float4 e of row half hh for 32-column step t
+    // is one linear 1 KB load per wave: lane l reads float4 l of sub-chunk
+    // (hh, e), i.e. row 16 hh + (l & 15), columns 32 t + 8 (l >> 4) + 4 e .. +3,
+    // and MFMA j of the step pairs columns 32 t + 8 q + j over quarters q.
+    // Rows are read exactly once: non-temporal loads keep them from displacing
+    // the query tile and the candidate lines in the caches.
+    const int nblk = rowEnd > rowBeg ? (int)((rowEnd - rowBeg) / 32) : 0;
+    const int g32 = p.dpad / 32;
+    const int64_t blkStride = (int64_t)32 * p.dpad;
+    const float* xw = p.X + rowBeg * p.dpad + lane * 4;
+    const float* qrow8 = sQs + r16 * ldq + quarter * 8;
+    auto ld = [&](int b, int t, int hh, int e) -> fx4 {
+        return __builtin_nontemporal_load((const fx4*)(xw + b * blkStride + t * 1024 + (hh * 2 + e) * 256));
+    };
+
+    constexpr int GB = G > 0 ? G : 1;
+    fx4 buf[2][GB][2];   // G > 0: the wave's whole current block [row half][step][e]
+    fx4 cur[2][2];       // G == 0: the current step
+    if (wave < nblk) {
+        if constexpr (G > 0) {
+#pragma unroll
+            for (int t = 0; t < GB; ++t)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) buf[hh][t][e] = ld(wave, t, hh, e);
+        } else {
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int e = 0; e < 2; ++e) cur[hh][e] = ld(wave, 0, hh, e);
+        }
+    }
+    for (int b = wave; b < nblk; b += 4) {
+        // The block's row norms are loaded BEFORE the next block's prefetch:
+        // vector-memory loads complete in order, so waiting for norms loaded
+        // after the prefetch would wait for the whole prefetch too.
+        fx4 xnh[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+        if (METRIC == 0) {
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+                xnh[hh] = *(const fx4*)(p.xnorm + rowBeg + (int64_t)b * 32 + hh * 16 + quarter * 4);
+        }
+        fx4 acc[2][NQB];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int bq = 0; bq < NQB; ++bq) acc[hh][bq] = fx4{0.0f, 0.0f, 0.0f, 0.0f};
+        auto step = [&](const fx4 (&x)[2][2], int t) {
+#pragma unroll
+            for (int bq = 0; bq < NQB; ++bq) {
+                const float* qp = qrow8 + bq * 16 * ldq + t * 32;
+                const fx4 bv0 = *(const fx4*)qp;
+                const fx4 bv1 = *(const fx4*)(qp + 4);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float bj = j < 4 ? bv0[j & 3] : bv1[j & 3];
+                    acc[0][bq] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[0][j >> 2][j & 3], bj, acc[0][bq], 0, 0, 0);
+                    acc[1][bq] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[1][j >> 2][j & 3], bj, acc[1][bq], 0, 0, 0);
+                }
+            }
+        };
+        const bool hasNext = b + 4 < nblk;
+        if constexpr (G > 0) {
+#pragma unroll
+            for (int t = 0; t < GB; ++t) {
+                fx4 x[2][2];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) x[hh][e] = buf[hh][t][e];
+                if (hasNext) {
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                        for (int e = 0; e < 2; ++e) buf[hh][t][e] = ld(b + 4, t, hh, e);
+                }
+                step(x, t);
+            }
+        } else {
+            for (int t = 0; t < g32; ++t) {
+                const bool lastT = t + 1 == g32;
+                const int nbk = lastT ? b + 4 : b;
+                const int nt = lastT ? 0 : t + 1;
+                fx4 nx[2][2];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) nx[hh][e] = cur[hh][e];
+                if (nbk < nblk) {
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                        for (int e = 0; e < 2; ++e) nx[hh][e] = ld(nbk, nt, hh, e);
+                }
+                step(cur, t);
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) cur[hh][e] = nx[hh][e];
+            }
+        }
+
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int64_t r0 = rowBeg + (int64_t)b * 32 + hh * 16 + quarter * 4;
+            const fx4 xn4 = xnh[hh];
+#pragma unroll
+            for (int bq = 0; bq < NQB; ++bq) {
+                bool f[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    f[i] = METRIC == 0 ? fmaf(-2.0f, acc[hh][bq][i], xn4[i]) <= ft[bq]
+                                       : acc[hh][bq][i] >= ft[bq];
+                if (!(f[0] | f[1] | f[2] | f[3])) continue;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (!f[i]) continue;
+                    const int64_t row = r0 + i;
+                    const int id = (int)(row * p.id_stride);
+                    const float dot = acc[hh][bq][i];
+                    float key;
+                    if (METRIC == 0) {
+                        const float tt = fmaf(-2.0f, dot, qn[bq] + xn4[i]);
+                        key = (tt < 0.0f ? 0.0f : tt) + 0.0f;
+                    } else {
+                        key = -dot + 0.0f;
+                    }
+                    const bool pass = row < p.nrows && qv[bq] &&
+                                      (key < tk[bq] || (key == tk[bq] && id <= ti[bq]));
+                    if (pass) {
+                        const int ql = bq * 16 + r16;
+                        const int slot = atomicAdd(&sCnt[ql], 1);
+                        if (slot < p.cap)
+                            p.cand[((int64_t)ql * p.nsplit + split) * p.cap + slot] =
+                                make_uint2(__float_as_uint(key), (unsigned)id);
+                    }
+                }
+            }
+        }
+    }
+
+    __syncthreads();
+    if (tid < 16 * NQB && tid < p.nq) p.cnt[(int64_t)tid * p.nsplit + split] = sCnt[tid];
+}
+
+// ---------------------------------------------------------------------------
 // select: exact per-query top-k of the candidate regions
 // ---------------------------------------------------------------------------
 
@@ -438,7 +713,7 @@ __device__ __forceinline__ uint64_t composite(uint2 c) {
 __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
     __shared__ uint64_t sBuf[kSelLds];
     __shared__ uint64_t sTop[kTopMax];
-    __shared__ int sOff[kMaxSplit + 1];
+    extern __shared__ int sOff[];   // nsplit + 1 entries (dynamic)
     __shared__ unsigned sHist[256];
     __shared__ unsigned sSel[3];
     __shared__ int sWave[4];
@@ -679,6 +954,43 @@ void launch_normalize_rows(float* v, int64_t n, int dpad, hipStream_t s) {
     check_launch("normalize_rows");
 }
 
+void launch_store_rows_blk(const float* src, int64_t n, int dim, float* X, int64_t row0, int dpad,
+                           hipStream_t s) {
+    if (n <= 0) return;
+    void* tok;
+    prof_begin(kFamPrep, s, &tok);
+    store_rows_blk_kernel<<<grid_for(n * dpad / 4, 256), 256, 0, s>>>(src, n, dim, X, row0, dpad);
+    prof_end(tok, s);
+    check_launch("store_rows_blk");
+}
+
+void launch_row_norms_blk(const float* X, int64_t row0, int64_t n, int dpad, float* out, hipStream_t s) {
+    if (n <= 0) return;
+    void* tok;
+    prof_begin(kFamNorms, s, &tok);
+    row_norms_blk_kernel<<<(int)((n + 255) / 256), 256, 0, s>>>(X, row0, n, dpad, out);
+    prof_end(tok, s);
+    check_launch("row_norms_blk");
+}
+
+void launch_normalize_rows_blk(float* X, int64_t row0, int64_t n, int dpad, hipStream_t s) {
+    if (n <= 0) return;
+    void* tok;
+    prof_begin(kFamNorms, s, &tok);
+    normalize_rows_blk_kernel<<<(int)((n + 255) / 256), 256, 0, s>>>(X, row0, n, dpad);
+    prof_end(tok, s);
+    check_launch("normalize_rows_blk");
+}
+
+void launch_gather_rows_blk(const float* X, const int* idx, int n, int dpad, float* dst, hipStream_t s) {
+    if (n <= 0) return;
+    void* tok;
+    prof_begin(kFamPrep, s, &tok);
+    gather_rows_blk_kernel<<<grid_for((int64_t)n * dpad / 4, 256), 256, 0, s>>>(X, idx, n, dpad, dst);
+    prof_end(tok, s);
+    check_launch("gather_rows_blk");
+}
+
 void launch_gather_rows(const float* src, const int* idx, int n, int dpad, float* dst,
                         int64_t n_pad, hipStream_t s) {
     if (n_pad <= 0) return;
@@ -735,7 +1047,46 @@ void launch_max_norm(const float* xn, int64_t n, unsigned* out, hipStream_t s) {
     check_launch("max_norm");
 }
 
+template <int M, int NQB, int G>
+static void launch_small_g(const ScanParams& p, int pass, int g, size_t lds, hipStream_t s) {
+    if (pass == kPassSample) scan_small_kernel<M, NQB, kPassSample, G><<<g, 256, lds, s>>>(p);
+    else if (pass == kPassRetry) scan_small_kernel<M, NQB, kPassRetry, G><<<g, 256, lds, s>>>(p);
+    else scan_small_kernel<M, NQB, kPassFull, G><<<g, 256, lds, s>>>(p);
+}
+template <int M, int NQB>
+static void launch_small(const ScanParams& p, int pass, int g, size_t lds, hipStream_t s) {
+    if (p.dpad == 96) launch_small_g<M, NQB, 3>(p, pass, g, lds, s);
+    else if (p.dpad == 128) launch_small_g<M, NQB, 4>(p, pass, g, lds, s);
+    else launch_small_g<M, NQB, 0>(p, pass, g, lds, s);
+}
+
+bool small_scan_fits(int nq, int dpad) {
+    const int nqb16 = nq <= 16 ? 1 : nq <= 32 ? 2 : 4;
+    return nq >= 1 && nq <= kSmallMaxQ && (size_t)16 * nqb16 * (dpad + 4) * 4 <= kSmallMaxLds;
+}
+
 void launch_scan_filter(const ScanParams& p, int metric, int pass, hipStream_t s) {
+    if (small_scan_fits(p.nq, p.dpad)) {
+        if (p.nsplit <= 0) return;
+        if (p.rows_per_split % kBM != 0 || p.cap < 1)
+            throw std::runtime_error("scan_small: bad tiling parameters");
+        const int nqb16 = p.nq <= 16 ? 1 : p.nq <= 32 ? 2 : 4;
+        const size_t lds = (size_t)16 * nqb16 * (p.dpad + 4) * sizeof(float);
+        void* tok;
+        prof_begin(pass == kPassSample ? kFamScanSample : pass == kPassRetry ? kFamScanRetry : kFamScan, s, &tok);
+        if (metric == 0) {
+            if (nqb16 == 1) launch_small<0, 1>(p, pass, p.nsplit, lds, s);
+            else if (nqb16 == 2) launch_small<0, 2>(p, pass, p.nsplit, lds, s);
+            else launch_small<0, 4>(p, pass, p.nsplit, lds, s);
+        } else {
+            if (nqb16 == 1) launch_small<1, 1>(p, pass, p.nsplit, lds, s);
+            else if (nqb16 == 2) launch_small<1, 2>(p, pass, p.nsplit, lds, s);
+            else launch_small<1, 4>(p, pass, p.nsplit, lds, s);
+        }
+        prof_end(tok, s);
+        check_launch("scan_small");
+        return;
+    }
     const int64_t grid = (int64_t)p.nqb * p.nsplit;
     if (grid <= 0) return;
     if (grid > 0x7FFFFFFF) throw std::runtime_error("scan_filter grid too large");
@@ -764,7 +1115,7 @@ void launch_select(const SelectParams& p, hipStream_t s) {
     if (p.nsplit < 1 || p.nsplit > kMaxSplit) throw std::runtime_error("select: bad nsplit");
     void* tok;
     prof_begin(kFamSelect, s, &tok);
-    select_kernel<<<p.nq, 256, 0, s>>>(p);
+    select_kernel<<<p.nq, 256, (size_t)(p.nsplit + 1) * sizeof(int), s>>>(p);
     prof_end(tok, s);
     check_launch("select");
 }

@@ -1,12 +1,19 @@
 // SPDX-License-Identifier: Apache-2.0
 // kernels.hpp -- device kernels of the flat-search hot path and their launchers.
 //
-// Data layout in HBM (all fp32, row-major):
-//   database  X[rows_pad][dpad]   rows_pad = roundup(nb, kBM), dpad = roundup(dim, kBK);
-//                                 pad rows and pad columns are zero
+// Data layout in HBM (all fp32):
+//   database  X, rows_pad = roundup(nb, kBM) rows of dpad = roundup(dim, kBK) columns,
+//             in 32 x 32 chunks ordered the way MFMA lanes consume them
+//             (blk_off below): a 32-row block occupies 32*dpad floats like a
+//             row-major block would, so row offsets of blocks are unchanged, but
+//             inside it each 4 KB chunk (32 rows x 32 columns) is laid out as
+//             [row half hh][float4 e][quarter q][row r16][4], i.e. element
+//             (row 16 hh + r16, column 8 q + 4 e + c). Lane q*16 + r16 of a wave
+//             then reads its operand float4 with one linear 1 KB load per
+//             (hh, e). Pad rows and pad columns are zero.
 //   row norms xn[rows_pad]        ||x||^2, double-accumulated (reference
 //                                 src/Distance.h:40-47), pad entries zero
-//   queries   Q[nqb*kBN][dpad]    same padding rules, qn[] likewise
+//   queries   Q[nqb*kBN][dpad]    row-major, zero padded, qn[] likewise
 //   candidates cand[nq][nsplit][cap] of (key bits, id), cnt[nq][nsplit]
 //
 // Ranking key (smaller = nearer), the value the reference's merge kernel ranks
@@ -28,13 +35,24 @@ constexpr int kBN = 128;   // queries per scan tile
 constexpr int kBK = 32;    // dimension chunk staged through LDS
 constexpr int kSelLds = 4096;   // candidates a select block holds in LDS
 constexpr int kTopMax = 1024;   // largest k (== MFLAT_MAX_K)
-constexpr int kMaxSplit = 2048; // most database splits one select block indexes
+constexpr int kMaxSplit = 16384;  // most database splits one select block indexes
+constexpr int kSmallMaxQ = 64;                 // scan_small serves batches up to this size
+constexpr size_t kSmallMaxLds = 64 * 1024;     // ... whose query tile fits this much LDS
 
 enum KernelFamily {
     kFamScan = 0, kFamScanSample = 1, kFamScanRetry = 2, kFamSelect = 3, kFamArgmin = 4,
     kFamNorms = 5, kFamPrep = 6, kFamCount = 7
 };
 enum ScanPass { kPassFull = 0, kPassSample = 1, kPassRetry = 2 };
+
+// Float offset of element (row, col) of the database in the chunked layout.
+__host__ __device__ inline int64_t blk_off(int64_t row, int col, int dpad) {
+    const int64_t b = row >> 5;
+    const int rr = (int)(row & 31);
+    const int t = col >> 5, cc = col & 31;
+    return ((b * (dpad >> 5) + t) << 10) +
+           ((((rr >> 4) * 2 + ((cc >> 2) & 1)) * 64 + (cc >> 3) * 16 + (rr & 15)) << 2) + (cc & 3);
+}
 
 struct ScanParams {
     const float* X;          // database tile source (see layout above)
@@ -81,10 +99,17 @@ struct SelectParams {
 
 // Launchers (kernels.hip). All are asynchronous on `s` and bracket the launch
 // with the process-wide kernel timer when it is enabled.
+// row-major (queries)
 void launch_pack_rows(const float* src, int64_t n, int dim, float* dst, int64_t n_pad, int dpad,
                       hipStream_t s);
 void launch_row_norms(const float* v, int64_t n, int dpad, float* out, hipStream_t s);
 void launch_normalize_rows(float* v, int64_t n, int dpad, hipStream_t s);
+// chunked database layout: rows [row0, row0 + n) of X
+void launch_store_rows_blk(const float* src, int64_t n, int dim, float* X, int64_t row0, int dpad,
+                           hipStream_t s);
+void launch_row_norms_blk(const float* X, int64_t row0, int64_t n, int dpad, float* out, hipStream_t s);
+void launch_normalize_rows_blk(float* X, int64_t row0, int64_t n, int dpad, hipStream_t s);
+void launch_gather_rows_blk(const float* X, const int* idx, int n, int dpad, float* dst, hipStream_t s);
 void launch_gather_rows(const float* src, const int* idx, int n, int dpad, float* dst,
                         int64_t n_pad, hipStream_t s);
 void launch_gather_f32(const float* src, const int* idx, int n, float* dst, hipStream_t s);
@@ -97,6 +122,9 @@ void launch_gather_tau(const TauSources& src, const int* idx, const int* sel, in
 void launch_fill_tau_none(float* key, int* id, int n, hipStream_t s);
 void launch_fill_empty(int32_t* ids, float* vals, int64_t count, float empty, hipStream_t s);
 void launch_max_norm(const float* xn, int64_t n, unsigned* out, hipStream_t s);
+// Dispatches to scan_small (small batches, HBM-streaming) when small_scan_fits,
+// else to the MFMA-tiled scan_filter.
+bool small_scan_fits(int nq, int dpad);
 void launch_scan_filter(const ScanParams& p, int metric, int pass, hipStream_t s);
 void launch_select(const SelectParams& p, hipStream_t s);
 
