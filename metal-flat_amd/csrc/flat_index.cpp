@@ -156,6 +156,7 @@ struct FlatIndex::Impl {
     DevBuf qbuf, qnorm, cand, cnt;
     DevBuf tauSk, tauSi, tauS2k, tauS2i, tauGk, tauGi, tauKk, tauKi, status;
     DevBuf cQ, cQn, cTk, cTi, cIdx, cSel;
+    DevBuf best;
 
     int kernMetric() const { return metric == Metric::L2 ? 0 : 1; }
     float emptyValue() const { return metric == Metric::L2 ? INFINITY : -INFINITY; }
@@ -164,8 +165,15 @@ struct FlatIndex::Impl {
         if (device >= 0) HIPC(hipSetDevice(device));
     }
 
+    // k = 1 on a batch too large for scan_small: one fused argmin pass.
+    bool argminPath(int64_t mb, int k) const { return k == 1 && !small_scan_fits((int)std::min<int64_t>(mb, 1 << 30), dpad); }
+
     Plan plan(int64_t mb, int k) const {
         Plan pl;
+        if (argminPath(mb, k)) {
+            pl.perQuery = 1;
+            return pl;
+        }
         int64_t r = (int64_t)std::ceil(std::sqrt(16.0 * (double)nb));
         // Small batches stream the database once whatever the bound; a sample of
         // at most kSelLds rows keeps its per-query select inside LDS.
@@ -298,6 +306,21 @@ struct FlatIndex::Impl {
     void searchBatch(int mb, int k, const Plan& pl, int32_t* oIds, float* oVals, hipStream_t s) {
         const float* Q = qbuf.as<float>();
         const float* qn = qnorm.as<float>();
+        if (argminPath(mb, k)) {
+            best.ensure((size_t)mb * sizeof(unsigned long long));
+            launch_fill_u64(best.as<unsigned long long>(), mb, ~0ull, s);
+            ScanParams p;
+            std::memset(&p, 0, sizeof p);
+            p.X = X.as<float>(); p.xnorm = xn.as<float>(); p.xnorm_max = xnMax; p.nrows = nb;
+            splitPlan(nb, mb, dpad, p.rows_per_split, p.nsplit);
+            p.id_stride = 1;
+            p.Q = Q; p.qnorm = qn; p.nq = mb; p.nqb = (mb + kBN - 1) / kBN; p.dpad = dpad;
+            p.cap = 1;
+            p.best = best.as<unsigned long long>();
+            launch_scan_filter(p, kernMetric(), kPassArgmin, s);
+            launch_argmin_finalize(best.as<unsigned long long>(), mb, kernMetric(), oIds, oVals, s);
+            return;
+        }
         tauSk.ensure((size_t)mb * 4); tauSi.ensure((size_t)mb * 4);
         tauS2k.ensure((size_t)mb * 4); tauS2i.ensure((size_t)mb * 4);
         tauGk.ensure((size_t)mb * 4); tauGi.ensure((size_t)mb * 4);
@@ -478,7 +501,7 @@ FlatIndex::~FlatIndex() {
     for (DevBuf* b : {&d_->X, &d_->xn, &d_->sX, &d_->sXn, &d_->sIdx, &d_->stage, &d_->qin, &d_->outIds,
                       &d_->outVals, &d_->qbuf, &d_->qnorm, &d_->cand, &d_->cnt, &d_->tauSk, &d_->tauSi, &d_->tauS2k, &d_->tauS2i, &d_->maxBits,
                       &d_->tauGk, &d_->tauGi, &d_->tauKk, &d_->tauKi, &d_->status, &d_->cQ, &d_->cQn,
-                      &d_->cTk, &d_->cTi, &d_->cIdx, &d_->cSel})
+                      &d_->cTk, &d_->cTi, &d_->cIdx, &d_->cSel, &d_->best})
         b->release();
     if (d_->stream) (void)hipStreamDestroy(d_->stream);
 }

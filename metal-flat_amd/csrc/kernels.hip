@@ -30,6 +30,19 @@ constexpr int kQGroup = 16;      // query blocks co-scheduled per XCD (see scan_
 constexpr int kLds = kBK + 4;   // LDS row stride in floats: 16-byte reads of 16
                                 // consecutive rows land in distinct banks
 
+// Order-preserving map of a float key to uint32 (ascending float order ==
+// ascending unsigned order); NaN never reaches here (the filter rejects it).
+__device__ __forceinline__ uint32_t key_to_ord(uint32_t bits) {
+    return (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+}
+__device__ __forceinline__ float ord_to_key(uint32_t o) {
+    const uint32_t bits = (o & 0x80000000u) ? (o ^ 0x80000000u) : ~o;
+    return __uint_as_float(bits);
+}
+__device__ __forceinline__ uint64_t composite(uint2 c) {
+    return ((uint64_t)key_to_ord(c.x) << 32) | (uint64_t)c.y;
+}
+
 static void check_launch(const char* what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
@@ -246,6 +259,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     __shared__ __attribute__((aligned(16))) float sQ[2 * kBN * kLds];
     __shared__ __attribute__((aligned(16))) float sXn[2 * kBM];   // tile row norms, by tile parity
     __shared__ int sCnt[kBN];
+    __shared__ unsigned long long sBest[kBN];   // argmin: per-query (ordered key, id)
 
     // Workgroup -> (query block, split). Hardware deals consecutive ids
     // round-robin over the 8 XCDs; v renumbers them so each XCD owns a
@@ -273,7 +287,10 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     const int r32 = lane & 31;
     const int h = lane >> 5;
 
-    if (tid < kBN) sCnt[tid] = 0;
+    if (tid < kBN) {
+        sCnt[tid] = 0;
+        sBest[tid] = ~0ull;
+    }
 
     // Per-lane query state for the two query blocks this lane sees.
     // ft is the fast-reject bound, a NECESSARY condition for key <= tau:
@@ -292,8 +309,13 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     for (int bn = 0; bn < 2; ++bn) {
         const int q = qb * kBN + wn * 64 + bn * 32 + r32;
         qv[bn] = q < p.nq;
-        tk[bn] = qv[bn] ? p.tau_key[q] : 0.0f;
-        ti[bn] = qv[bn] ? p.tau_id[q] : -1;
+        if (PASS == kPassArgmin) {   // running best of this lane, from "no bound"
+            tk[bn] = INFINITY;
+            ti[bn] = -1;
+        } else {
+            tk[bn] = qv[bn] ? p.tau_key[q] : 0.0f;
+            ti[bn] = qv[bn] ? p.tau_id[q] : -1;
+        }
         qn[bn] = (METRIC == 0 && qv[bn]) ? p.qnorm[q] : 0.0f;
         if (METRIC == 0) {
             const float m = 0x1p-20f * (tk[bn] + 2.0f * qn[bn] + 2.0f * p.xnorm_max);
@@ -451,6 +473,17 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
                             } else {
                                 key = -dot + 0.0f;
                             }
+                            if (PASS == kPassArgmin) {
+                                // k = 1: keep the lexicographically smallest (key, id)
+                                if (rv && qv[bn] && (key < tk[bn] || (key == tk[bn] && id < ti[bn]))) {
+                                    tk[bn] = key;
+                                    ti[bn] = id;
+                                    ft[bn] = METRIC == 0
+                                        ? (key - qn[bn]) + 0x1p-20f * (key + 2.0f * qn[bn] + 2.0f * p.xnorm_max)
+                                        : -key;
+                                }
+                                continue;
+                            }
                             const bool pass = rv && qv[bn] &&
                                               (key < tk[bn] || (key == tk[bn] && id <= ti[bn]));
                             if (pass) {
@@ -474,6 +507,20 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
         kc = nkc;
     }
 
+    if (PASS == kPassArgmin) {
+        // the 4 lanes that saw each query -> LDS -> one global atomic per query
+#pragma unroll
+        for (int bn = 0; bn < 2; ++bn)
+            if (ti[bn] >= 0)
+                atomicMin(&sBest[wn * 64 + bn * 32 + r32],
+                          ((unsigned long long)key_to_ord(__float_as_uint(tk[bn])) << 32) | (unsigned)ti[bn]);
+        __syncthreads();
+        if (tid < kBN) {
+            const int q = qb * kBN + tid;
+            if (q < p.nq && sBest[tid] != ~0ull) atomicMin(&p.best[q], sBest[tid]);
+        }
+        return;
+    }
     __syncthreads();
     if (tid < kBN) {
         const int q = qb * kBN + tid;
@@ -694,19 +741,6 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
 // select: exact per-query top-k of the candidate regions
 // ---------------------------------------------------------------------------
 
-// Order-preserving map of a float key to uint32 (ascending float order ==
-// ascending unsigned order); NaN never reaches here (the filter rejects it).
-__device__ __forceinline__ uint32_t key_to_ord(uint32_t bits) {
-    return (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
-}
-__device__ __forceinline__ float ord_to_key(uint32_t o) {
-    const uint32_t bits = (o & 0x80000000u) ? (o ^ 0x80000000u) : ~o;
-    return __uint_as_float(bits);
-}
-__device__ __forceinline__ uint64_t composite(uint2 c) {
-    return ((uint64_t)key_to_ord(c.x) << 32) | (uint64_t)c.y;
-}
-
 // One workgroup (256 threads) per query. The (key, id) composites are distinct
 // (an id appears at most once per query), so the k-th smallest composite T is
 // unique and the winners are exactly the composites <= T.
@@ -915,6 +949,28 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
     }
 }
 
+// k = 1 results: packed (ordered key, id) -> id, reported value; all-ones = empty.
+__global__ void argmin_finalize_kernel(const unsigned long long* __restrict__ best, int nq, int metric,
+                                       int32_t* __restrict__ ids, float* __restrict__ vals) {
+    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= nq) return;
+    const unsigned long long x = best[q];
+    int32_t id = -1;
+    float val = metric == 0 ? INFINITY : -INFINITY;
+    if (x != ~0ull) {
+        id = (int32_t)(uint32_t)(x & 0xFFFFFFFFull);
+        const float key = ord_to_key((uint32_t)(x >> 32));
+        val = metric == 0 ? key : -key;
+    }
+    if (ids) ids[q] = id;
+    if (vals) vals[q] = val;
+}
+
+__global__ void fill_u64_kernel(unsigned long long* __restrict__ p, int64_t n, unsigned long long v) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
@@ -1066,7 +1122,7 @@ bool small_scan_fits(int nq, int dpad) {
 }
 
 void launch_scan_filter(const ScanParams& p, int metric, int pass, hipStream_t s) {
-    if (small_scan_fits(p.nq, p.dpad)) {
+    if (pass != kPassArgmin && small_scan_fits(p.nq, p.dpad)) {
         if (p.nsplit <= 0) return;
         if (p.rows_per_split % kBM != 0 || p.cap < 1)
             throw std::runtime_error("scan_small: bad tiling parameters");
@@ -1093,19 +1149,41 @@ void launch_scan_filter(const ScanParams& p, int metric, int pass, hipStream_t s
     if (p.dpad % kBK != 0 || p.rows_per_split % kBM != 0 || p.cap < 1)
         throw std::runtime_error("scan_filter: bad tiling parameters");
     void* tok;
-    prof_begin(pass == kPassSample ? kFamScanSample : pass == kPassRetry ? kFamScanRetry : kFamScan, s, &tok);
+    prof_begin(pass == kPassSample ? kFamScanSample : pass == kPassRetry ? kFamScanRetry
+               : pass == kPassArgmin ? kFamArgmin : kFamScan, s, &tok);
     const int g = (int)grid;
     if (metric == 0) {
         if (pass == kPassSample) scan_filter_kernel<0, kPassSample><<<g, 256, 0, s>>>(p);
         else if (pass == kPassRetry) scan_filter_kernel<0, kPassRetry><<<g, 256, 0, s>>>(p);
+        else if (pass == kPassArgmin) scan_filter_kernel<0, kPassArgmin><<<g, 256, 0, s>>>(p);
         else scan_filter_kernel<0, kPassFull><<<g, 256, 0, s>>>(p);
     } else {
         if (pass == kPassSample) scan_filter_kernel<1, kPassSample><<<g, 256, 0, s>>>(p);
         else if (pass == kPassRetry) scan_filter_kernel<1, kPassRetry><<<g, 256, 0, s>>>(p);
+        else if (pass == kPassArgmin) scan_filter_kernel<1, kPassArgmin><<<g, 256, 0, s>>>(p);
         else scan_filter_kernel<1, kPassFull><<<g, 256, 0, s>>>(p);
     }
     prof_end(tok, s);
     check_launch("scan_filter");
+}
+
+void launch_argmin_finalize(const unsigned long long* best, int nq, int metric, int32_t* ids, float* vals,
+                            hipStream_t s) {
+    if (nq <= 0) return;
+    void* tok;
+    prof_begin(kFamPrep, s, &tok);
+    argmin_finalize_kernel<<<(nq + 255) / 256, 256, 0, s>>>(best, nq, metric, ids, vals);
+    prof_end(tok, s);
+    check_launch("argmin_finalize");
+}
+
+void launch_fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hipStream_t s) {
+    if (n <= 0) return;
+    void* tok;
+    prof_begin(kFamPrep, s, &tok);
+    fill_u64_kernel<<<grid_for(n, 256), 256, 0, s>>>(p, n, v);
+    prof_end(tok, s);
+    check_launch("fill_u64");
 }
 
 void launch_select(const SelectParams& p, hipStream_t s) {

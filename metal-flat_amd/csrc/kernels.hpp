@@ -43,7 +43,10 @@ enum KernelFamily {
     kFamScan = 0, kFamScanSample = 1, kFamScanRetry = 2, kFamSelect = 3, kFamArgmin = 4,
     kFamNorms = 5, kFamPrep = 6, kFamCount = 7
 };
-enum ScanPass { kPassFull = 0, kPassSample = 1, kPassRetry = 2 };
+// kPassArgmin: k = 1; each query's best (key, id) goes to ScanParams::best
+// (packed ordered key << 32 | id, combined with 64-bit atomicMin) instead of
+// candidate regions, and the bound is each lane's running best.
+enum ScanPass { kPassFull = 0, kPassSample = 1, kPassRetry = 2, kPassArgmin = 3 };
 
 // Float offset of element (row, col) of the database in the chunked layout.
 __host__ __device__ inline int64_t blk_off(int64_t row, int col, int dpad) {
@@ -72,6 +75,7 @@ struct ScanParams {
     uint2* cand;             // candidate regions
     int* cnt;                // per (query, split) candidate counts (may exceed cap)
     int cap;                 // entries per (query, split) region
+    unsigned long long* best;  // kPassArgmin: per-query packed best, pre-filled with all ones
 };
 
 struct SelectParams {
@@ -127,6 +131,9 @@ void launch_max_norm(const float* xn, int64_t n, unsigned* out, hipStream_t s);
 bool small_scan_fits(int nq, int dpad);
 void launch_scan_filter(const ScanParams& p, int metric, int pass, hipStream_t s);
 void launch_select(const SelectParams& p, hipStream_t s);
+void launch_argmin_finalize(const unsigned long long* best, int nq, int metric, int32_t* ids, float* vals,
+                            hipStream_t s);
+void launch_fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hipStream_t s);
 
 // Kernel timer (profile.cpp).
 void prof_begin(int fam, hipStream_t s, void** token);
