@@ -1,7 +1,7 @@
 # SPDX-License-Identifier: Apache-2.0
 """Flat-search benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2] [--nq N]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2] [--nq N] [--storage f32]
 
 A step is one exact search of the configuration's whole query batch against the
 whole database, with queries, database and outputs already resident in HBM (the
@@ -10,10 +10,16 @@ not what `value` measures). Default workload: BASELINE.json configs[1] (C2):
 L2, nb = 1,000,000 x d = 128 GMM(1,024 centres, sigma 0.3), nq = 10,000, k = 100,
 seed 1. Prints ONE JSON line on stdout; progress goes to stderr.
 
-roofline: the dominant kernel is scan_filter (fused fp32 MFMA distance tile +
+roofline: the dominant kernel is scan_filter (fused MFMA distance tile +
 threshold filter over the full database, one launch per step). achieved =
 2 * nq * nb * d algorithmic FLOP per launch / its mean duration, timed with HIP
-events on the launch stream over the timed steps.
+events on the launch stream over the timed steps, against the dense MFMA peak
+of the storage type (fp32 157.3, fp16/bf16 2516.6 TFLOP/s); for HBM-bound
+small batches (C4, nq <= 16) the algorithmic bytes (database in its storage
+type + queries + results) per launch against 8 TB/s.
+
+--storage f16 / bf16 runs the reduced-precision variant (database and queries
+rounded to that type, fp32 accumulation; mflat_flat_create_ex).
 
 cpu_baseline: the oracle's restatement of the reference CPU path (cpuSearch,
 src/FlatIndex.mm:259-290; serial, as the reference) timed on a bounded prefix of
@@ -33,6 +39,7 @@ for p in (os.path.join(ROOT, "metal-flat_amd"), os.path.join(ROOT, "oracle")):
         sys.path.insert(0, p)
 
 PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_F16_MFMA_TFLOPS = 2516.6   # dense fp16 / bf16
 PEAK_HBM_GBS = 8000.0
 
 # HBM bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE + WRITE_SIZE
@@ -69,10 +76,14 @@ def make_data(cfg, nq_override):
     raise SystemExit(f"unknown config {cfg}")
 
 
-def cpu_baseline(x, q, k, metric, gpu_ids, seconds_target=12.0):
-    """Times the oracle (one core) on a prefix of the queries sized to ~10-15 s."""
+def cpu_baseline(x, q, k, metric, gpu_ids, storage=0, seconds_target=12.0):
+    """Times the oracle (one core) on a prefix of the queries sized to ~10-15 s.
+    Reduced-precision storage: the oracle runs on the identically rounded inputs."""
     import numpy as np
     import oracle
+
+    if storage:
+        x, q, metric = oracle.storage_inputs(x, q[:4096], metric, storage)
 
     nb, d = x.shape
     # per-query cost ~ nb*d sequential fp32 steps; calibrate on one query
@@ -101,6 +112,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", default="C2", choices=sorted(WORKLOADS))
     ap.add_argument("--nq", type=int, default=0, help="query count override (C4: 1, 16 or 64)")
+    ap.add_argument("--storage", default="f32", choices=["f32", "f16", "bf16"],
+                    help="element type of the stored database and the queries")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 3 device-to-device copies of MIB MiB (counter calibration)")
@@ -139,7 +152,9 @@ def main():
     nq = q.shape[0]
     log(f"[bench] {args.config}: nb={nb} d={d} nq={nq} k={k} data in {time.perf_counter() - t0:.1f}s")
 
-    idx = mflat.FlatIndex(d, metric)
+    storage = mflat.STORAGE_NAMES[args.storage]
+    esize = 4 if storage == mflat.MFLAT_STORAGE_F32 else 2
+    idx = mflat.FlatIndex(d, metric, storage)
     if not idx.ready():
         raise SystemExit("no usable gfx950 device")
     t0 = time.perf_counter()
@@ -181,15 +196,16 @@ def main():
     # larger than the candidate workspace, e.g. C5).
     scan_s = scan["total_ms"] / 1000.0
     if args.config == "C4" and nq <= 16:
-        byts = (nb * d * 4 + nq * d * 4 + nq * k * 8) * args.steps
+        byts = (nb * d * esize + nq * d * esize + nq * k * 8) * args.steps
         ach = byts / scan_s / 1e9
         roof = {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None}
     else:
         ach = flop * args.steps / scan_s / 1e12
-        roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4),
-                "traffic": MEASURED_TRAFFIC_BYTES.get(args.config) if args.nq == 0 else None}
+        peak = PEAK_FP32_MFMA_TFLOPS if esize == 4 else PEAK_F16_MFMA_TFLOPS
+        roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
+                "frac": round(ach / peak, 4),
+                "traffic": MEASURED_TRAFFIC_BYTES.get(args.config) if args.nq == 0 and esize == 4 else None}
 
     out = {
         "metric": "QPS + % of MFMA/HBM roofline, flat L2 d=128 nb=1M k=100 (1 GPU)",
@@ -202,16 +218,18 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": {"f32": "fp32", "f16": "fp16 storage, fp32 accumulate",
+                  "bf16": "bf16 storage, fp32 accumulate"}[args.storage],
         "data": "synthetic",
         "config": {"workload": name.replace("{nq}", str(nq)), "nb": nb, "d": d, "nq": nq, "k": k,
-                   "metric": "L2" if metric == 0 else "IP", "parallelism": "single GPU"},
+                   "metric": "L2" if metric == 0 else "IP", "storage": args.storage,
+                   "parallelism": "single GPU"},
         "roofline": roof,
         "kernels": kern,
     }
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline ...")
-        out["cpu_baseline"] = cpu_baseline(x, q, k, metric, gpu_ids)
+        out["cpu_baseline"] = cpu_baseline(x, q, k, metric, gpu_ids, storage)
         log("[bench] cpu baseline done")
     idx.close()
     print(json.dumps(out), flush=True)

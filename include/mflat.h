@@ -21,8 +21,9 @@
  *    src/FlatIndex.mm:317-321).
  *  - The IVF / IVF-PQ entry points (reference c/include/mflat.h:92-129) are
  *    not part of this library.
- *  - Additive entry points (device-pointer search/add, kernel timing) follow
- *    the flat block; they have no counterpart in the reference.
+ *  - Additive entry points (reduced-precision storage, device-pointer
+ *    search/add, kernel timing) follow the flat block; they have no
+ *    counterpart in the reference.
  */
 #ifndef MFLAT_H
 #define MFLAT_H
@@ -103,6 +104,28 @@ MFLAT_API mflat_status_t mflat_flat_reset(mflat_flat_index_t*);
    *out_k_used = 0. queries: m*dim floats in host memory. */
 MFLAT_API mflat_status_t mflat_flat_search(mflat_flat_index_t*, const float* queries,
         int m, int k, int32_t* out_ids, float* out_distances, int* out_k_used);
+
+/* ---------------- Additive: reduced-precision storage --------------------- */
+/* No counterpart in the reference (its FlatIndex stores fp32 only,
+   src/FlatIndex.mm:236-245). The index holds its database, and each search
+   its queries, in the chosen element type: the caller's fp32 values are
+   rounded to nearest even (after the Cosine normalisation, in fp32), dots
+   accumulate in fp32 on the fp16/bf16 matrix cores, norms are double sums of
+   the rounded values. Results are those of exact fp32 search on the rounded
+   inputs (up to fp32 accumulation order); values beyond the type's range
+   become +-inf and such rows or queries are never returned. Half the HBM of
+   fp32. Every other entry point behaves as for an fp32 index. */
+typedef enum {
+    MFLAT_STORAGE_F32  = 0,
+    MFLAT_STORAGE_F16  = 1,   /* IEEE binary16 */
+    MFLAT_STORAGE_BF16 = 2    /* bfloat16 */
+} mflat_storage_t;
+
+/* As mflat_flat_create; an unknown storage value -> NULL + MFLAT_ERR_BAD_ARG. */
+MFLAT_API mflat_flat_index_t*
+mflat_flat_create_ex(int dim, mflat_metric_t metric, mflat_storage_t storage, mflat_status_t* out_status);
+/* storage type of the index (MFLAT_STORAGE_F32 for NULL) */
+MFLAT_API mflat_storage_t mflat_flat_storage(const mflat_flat_index_t*);
 
 /* ---------------- Additive: device-resident data ------------------------- */
 /* No counterpart in the reference (its buffers are unified memory,

@@ -95,13 +95,14 @@ int chooseJ(int k, double lambda, double tail) {
 
 // nq: queries of the launch (small batches go to scan_small, which streams the
 // database and wants many more, smaller workgroups).
-void splitPlan(int64_t nrows, int nq, int dpad, int64_t& rowsPerSplit, int& nsplit) {
+void splitPlan(int64_t nrows, int nq, int dpad, int storage, int64_t& rowsPerSplit, int& nsplit) {
     const int nqb = (nq + kBN - 1) / kBN;
     const int64_t ntiles = std::max<int64_t>(1, (nrows + kBM - 1) / kBM);
-    const int64_t target = small_scan_fits(nq, dpad) ? kTargetWGSmall : kTargetWG;
+    const int64_t target = small_scan_fits(nq, dpad, storage) ? kTargetWGSmall : kTargetWG;
     int64_t want = std::max<int64_t>(1, (target + nqb - 1) / nqb);
     // keep a split's bytes addressable with 32-bit offsets
-    const int64_t maxTiles = std::max<int64_t>(1, ((int64_t)1 << 31) / ((int64_t)kBM * dpad * 4) - 1);
+    const int64_t maxTiles =
+        std::max<int64_t>(1, ((int64_t)1 << 31) / ((int64_t)kBM * dpad * elem_bytes(storage)) - 1);
     want = std::max(want, (ntiles + maxTiles - 1) / maxTiles);
     want = std::min<int64_t>(want, kMaxSplit);
     want = std::min(want, ntiles);
@@ -134,6 +135,8 @@ struct Plan {
 struct FlatIndex::Impl {
     int dim = 0, dpad = 0;
     Metric metric = Metric::L2;
+    int storage = kF32;   // element type of the database and of the queries
+    int esize = 4;
     int device = -1;
     bool ready = false;
     bool warnedK = false;
@@ -152,8 +155,8 @@ struct FlatIndex::Impl {
     DevBuf sX, sXn, sIdx;
 
     // per-search workspace
-    DevBuf stage, qin, outIds, outVals;
-    DevBuf qbuf, qnorm, cand, cnt;
+    DevBuf stage, inv, qin, outIds, outVals;
+    DevBuf qbuf, qh, qnorm, cand, cnt;
     DevBuf tauSk, tauSi, tauS2k, tauS2i, tauGk, tauGi, tauKk, tauKi, status;
     DevBuf cQ, cQn, cTk, cTi, cIdx, cSel;
     DevBuf best;
@@ -166,7 +169,9 @@ struct FlatIndex::Impl {
     }
 
     // k = 1 on a batch too large for scan_small: one fused argmin pass.
-    bool argminPath(int64_t mb, int k) const { return k == 1 && !small_scan_fits((int)std::min<int64_t>(mb, 1 << 30), dpad); }
+    bool argminPath(int64_t mb, int k) const {
+        return k == 1 && !small_scan_fits((int)std::min<int64_t>(mb, 1 << 30), dpad, storage);
+    }
 
     Plan plan(int64_t mb, int k) const {
         Plan pl;
@@ -182,7 +187,7 @@ struct FlatIndex::Impl {
         r = roundUp(r, kBM);
         if (nb <= 2 * r) {
             pl.direct = true;
-            splitPlan(nb, (int)mb, dpad, pl.rps1, pl.nsplit1);
+            splitPlan(nb, (int)mb, dpad, storage, pl.rps1, pl.nsplit1);
             pl.cap1 = (int)pl.rps1;
             pl.perQuery = (size_t)pl.nsplit1 * pl.cap1;
             return pl;
@@ -197,9 +202,9 @@ struct FlatIndex::Impl {
         // time per query block of kBN); ~1% misses balances the two.
         pl.j = chooseJ(k, lambda, 0.01);
         pl.j2 = chooseJ(k, lambda, 1e-9);
-        splitPlan(r, (int)mb, dpad, pl.rps0, pl.nsplit0);
+        splitPlan(r, (int)mb, dpad, storage, pl.rps0, pl.nsplit0);
         pl.cap0 = (int)pl.rps0;
-        splitPlan(nb, (int)mb, dpad, pl.rps1, pl.nsplit1);
+        splitPlan(nb, (int)mb, dpad, storage, pl.rps1, pl.nsplit1);
         const double e1 = (double)pl.j * (double)nb / (double)r;   // expected survivors
         const int64_t perSplit = (int64_t)(2.0 * e1 / pl.nsplit1) + 64;
         pl.cap1 = std::max<int>({2 * k, 64, pow2ceil(perSplit)});
@@ -212,21 +217,21 @@ struct FlatIndex::Impl {
         const int64_t newCap = std::max(need, roundUp(capRows + capRows / 2, kBM));
         void* nx = nullptr;
         void* nn = nullptr;
-        HIPC(hipMalloc(&nx, (size_t)newCap * dpad * sizeof(float)));
+        HIPC(hipMalloc(&nx, (size_t)newCap * dpad * esize));
         hipError_t e = hipMalloc(&nn, (size_t)newCap * sizeof(float));
         if (e != hipSuccess) { (void)hipFree(nx); hipCheck(e, "hipMalloc(norms)"); }
-        HIPC(hipMemsetAsync(nx, 0, (size_t)newCap * dpad * sizeof(float), s));
+        HIPC(hipMemsetAsync(nx, 0, (size_t)newCap * dpad * esize, s));
         HIPC(hipMemsetAsync(nn, 0, (size_t)newCap * sizeof(float), s));
         if (nb > 0) {
             // whole 32-row blocks: the chunked layout interleaves a block's rows
-            HIPC(hipMemcpyAsync(nx, X.p, (size_t)roundUp(nb, 32) * dpad * sizeof(float),
+            HIPC(hipMemcpyAsync(nx, X.p, (size_t)roundUp(nb, 32) * dpad * esize,
                                 hipMemcpyDeviceToDevice, s));
             HIPC(hipMemcpyAsync(nn, xn.p, (size_t)nb * sizeof(float), hipMemcpyDeviceToDevice, s));
         }
         HIPC(hipStreamSynchronize(s));
         X.release();
         xn.release();
-        X.p = nx; X.bytes = (size_t)newCap * dpad * sizeof(float);
+        X.p = nx; X.bytes = (size_t)newCap * dpad * esize;
         xn.p = nn; xn.bytes = (size_t)newCap * sizeof(float);
         capRows = newCap;
     }
@@ -237,7 +242,9 @@ struct FlatIndex::Impl {
         if (!ready) { nb += n; return; }
         setDevice();
         growRows(roundUp(nb + n, kBM), s);
-        // rows go to the chunked database layout (kernels.hpp, blk_off)
+        // rows go to the chunked database layout (kernels.hpp, blk_off), Cosine
+        // rows normalised in fp32 (reference src/FlatIndex.mm:241-242) and then
+        // rounded to the storage type
         const int64_t chunk = std::max<int64_t>(1, (int64_t)(kStageBytes / (sizeof(float) * dim)));
         for (int64_t r0 = 0; r0 < n; r0 += chunk) {
             const int64_t rn = std::min<int64_t>(chunk, n - r0);
@@ -247,10 +254,15 @@ struct FlatIndex::Impl {
                 HIPC(hipMemcpyAsync(stage.p, from, (size_t)rn * dim * sizeof(float), kind, s));
                 from = stage.as<float>();
             }
-            launch_store_rows_blk(from, rn, dim, X.as<float>(), nb + r0, dpad, s);
+            const float* scale = nullptr;
+            if (metric == Metric::Cosine) {
+                inv.ensure((size_t)rn * sizeof(float));
+                launch_row_inv_norms(from, rn, dim, inv.as<float>(), s);
+                scale = inv.as<float>();
+            }
+            launch_store_rows_blk(from, rn, dim, scale, X.p, nb + r0, dpad, storage, s);
         }
-        if (metric == Metric::Cosine) launch_normalize_rows_blk(X.as<float>(), nb, n, dpad, s);
-        launch_row_norms_blk(X.as<float>(), nb, n, dpad, xn.as<float>() + nb, s);
+        launch_row_norms_blk(X.p, nb, n, dpad, storage, xn.as<float>() + nb, s);
         maxBits.ensure(sizeof(unsigned));
         HIPC(hipMemsetAsync(maxBits.p, 0, sizeof(unsigned), s));
         launch_max_norm(xn.as<float>() + nb, n, maxBits.as<unsigned>(), s);
@@ -266,10 +278,10 @@ struct FlatIndex::Impl {
         std::vector<int> idx((size_t)pl.R0);
         for (int64_t r = 0; r < pl.R0; ++r) idx[(size_t)r] = (int)(r * pl.stride);
         sIdx.ensure(idx.size() * sizeof(int));
-        sX.ensure((size_t)pl.R0 * dpad * sizeof(float));
+        sX.ensure((size_t)pl.R0 * dpad * esize);
         sXn.ensure((size_t)pl.R0 * sizeof(float));
         HIPC(hipMemcpyAsync(sIdx.p, idx.data(), idx.size() * sizeof(int), hipMemcpyHostToDevice, s));
-        launch_gather_rows_blk(X.as<float>(), sIdx.as<int>(), (int)pl.R0, dpad, sX.as<float>(), s);
+        launch_gather_rows_blk(X.p, sIdx.as<int>(), (int)pl.R0, dpad, storage, sX.p, s);
         launch_gather_f32(xn.as<float>(), sIdx.as<int>(), (int)pl.R0, sXn.as<float>(), s);
         HIPC(hipStreamSynchronize(s));
         sampleNb = nb;
@@ -277,8 +289,8 @@ struct FlatIndex::Impl {
         sampleStride = pl.stride;
     }
 
-    void scan(const float* Xs, const float* xns, int64_t nrows, int64_t rps, int nsplit, int idStride,
-              const float* Q, const float* qn, int nq, const float* tk, const int* ti, int cap,
+    void scan(const void* Xs, const float* xns, int64_t nrows, int64_t rps, int nsplit, int idStride,
+              const void* Q, const float* qn, int nq, const float* tk, const int* ti, int cap,
               hipStream_t s, int pass = kPassFull) {
         const int nqb = (nq + kBN - 1) / kBN;
         cand.ensure((size_t)nq * nsplit * cap * sizeof(uint2));
@@ -289,7 +301,7 @@ struct FlatIndex::Impl {
         p.Q = Q; p.qnorm = qn; p.nq = nq; p.nqb = nqb; p.dpad = dpad;
         p.tau_key = tk; p.tau_id = ti;
         p.cand = cand.as<uint2>(); p.cnt = cnt.as<int>(); p.cap = cap;
-        launch_scan_filter(p, kernMetric(), pass, s);
+        launch_scan_filter(p, kernMetric(), pass, storage, s);
     }
 
     SelectParams selectParams(int nq, int nsplit, int cap, int k, int j) const {
@@ -302,22 +314,23 @@ struct FlatIndex::Impl {
         return sp;
     }
 
-    // Search mb staged queries (qbuf/qnorm) and write rows [0, mb) of the outputs.
+    // Search mb staged queries (storage type, qh or qbuf; norms in qnorm) and
+    // write rows [0, mb) of the outputs.
     void searchBatch(int mb, int k, const Plan& pl, int32_t* oIds, float* oVals, hipStream_t s) {
-        const float* Q = qbuf.as<float>();
+        const void* Q = storage == kF32 ? qbuf.p : qh.p;
         const float* qn = qnorm.as<float>();
         if (argminPath(mb, k)) {
             best.ensure((size_t)mb * sizeof(unsigned long long));
             launch_fill_u64(best.as<unsigned long long>(), mb, ~0ull, s);
             ScanParams p;
             std::memset(&p, 0, sizeof p);
-            p.X = X.as<float>(); p.xnorm = xn.as<float>(); p.xnorm_max = xnMax; p.nrows = nb;
-            splitPlan(nb, mb, dpad, p.rows_per_split, p.nsplit);
+            p.X = X.p; p.xnorm = xn.as<float>(); p.xnorm_max = xnMax; p.nrows = nb;
+            splitPlan(nb, mb, dpad, storage, p.rows_per_split, p.nsplit);
             p.id_stride = 1;
             p.Q = Q; p.qnorm = qn; p.nq = mb; p.nqb = (mb + kBN - 1) / kBN; p.dpad = dpad;
             p.cap = 1;
             p.best = best.as<unsigned long long>();
-            launch_scan_filter(p, kernMetric(), kPassArgmin, s);
+            launch_scan_filter(p, kernMetric(), kPassArgmin, storage, s);
             launch_argmin_finalize(best.as<unsigned long long>(), mb, kernMetric(), oIds, oVals, s);
             return;
         }
@@ -329,7 +342,7 @@ struct FlatIndex::Impl {
 
         if (pl.direct) {
             launch_fill_tau_none(tauSk.as<float>(), tauSi.as<int>(), mb, s);
-            scan(X.as<float>(), xn.as<float>(), nb, pl.rps1, pl.nsplit1, 1, Q, qn, mb,
+            scan(X.p, xn.as<float>(), nb, pl.rps1, pl.nsplit1, 1, Q, qn, mb,
                  tauSk.as<float>(), tauSi.as<int>(), pl.cap1, s);
             SelectParams sp = selectParams(mb, pl.nsplit1, pl.cap1, k, 1);
             sp.out_ids = oIds; sp.out_vals = oVals;
@@ -344,7 +357,7 @@ struct FlatIndex::Impl {
                          pl.stride, pl.j, pl.j2, pl.nsplit0, pl.cap0, pl.nsplit1, pl.cap1);
         // L0: sample, no bound -> speculative (j-th) and guaranteed (k-th) bounds
         launch_fill_tau_none(tauSk.as<float>(), tauSi.as<int>(), mb, s);
-        scan(sX.as<float>(), sXn.as<float>(), pl.R0, pl.rps0, pl.nsplit0, pl.stride, Q, qn, mb,
+        scan(sX.p, sXn.as<float>(), pl.R0, pl.rps0, pl.nsplit0, pl.stride, Q, qn, mb,
              tauSk.as<float>(), tauSi.as<int>(), pl.cap0, s, kPassSample);
         {
             SelectParams sp = selectParams(mb, pl.nsplit0, pl.cap0, k, pl.j);
@@ -355,7 +368,7 @@ struct FlatIndex::Impl {
             launch_select(sp, s);
         }
         // L1: full database with the speculative bound
-        scan(X.as<float>(), xn.as<float>(), nb, pl.rps1, pl.nsplit1, 1, Q, qn, mb,
+        scan(X.p, xn.as<float>(), nb, pl.rps1, pl.nsplit1, 1, Q, qn, mb,
              tauSk.as<float>(), tauSi.as<int>(), pl.cap1, s);
         {
             SelectParams sp = selectParams(mb, pl.nsplit1, pl.cap1, k, k);
@@ -398,10 +411,10 @@ struct FlatIndex::Impl {
             const int nf = (int)idx.size();
             const int nfPad = (int)roundUp(nf, kBN);
             cIdx.ensure((size_t)nf * 4); cSel.ensure((size_t)nf * 4);
-            cQ.ensure((size_t)nfPad * dpad * 4); cQn.ensure((size_t)nfPad * 4);
+            cQ.ensure((size_t)nfPad * dpad * esize); cQn.ensure((size_t)nfPad * 4);
             cTk.ensure((size_t)nf * 4); cTi.ensure((size_t)nf * 4);
             HIPC(hipMemcpyAsync(cIdx.p, idx.data(), (size_t)nf * 4, hipMemcpyHostToDevice, s));
-            launch_gather_rows(Q, cIdx.as<int>(), nf, dpad, cQ.as<float>(), nfPad, s);
+            launch_gather_rows(Q, cIdx.as<int>(), nf, dpad * esize, cQ.p, nfPad, s);
             launch_gather_f32(qn, cIdx.as<int>(), nf, cQn.as<float>(), s);
             HIPC(hipMemcpyAsync(cSel.p, sel.data(), (size_t)nf * 4, hipMemcpyHostToDevice, s));
             TauSources ts;
@@ -411,9 +424,9 @@ struct FlatIndex::Impl {
             launch_gather_tau(ts, cIdx.as<int>(), cSel.as<int>(), nf, cTk.as<float>(), cTi.as<int>(), s);
             int64_t rps;
             int nsplit;
-            splitPlan(nb, nf, dpad, rps, nsplit);
+            splitPlan(nb, nf, dpad, storage, rps, nsplit);
             const int cap = std::max(2 * k, 64);
-            scan(X.as<float>(), xn.as<float>(), nb, rps, nsplit, 1, cQ.as<float>(), cQn.as<float>(), nf,
+            scan(X.p, xn.as<float>(), nb, rps, nsplit, 1, cQ.p, cQn.as<float>(), nf,
                  cTk.as<float>(), cTi.as<int>(), cap, s, kPassRetry);
             SelectParams sp = selectParams(nf, nsplit, cap, k, k);
             sp.qmap = cIdx.as<int>();
@@ -460,7 +473,13 @@ struct FlatIndex::Impl {
             qnorm.ensure((size_t)nPad * sizeof(float));
             launch_pack_rows(dq + b0 * dim, n, dim, qbuf.as<float>(), nPad, dpad, s);
             if (metric == Metric::Cosine) launch_normalize_rows(qbuf.as<float>(), n, dpad, s);
-            if (metric == Metric::L2) launch_row_norms(qbuf.as<float>(), n, dpad, qnorm.as<float>(), s);
+            const void* qs = qbuf.p;
+            if (storage != kF32) {   // queries take the database's element type
+                qh.ensure((size_t)nPad * dpad * esize);
+                launch_round_rows(qbuf.as<float>(), nPad * dpad, storage, qh.p, s);
+                qs = qh.p;
+            }
+            if (metric == Metric::L2) launch_row_norms(qs, n, dpad, storage, qnorm.as<float>(), s);
             searchBatch(n, k, pb, ids ? ids + b0 * k : nullptr, vals ? vals + b0 * k : nullptr, s);
         }
         HIPC(hipStreamSynchronize(s));
@@ -468,10 +487,13 @@ struct FlatIndex::Impl {
     }
 };
 
-FlatIndex::FlatIndex(int dim, Metric metric) : d_(new Impl) {
+FlatIndex::FlatIndex(int dim, Metric metric, Storage storage) : d_(new Impl) {
+    if (storage != kF32 && storage != kF16 && storage != kBF16) throw BadArg("unknown storage type");
     d_->dim = dim;
     d_->dpad = (int)roundUp(dim, kBK);
     d_->metric = metric;
+    d_->storage = storage;
+    d_->esize = elem_bytes(storage);
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
         (void)hipGetLastError();
@@ -498,8 +520,8 @@ FlatIndex::~FlatIndex() {
     if (!d_) return;
     if (d_->device >= 0) (void)hipSetDevice(d_->device);
     if (d_->stream) (void)hipStreamSynchronize(d_->stream);
-    for (DevBuf* b : {&d_->X, &d_->xn, &d_->sX, &d_->sXn, &d_->sIdx, &d_->stage, &d_->qin, &d_->outIds,
-                      &d_->outVals, &d_->qbuf, &d_->qnorm, &d_->cand, &d_->cnt, &d_->tauSk, &d_->tauSi, &d_->tauS2k, &d_->tauS2i, &d_->maxBits,
+    for (DevBuf* b : {&d_->X, &d_->xn, &d_->sX, &d_->sXn, &d_->sIdx, &d_->stage, &d_->inv, &d_->qin, &d_->outIds,
+                      &d_->outVals, &d_->qbuf, &d_->qh, &d_->qnorm, &d_->cand, &d_->cnt, &d_->tauSk, &d_->tauSi, &d_->tauS2k, &d_->tauS2i, &d_->maxBits,
                       &d_->tauGk, &d_->tauGi, &d_->tauKk, &d_->tauKi, &d_->status, &d_->cQ, &d_->cQn,
                       &d_->cTk, &d_->cTi, &d_->cIdx, &d_->cSel, &d_->best})
         b->release();
@@ -510,6 +532,7 @@ bool FlatIndex::ready() const { return d_->ready; }
 int FlatIndex::size() const { return (int)d_->nb; }
 int FlatIndex::dim() const { return d_->dim; }
 Metric FlatIndex::metric() const { return d_->metric; }
+Storage FlatIndex::storage() const { return static_cast<Storage>(d_->storage); }
 
 void FlatIndex::add(const float* rows, int n) {
     d_->append(rows, n, hipMemcpyHostToDevice, d_->stream);

@@ -14,6 +14,8 @@
 #include <memory>
 #include <stdexcept>
 
+#include "kernels.hpp"
+
 namespace mflat_amd {
 
 enum class Metric : int { L2 = 0, InnerProduct = 1, Cosine = 2 };
@@ -31,7 +33,10 @@ class FlatIndex {
 public:
     static constexpr int kMaxK = 1024;
 
-    FlatIndex(int dim, Metric metric);
+    // storage: element type the database and the queries are held in (kF32,
+    // or the reduced-precision kF16 / kBF16: fp32 inputs rounded to nearest
+    // even, dots accumulated in fp32).
+    FlatIndex(int dim, Metric metric, Storage storage = kF32);
     ~FlatIndex();
     FlatIndex(const FlatIndex&) = delete;
     FlatIndex& operator=(const FlatIndex&) = delete;
@@ -40,6 +45,7 @@ public:
     int size() const;
     int dim() const;
     Metric metric() const;
+    Storage storage() const;
 
     // Append n rows (n * dim floats). Host or device memory.
     void add(const float* host_rows, int n);

@@ -25,6 +25,22 @@ namespace mflat_amd {
 
 typedef float fx4 __attribute__((ext_vector_type(4)));
 typedef float fx16 __attribute__((ext_vector_type(16)));
+typedef _Float16 hx8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bx8 __attribute__((ext_vector_type(8)));
+
+// fp16 / bf16 MFMA on 16-byte operand pieces (8 values per lane), fp32 accumulate.
+template <int S> __device__ __forceinline__ fx16 mfma32x32x16(fx4 a, fx4 b, fx16 c) {
+    if constexpr (S == kF16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(hx8, a), __builtin_bit_cast(hx8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bx8, a), __builtin_bit_cast(bx8, b), c, 0, 0, 0);
+}
+template <int S> __device__ __forceinline__ fx4 mfma16x16x32(fx4 a, fx4 b, fx4 c) {
+    if constexpr (S == kF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(hx8, a), __builtin_bit_cast(hx8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bx8, a), __builtin_bit_cast(bx8, b), c, 0, 0, 0);
+}
 
 constexpr int kQGroup = 16;      // query blocks co-scheduled per XCD (see scan_filter)
 constexpr int kLds = kBK + 4;   // LDS row stride in floats: 16-byte reads of 16
@@ -65,27 +81,58 @@ __global__ void pack_rows_kernel(const float* __restrict__ src, int64_t n, int d
     }
 }
 
-// ||row||^2 with a sequential double sum, cast to float: the accumulation the
-// reference's rowSqNorms uses (src/Distance.h:40-47), so the norms match it
-// bit for bit. One thread per row.
-__global__ void row_norms_kernel(const float* __restrict__ v, int64_t n, int dpad,
-                                 float* __restrict__ out) {
+// fp32 -> storage element bits, round to nearest even. fp16 by the hardware
+// conversion (IEEE overflow to inf, subnormals kept); bf16 by rounding the
+// upper half of the fp32 pattern (NaN -> the canonical quiet NaN 0x7fc0).
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) {
+    const uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+template <int S> __device__ __forceinline__ uint16_t to_bits(float x) {
+    return S == kF16 ? f32_to_f16_bits(x) : f32_to_bf16_bits(x);
+}
+template <int S> __device__ __forceinline__ float from_bits(uint16_t b) {
+    return S == kF16 ? (float)__builtin_bit_cast(_Float16, b) : __uint_as_float((uint32_t)b << 16);
+}
+// element c of a 16-byte piece (4 fp32 or 8 fp16/bf16 values) as fp32
+template <int S> __device__ __forceinline__ float piece_elem(const fx4& v, int c) {
+    if constexpr (S == kF32) {
+        return v[c];
+    } else {
+        const uint32_t w = __float_as_uint(v[c >> 1]);
+        return from_bits<S>((uint16_t)((c & 1) ? (w >> 16) : (w & 0xffffu)));
+    }
+}
+template <int S> constexpr int piece_elems() { return S == kF32 ? 4 : 8; }
+
+// ||row||^2 with a sequential double sum of the stored values, cast to float:
+// the accumulation the reference's rowSqNorms uses (src/Distance.h:40-47), so
+// fp32 norms match it bit for bit. One thread per row of a row-major array.
+template <int S>
+__global__ void row_norms_kernel(const void* __restrict__ v, int64_t n, int dpad, float* __restrict__ out) {
     const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (r >= n) return;
-    const float* row = v + r * dpad;
+    constexpr int PE = piece_elems<S>();
+    const fx4* row = (const fx4*)v + r * (dpad / PE);
     double s = 0.0;
-    for (int c = 0; c < dpad; c += 4) {
-        const fx4 x = *(const fx4*)(row + c);
-        s += (double)x.x * x.x;
-        s += (double)x.y * x.y;
-        s += (double)x.z * x.z;
-        s += (double)x.w * x.w;
+    for (int u = 0; u < dpad / PE; ++u) {
+        const fx4 x = row[u];
+#pragma unroll
+        for (int c = 0; c < PE; ++c) {
+            const float e = piece_elem<S>(x, c);
+            s += (double)e * e;
+        }
     }
     out[r] = (float)s;
 }
 
-// In-place L2 normalisation (reference src/Distance.h:50-60): double sum,
-// inv = float(1 / sqrt(s)), x *= inv, zero rows unchanged.
+// In-place L2 normalisation of fp32 row-major rows (reference
+// src/Distance.h:50-60): double sum, inv = float(1 / sqrt(s)), x *= inv, zero
+// rows unchanged.
 __global__ void normalize_rows_kernel(float* __restrict__ v, int64_t n, int dpad) {
     const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (r >= n) return;
@@ -98,77 +145,103 @@ __global__ void normalize_rows_kernel(float* __restrict__ v, int64_t n, int dpad
     }
 }
 
-// Database (chunked layout) helpers; see blk_off.
+// The same rule's scale factor for rows about to be stored: inv[r] =
+// float(1 / sqrt(s)), or 1 for a zero row (x * 1 == x leaves it unchanged).
+__global__ void row_inv_norms_kernel(const float* __restrict__ src, int64_t n, int dim,
+                                     float* __restrict__ inv) {
+    const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (r >= n) return;
+    const float* row = src + r * dim;
+    double s = 0.0;
+    for (int c = 0; c < dim; ++c) s += (double)row[c] * row[c];
+    inv[r] = s > 0.0 ? (float)(1.0 / sqrt(s)) : 1.0f;
+}
+
+// fp32 -> storage type, elementwise (count multiple of 8 for fp16/bf16).
+template <int S>
+__global__ void round_rows_kernel(const float* __restrict__ src, int64_t count, uint16_t* __restrict__ dst) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < count;
+         i += (int64_t)gridDim.x * blockDim.x)
+        dst[i] = to_bits<S>(src[i]);
+}
+
+// Database (chunked layout) helpers; see blk_off / blk_off_h. One thread per
+// 16-byte piece: 4 fp32 or 8 fp16/bf16 consecutive columns of one row.
+template <int S>
+__device__ __forceinline__ int64_t piece_off(int64_t row, int col, int dpad) {
+    return S == kF32 ? blk_off(row, col, dpad) : blk_off_h(row, col, dpad);
+}
+
+template <int S>
 __global__ void store_rows_blk_kernel(const float* __restrict__ src, int64_t n, int dim,
-                                      float* __restrict__ X, int64_t row0, int dpad) {
-    const int c4n = dpad / 4;
-    const int64_t total = n * c4n;
+                                      const float* __restrict__ inv, void* __restrict__ X, int64_t row0,
+                                      int dpad) {
+    constexpr int PE = piece_elems<S>();
+    const int pn = dpad / PE;
+    const int64_t total = n * pn;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t r = i / c4n;
-        const int c = (int)(i - r * c4n) * 4;
-        fx4 v;
-        for (int j = 0; j < 4; ++j) v[j] = c + j < dim ? src[r * dim + c + j] : 0.0f;
-        *(fx4*)(X + blk_off(row0 + r, c, dpad)) = v;
+        const int64_t r = i / pn;
+        const int c = (int)(i - r * pn) * PE;
+        const float sc = inv ? inv[r] : 1.0f;
+        float v[PE];
+#pragma unroll
+        for (int j = 0; j < PE; ++j) v[j] = c + j < dim ? (inv ? src[r * dim + c + j] * sc : src[r * dim + c + j]) : 0.0f;
+        fx4 w;
+        if constexpr (S == kF32) {
+            w = fx4{v[0], v[1], v[2], v[3]};
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                w[j] = __uint_as_float((uint32_t)to_bits<S>(v[2 * j]) | ((uint32_t)to_bits<S>(v[2 * j + 1]) << 16));
+        }
+        *((fx4*)X + piece_off<S>(row0 + r, c, dpad) / PE) = w;
     }
 }
 
 // Sequential double sum over the row in column order (reference rowSqNorms).
-__global__ void row_norms_blk_kernel(const float* __restrict__ X, int64_t row0, int64_t n, int dpad,
+template <int S>
+__global__ void row_norms_blk_kernel(const void* __restrict__ X, int64_t row0, int64_t n, int dpad,
                                      float* __restrict__ out) {
     const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (r >= n) return;
+    constexpr int PE = piece_elems<S>();
     double s = 0.0;
-    for (int c = 0; c < dpad; c += 4) {
-        const fx4 x = *(const fx4*)(X + blk_off(row0 + r, c, dpad));
-        s += (double)x.x * x.x;
-        s += (double)x.y * x.y;
-        s += (double)x.z * x.z;
-        s += (double)x.w * x.w;
+    for (int c = 0; c < dpad; c += PE) {
+        const fx4 x = *((const fx4*)X + piece_off<S>(row0 + r, c, dpad) / PE);
+#pragma unroll
+        for (int j = 0; j < PE; ++j) {
+            const float e = piece_elem<S>(x, j);
+            s += (double)e * e;
+        }
     }
     out[r] = (float)s;
 }
 
-__global__ void normalize_rows_blk_kernel(float* __restrict__ X, int64_t row0, int64_t n, int dpad) {
-    const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (r >= n) return;
-    double s = 0.0;
-    for (int c = 0; c < dpad; c += 4) {
-        const fx4 x = *(const fx4*)(X + blk_off(row0 + r, c, dpad));
-        for (int j = 0; j < 4; ++j) s += (double)x[j] * x[j];
-    }
-    if (s > 0.0) {
-        const float inv = (float)(1.0 / sqrt(s));
-        for (int c = 0; c < dpad; c += 4) {
-            fx4* px = (fx4*)(X + blk_off(row0 + r, c, dpad));
-            fx4 x = *px;
-            for (int j = 0; j < 4; ++j) x[j] *= inv;
-            *px = x;
-        }
-    }
-}
-
 // dst row r (chunked) = X row idx[r] (chunked), r < n
-__global__ void gather_rows_blk_kernel(const float* __restrict__ X, const int* __restrict__ idx, int n,
-                                       int dpad, float* __restrict__ dst) {
-    const int c4n = dpad / 4;
-    const int64_t total = (int64_t)n * c4n;
+template <int S>
+__global__ void gather_rows_blk_kernel(const void* __restrict__ X, const int* __restrict__ idx, int n,
+                                       int dpad, void* __restrict__ dst) {
+    constexpr int PE = piece_elems<S>();
+    const int pn = dpad / PE;
+    const int64_t total = (int64_t)n * pn;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t r = i / c4n;
-        const int c = (int)(i - r * c4n) * 4;
-        *(fx4*)(dst + blk_off(r, c, dpad)) = *(const fx4*)(X + blk_off(idx[r], c, dpad));
+        const int64_t r = i / pn;
+        const int c = (int)(i - r * pn) * PE;
+        *((fx4*)dst + piece_off<S>(r, c, dpad) / PE) = *((const fx4*)X + piece_off<S>(idx[r], c, dpad) / PE);
     }
 }
 
-__global__ void gather_rows_kernel(const float* __restrict__ src, const int* __restrict__ idx,
-                                   int n, int dpad, float* __restrict__ dst, int64_t n_pad) {
-    const int64_t total = n_pad * dpad;
+// row-major rows of `pieces` 16-byte pieces
+__global__ void gather_rows_kernel(const fx4* __restrict__ src, const int* __restrict__ idx,
+                                   int n, int pieces, fx4* __restrict__ dst, int64_t n_pad) {
+    const int64_t total = n_pad * pieces;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t r = i / dpad;
-        const int c = (int)(i - r * dpad);
-        dst[i] = r < n ? src[(int64_t)idx[r] * dpad + c] : 0.0f;
+        const int64_t r = i / pieces;
+        const int c = (int)(i - r * pieces);
+        dst[i] = r < n ? src[(int64_t)idx[r] * pieces + c] : fx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 }
 
@@ -227,22 +300,28 @@ __global__ void max_norm_kernel(const float* __restrict__ xn, int64_t n, unsigne
 }
 
 // ---------------------------------------------------------------------------
-// scan_filter: fp32 MFMA distance tile + threshold filter
+// scan_filter: MFMA distance tile + threshold filter
 // ---------------------------------------------------------------------------
 //
 // Workgroup: 256 threads = 4 waves in a 2 x 2 arrangement; each wave owns a
 // 64-row x 64-query quarter of the 128 x 128 tile as 2 x 2 blocks of
-// v_mfma_f32_32x32x2_f32. The operand roles: A = database rows (M), B = queries
-// (N), so accumulator register r of lane l holds
+// v_mfma_f32_32x32x2_f32 (fp32 storage) or v_mfma_f32_32x32x16_{f16,bf16}.
+// The operand roles: A = database rows (M), B = queries (N), so accumulator
+// register r of lane l holds
 //     row   = 8*(r/4) + 4*(l/32) + (r%4),   query = l%32
 // i.e. every lane sees 16 rows of ONE query per block, which keeps the
 // per-query threshold in a register during the epilogue.
 //
-// The K dimension is consumed in chunks of kBK = 32 staged through LDS, double
-// buffered; one barrier per chunk. Within a chunk the two lane halves read
-// float4s of 4 consecutive columns, and MFMA step j of group g pairs columns
-// (8g + j, 8g + 4 + j): the same permutation on both operands, so the dot is
-// unchanged while every LDS read is a single ds_read_b128.
+// The K dimension is consumed in chunks of 128 bytes per row (32 fp32 or 64
+// fp16/bf16 columns) staged through LDS, double buffered; one barrier per
+// chunk. Every LDS operand read is a single ds_read_b128 of 16 bytes at byte
+// 16 h + 32 g of the row (lane half h, group g = 0..3), on both operands:
+//   fp32: MFMA step j of group g pairs columns (8g + j, 8g + 4 + j);
+//   fp16/bf16: group g is one MFMA over columns 16g .. 16g + 15, lane half h
+//   supplying 8h .. 8h + 7 of them.
+// The same permutation on both operands leaves the dot unchanged. With fp16 /
+// bf16 and dpad = 64 c + 32, the last chunk holds 32 real columns; the loaders
+// fill its other half of LDS with zeros.
 //
 // A workgroup owns one query block and one split (a contiguous range of
 // database rows) and walks the split's tiles in ascending row order. Linear
@@ -253,8 +332,9 @@ __global__ void max_norm_kernel(const float* __restrict__ xn, int64_t n, unsigne
 // PASS only names the instantiation (0 = full database, 1 = row sample,
 // 2 = retry of a few queries), so profiles separate the passes; the code is
 // the same.
-template <int METRIC, int PASS>
+template <int S, int METRIC, int PASS>
 __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
+    constexpr int ES = S == kF32 ? 4 : 2;   // element bytes
     __shared__ __attribute__((aligned(16))) float sX[2 * kBM * kLds];
     __shared__ __attribute__((aligned(16))) float sQ[2 * kBN * kLds];
     __shared__ __attribute__((aligned(16))) float sXn[2 * kBM];   // tile row norms, by tile parity
@@ -330,30 +410,40 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     int64_t rowEnd = rowBeg + p.rows_per_split;
     if (rowEnd > rows_pad) rowEnd = rows_pad;
     const int ntiles = rowEnd > rowBeg ? (int)((rowEnd - rowBeg) / kBM) : 0;
-    const int nk = p.dpad / kBK;
+    const int nk = S == kF32 ? p.dpad / kBK : (p.dpad + 63) / 64;
+    const bool halfTail = S != kF32 && (p.dpad & 32) != 0;   // last chunk: 32 columns
     const int total = ntiles * nk;
 
-    // global -> register staging: 4 float4 per thread per operand
+    // global -> register staging: 4 pieces of 16 bytes per thread per operand
     const int ldRow = tid >> 3;         // + 32*i
-    const int ldCol = (tid & 7) * 4;
-    const float* Xb = p.X + rowBeg * p.dpad;
-    const float* Qb = p.Q + (int64_t)qb * kBN * p.dpad;
+    const int ldCol = (tid & 7) * 4;    // in floats = 16-byte pieces
+    const char* Xb = (const char*)p.X + rowBeg * p.dpad * ES;
+    const char* Qb = (const char*)p.Q + (int64_t)qb * kBN * p.dpad * ES;
     fx4 rx[4], rq[4], rn;
     // The first chunk of every tile also brings the tile's 128 row norms
     // (threads 0..31, one float4 each) into sXn[tile & 1]; the epilogue of
     // that tile reads them from LDS instead of waiting on global memory.
     // Database chunks are linear 4 KB pieces (one per 32-row block, chunked
-    // layout): thread t takes float4 t of each piece, i.e. row
-    // 32 i + 16 (t >> 7) + (t & 15), columns 8 ((t >> 4) & 3) + 4 ((t >> 6) & 1) .. +3.
-    const int xRow = 16 * (tid >> 7) + (tid & 15);
-    const int xCol = 8 * ((tid >> 4) & 3) + 4 * ((tid >> 6) & 1);
+    // layout): thread t takes 16-byte piece t of each, i.e. row 32 i + xRow,
+    // LDS float column xCol (fp32: columns 8 ((t >> 4) & 3) + 4 ((t >> 6) & 1)
+    // .. +3; fp16/bf16: sub-chunk t >> 7, columns 32 (t >> 7) + 8 ((t >> 4) & 3)
+    // .. +7). A 32-column fp16/bf16 tail chunk has only sub-chunk 0: threads
+    // t >= 128 load nothing and stage zeros, as do the query loaders of its
+    // second half.
+    const int xRow = S == kF32 ? 16 * (tid >> 7) + (tid & 15) : 16 * ((tid >> 6) & 1) + (tid & 15);
+    const int xCol = S == kF32 ? 8 * ((tid >> 4) & 3) + 4 * ((tid >> 6) & 1)
+                               : 16 * (tid >> 7) + 4 * ((tid >> 4) & 3);
     auto gload = [&](int tile, int kc) {
-        const float* xs = Xb + ((int64_t)tile * kBM) * p.dpad + kc * 1024 + tid * 4;
-        const float* qs = Qb + kc * kBK + ldCol;
+        const char* xs = Xb + ((int64_t)tile * kBM) * p.dpad * ES + kc * 4096 + tid * 16;
+        const char* qs = Qb + kc * 128 + ldCol * 4;
+        const bool zx = S != kF32 && halfTail && kc == nk - 1 && tid >= 128;
+        const bool zq = S != kF32 && halfTail && kc == nk - 1 && (tid & 7) >= 4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            rx[i] = *(const fx4*)(xs + (int64_t)i * 32 * p.dpad);
-            rq[i] = *(const fx4*)(qs + (int64_t)(ldRow + 32 * i) * p.dpad);
+            rx[i] = fx4{0.0f, 0.0f, 0.0f, 0.0f};
+            rq[i] = fx4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (!zx) rx[i] = *(const fx4*)(xs + (int64_t)i * 32 * p.dpad * ES);
+            if (!zq) rq[i] = *(const fx4*)(qs + (int64_t)(ldRow + 32 * i) * p.dpad * ES);
         }
         if (METRIC == 0 && kc == 0 && tid < kBM / 4)
             rn = *(const fx4*)(p.xnorm + rowBeg + (int64_t)tile * kBM + tid * 4);
@@ -407,11 +497,19 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
             const fx16 z = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f,
                             0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int g = 0; g < kBK / 8; ++g) {
+            for (int g = 0; g < 4; ++g) {
                 fx4 a0 = *(const fx4*)(sx + aOff + g * 8);
                 fx4 a1 = *(const fx4*)(sx + aOff + 32 * kLds + g * 8);
                 fx4 b0 = *(const fx4*)(sq + bOff + g * 8);
                 fx4 b1 = *(const fx4*)(sq + bOff + 32 * kLds + g * 8);
+                if constexpr (S != kF32) {
+                    const bool zc = ZERO && g == 0;
+                    acc[0][0] = mfma32x32x16<S>(a0, b0, zc ? z : acc[0][0]);
+                    acc[0][1] = mfma32x32x16<S>(a0, b1, zc ? z : acc[0][1]);
+                    acc[1][0] = mfma32x32x16<S>(a1, b0, zc ? z : acc[1][0]);
+                    acc[1][1] = mfma32x32x16<S>(a1, b1, zc ? z : acc[1][1]);
+                    continue;
+                }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     if (ZERO && g == 0 && j == 0) {
@@ -535,21 +633,26 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
 // With few queries every database byte is used by at most 64 queries, so the
 // pass is bound by reading the database once from HBM, not by MFMA. The
 // database rows go straight from global memory into the A operand of
-// v_mfma_f32_16x16x4_f32 (no LDS staging: each row is used by one wave only);
-// the queries, NQB blocks of 16, sit in LDS as the B operand. Output layout:
-// lane l holds query l%16 of the block and rows 4*(l/16) .. +3, so the
-// epilogue keeps the per-query bound in a register as in scan_filter.
-// K is consumed 16 columns at a time: lane quarter q = l/16 reads the float4 at
-// columns 16t + 4q .. +3 of its row and MFMA step j pairs columns
-// 16t + 4q + j across the quarters -- the same permutation on both operands.
+// v_mfma_f32_16x16x4_f32 (fp32) or v_mfma_f32_16x16x32_{f16,bf16} (no LDS
+// staging: each row is used by one wave only); the queries, NQB blocks of 16,
+// sit in LDS as the B operand. Output layout: lane l holds query l%16 of the
+// block and rows 4*(l/16) .. +3, so the epilogue keeps the per-query bound in
+// a register as in scan_filter.
+// K is consumed 32 columns (one chunk) at a time: lane quarter q = l/16 holds
+// columns 32t + 8q .. +7 of its row -- fp32 as two float4 pieces e, MFMA j
+// pairing column 32t + 8q + j across the quarters; fp16/bf16 as one 16-byte
+// piece, one MFMA per chunk -- the same permutation on both operands.
 // One workgroup per split.
 // G > 0: dpad == 32 G, and a whole 32-row block is buffered in registers
 // (the next block's step t is fetched as soon as step t of the current block is
-// consumed), which keeps ~G KB per wave in flight. G == 0: any dpad, one step
-// of prefetch.
-template <int METRIC, int NQB, int PASS, int G>
+// consumed), which keeps G pieces per lane in flight. G == 0: any dpad, one
+// step of prefetch.
+template <int S, int METRIC, int NQB, int PASS, int G>
 __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
-    extern __shared__ __attribute__((aligned(16))) float sQs[];   // [16*NQB][dpad + 4]
+    constexpr int ES = S == kF32 ? 4 : 2;
+    constexpr int U = S == kF32 ? 2 : 1;      // 16-byte pieces per row half per chunk
+    constexpr int PAD = 16 / ES;              // LDS row padding (elements)
+    extern __shared__ __attribute__((aligned(16))) float sQs[];   // [16*NQB][dpad + PAD] elements
     __shared__ int sCnt[16 * NQB];
 
     const int split = blockIdx.x;
@@ -558,12 +661,13 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
     const int wave = tid >> 6;
     const int r16 = lane & 15;
     const int quarter = lane >> 4;
-    const int ldq = p.dpad + 4;
+    const int ldqB = (p.dpad + PAD) * ES;     // LDS query row stride, bytes
+    const int rowP = p.dpad * ES / 16;        // 16-byte pieces per query row
 
-    for (int i = tid; i < 16 * NQB * (p.dpad / 4); i += 256) {
-        const int row = i / (p.dpad / 4);
-        const int c4 = i - row * (p.dpad / 4);
-        *(fx4*)(sQs + row * ldq + c4 * 4) = *(const fx4*)(p.Q + (int64_t)row * p.dpad + c4 * 4);
+    for (int i = tid; i < 16 * NQB * rowP; i += 256) {
+        const int row = i / rowP;
+        const int c = i - row * rowP;
+        *(fx4*)((char*)sQs + row * ldqB + c * 16) = *((const fx4*)p.Q + (int64_t)row * rowP + c);
     }
     if (tid < 16 * NQB) sCnt[tid] = 0;
 
@@ -591,24 +695,23 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
     int64_t rowEnd = rowBeg + p.rows_per_split;
     if (rowEnd > rows_pad) rowEnd = rows_pad;
     // Each wave takes 32-row blocks (two 16-row MFMA sets) round-robin. In the
-    // chunked layout, the operand float4 e of row half hh for 32-column step t
-    // is one linear 1 KB load per wave: lane l reads float4 l of sub-chunk
-    // (hh, e), i.e. row 16 hh + (l & 15), columns 32 t + 8 (l >> 4) + 4 e .. +3,
-    // and MFMA j of the step pairs columns 32 t + 8 q + j over quarters q.
+    // chunked layout, the operand piece e of row half hh for chunk t is one
+    // linear 1 KB load per wave: lane l reads piece l of sub-chunk (hh, e),
+    // i.e. row 16 hh + (l & 15), columns 32 t + 8 (l >> 4) (+ 4 e for fp32).
     // Rows are read exactly once: non-temporal loads keep them from displacing
     // the query tile and the candidate lines in the caches.
     const int nblk = rowEnd > rowBeg ? (int)((rowEnd - rowBeg) / 32) : 0;
     const int g32 = p.dpad / 32;
-    const int64_t blkStride = (int64_t)32 * p.dpad;
-    const float* xw = p.X + rowBeg * p.dpad + lane * 4;
-    const float* qrow8 = sQs + r16 * ldq + quarter * 8;
+    const int64_t blkStride = (int64_t)32 * p.dpad * ES;   // bytes
+    const char* xw = (const char*)p.X + rowBeg * p.dpad * ES + lane * 16;
+    const char* qrow8 = (const char*)sQs + r16 * ldqB + quarter * 8 * ES;
     auto ld = [&](int b, int t, int hh, int e) -> fx4 {
-        return __builtin_nontemporal_load((const fx4*)(xw + b * blkStride + t * 1024 + (hh * 2 + e) * 256));
+        return __builtin_nontemporal_load((const fx4*)(xw + b * blkStride + t * (U * 2048) + (hh * U + e) * 1024));
     };
 
     constexpr int GB = G > 0 ? G : 1;
-    fx4 buf[2][GB][2];   // G > 0: the wave's whole current block [row half][step][e]
-    fx4 cur[2][2];       // G == 0: the current step
+    fx4 buf[2][GB][U];   // G > 0: the wave's whole current block [row half][step][e]
+    fx4 cur[2][U];       // G == 0: the current step
     if (wave < nblk) {
         if constexpr (G > 0) {
 #pragma unroll
@@ -616,12 +719,12 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                    for (int e = 0; e < 2; ++e) buf[hh][t][e] = ld(wave, t, hh, e);
+                    for (int e = 0; e < U; ++e) buf[hh][t][e] = ld(wave, t, hh, e);
         } else {
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                for (int e = 0; e < 2; ++e) cur[hh][e] = ld(wave, 0, hh, e);
+                for (int e = 0; e < U; ++e) cur[hh][e] = ld(wave, 0, hh, e);
         }
     }
     for (int b = wave; b < nblk; b += 4) {
@@ -639,17 +742,23 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
         for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
             for (int bq = 0; bq < NQB; ++bq) acc[hh][bq] = fx4{0.0f, 0.0f, 0.0f, 0.0f};
-        auto step = [&](const fx4 (&x)[2][2], int t) {
+        auto step = [&](const fx4 (&x)[2][U], int t) {
 #pragma unroll
             for (int bq = 0; bq < NQB; ++bq) {
-                const float* qp = qrow8 + bq * 16 * ldq + t * 32;
-                const fx4 bv0 = *(const fx4*)qp;
-                const fx4 bv1 = *(const fx4*)(qp + 4);
+                const char* qp = qrow8 + bq * 16 * ldqB + t * 32 * ES;
+                if constexpr (S == kF32) {
+                    const fx4 bv0 = *(const fx4*)qp;
+                    const fx4 bv1 = *(const fx4*)(qp + 16);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float bj = j < 4 ? bv0[j & 3] : bv1[j & 3];
-                    acc[0][bq] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[0][j >> 2][j & 3], bj, acc[0][bq], 0, 0, 0);
-                    acc[1][bq] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[1][j >> 2][j & 3], bj, acc[1][bq], 0, 0, 0);
+                    for (int j = 0; j < 8; ++j) {
+                        const float bj = j < 4 ? bv0[j & 3] : bv1[j & 3];
+                        acc[0][bq] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[0][j >> 2][j & 3], bj, acc[0][bq], 0, 0, 0);
+                        acc[1][bq] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[1][j >> 2][j & 3], bj, acc[1][bq], 0, 0, 0);
+                    }
+                } else {
+                    const fx4 bv = *(const fx4*)qp;
+                    acc[0][bq] = mfma16x16x32<S>(x[0][0], bv, acc[0][bq]);
+                    acc[1][bq] = mfma16x16x32<S>(x[1][0], bv, acc[1][bq]);
                 }
             }
         };
@@ -657,16 +766,16 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
         if constexpr (G > 0) {
 #pragma unroll
             for (int t = 0; t < GB; ++t) {
-                fx4 x[2][2];
+                fx4 x[2][U];
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                    for (int e = 0; e < 2; ++e) x[hh][e] = buf[hh][t][e];
+                    for (int e = 0; e < U; ++e) x[hh][e] = buf[hh][t][e];
                 if (hasNext) {
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                        for (int e = 0; e < 2; ++e) buf[hh][t][e] = ld(b + 4, t, hh, e);
+                        for (int e = 0; e < U; ++e) buf[hh][t][e] = ld(b + 4, t, hh, e);
                 }
                 step(x, t);
             }
@@ -675,22 +784,22 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
                 const bool lastT = t + 1 == g32;
                 const int nbk = lastT ? b + 4 : b;
                 const int nt = lastT ? 0 : t + 1;
-                fx4 nx[2][2];
+                fx4 nx[2][U];
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                    for (int e = 0; e < 2; ++e) nx[hh][e] = cur[hh][e];
+                    for (int e = 0; e < U; ++e) nx[hh][e] = cur[hh][e];
                 if (nbk < nblk) {
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                        for (int e = 0; e < 2; ++e) nx[hh][e] = ld(nbk, nt, hh, e);
+                        for (int e = 0; e < U; ++e) nx[hh][e] = ld(nbk, nt, hh, e);
                 }
                 step(cur, t);
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                    for (int e = 0; e < 2; ++e) cur[hh][e] = nx[hh][e];
+                    for (int e = 0; e < U; ++e) cur[hh][e] = nx[hh][e];
             }
         }
 
@@ -992,15 +1101,6 @@ void launch_pack_rows(const float* src, int64_t n, int dim, float* dst, int64_t 
     check_launch("pack_rows");
 }
 
-void launch_row_norms(const float* v, int64_t n, int dpad, float* out, hipStream_t s) {
-    if (n <= 0) return;
-    void* tok;
-    prof_begin(kFamNorms, s, &tok);
-    row_norms_kernel<<<(int)((n + 255) / 256), 256, 0, s>>>(v, n, dpad, out);
-    prof_end(tok, s);
-    check_launch("row_norms");
-}
-
 void launch_normalize_rows(float* v, int64_t n, int dpad, hipStream_t s) {
     if (n <= 0) return;
     void* tok;
@@ -1010,49 +1110,98 @@ void launch_normalize_rows(float* v, int64_t n, int dpad, hipStream_t s) {
     check_launch("normalize_rows");
 }
 
-void launch_store_rows_blk(const float* src, int64_t n, int dim, float* X, int64_t row0, int dpad,
-                           hipStream_t s) {
-    if (n <= 0) return;
+static void check_storage(int storage) {
+    if (storage != kF32 && storage != kF16 && storage != kBF16)
+        throw std::runtime_error("unknown storage type");
+}
+
+void launch_round_rows(const float* src, int64_t count, int storage, void* dst, hipStream_t s) {
+    if (count <= 0) return;
+    check_storage(storage);
+    if (storage == kF32) throw std::runtime_error("round_rows: fp32 needs no rounding");
     void* tok;
     prof_begin(kFamPrep, s, &tok);
-    store_rows_blk_kernel<<<grid_for(n * dpad / 4, 256), 256, 0, s>>>(src, n, dim, X, row0, dpad);
+    if (storage == kF16)
+        round_rows_kernel<kF16><<<grid_for(count, 256), 256, 0, s>>>(src, count, (uint16_t*)dst);
+    else
+        round_rows_kernel<kBF16><<<grid_for(count, 256), 256, 0, s>>>(src, count, (uint16_t*)dst);
+    prof_end(tok, s);
+    check_launch("round_rows");
+}
+
+void launch_row_norms(const void* v, int64_t n, int dpad, int storage, float* out, hipStream_t s) {
+    if (n <= 0) return;
+    check_storage(storage);
+    void* tok;
+    prof_begin(kFamNorms, s, &tok);
+    const int g = (int)((n + 255) / 256);
+    if (storage == kF32) row_norms_kernel<kF32><<<g, 256, 0, s>>>(v, n, dpad, out);
+    else if (storage == kF16) row_norms_kernel<kF16><<<g, 256, 0, s>>>(v, n, dpad, out);
+    else row_norms_kernel<kBF16><<<g, 256, 0, s>>>(v, n, dpad, out);
+    prof_end(tok, s);
+    check_launch("row_norms");
+}
+
+void launch_row_inv_norms(const float* src, int64_t n, int dim, float* inv, hipStream_t s) {
+    if (n <= 0) return;
+    void* tok;
+    prof_begin(kFamNorms, s, &tok);
+    row_inv_norms_kernel<<<(int)((n + 255) / 256), 256, 0, s>>>(src, n, dim, inv);
+    prof_end(tok, s);
+    check_launch("row_inv_norms");
+}
+
+void launch_store_rows_blk(const float* src, int64_t n, int dim, const float* inv, void* X, int64_t row0,
+                           int dpad, int storage, hipStream_t s) {
+    if (n <= 0) return;
+    check_storage(storage);
+    void* tok;
+    prof_begin(kFamPrep, s, &tok);
+    const int g = grid_for(n * dpad / 4, 256);
+    if (storage == kF32) store_rows_blk_kernel<kF32><<<g, 256, 0, s>>>(src, n, dim, inv, X, row0, dpad);
+    else if (storage == kF16) store_rows_blk_kernel<kF16><<<g, 256, 0, s>>>(src, n, dim, inv, X, row0, dpad);
+    else store_rows_blk_kernel<kBF16><<<g, 256, 0, s>>>(src, n, dim, inv, X, row0, dpad);
     prof_end(tok, s);
     check_launch("store_rows_blk");
 }
 
-void launch_row_norms_blk(const float* X, int64_t row0, int64_t n, int dpad, float* out, hipStream_t s) {
+void launch_row_norms_blk(const void* X, int64_t row0, int64_t n, int dpad, int storage, float* out,
+                          hipStream_t s) {
     if (n <= 0) return;
+    check_storage(storage);
     void* tok;
     prof_begin(kFamNorms, s, &tok);
-    row_norms_blk_kernel<<<(int)((n + 255) / 256), 256, 0, s>>>(X, row0, n, dpad, out);
+    const int g = (int)((n + 255) / 256);
+    if (storage == kF32) row_norms_blk_kernel<kF32><<<g, 256, 0, s>>>(X, row0, n, dpad, out);
+    else if (storage == kF16) row_norms_blk_kernel<kF16><<<g, 256, 0, s>>>(X, row0, n, dpad, out);
+    else row_norms_blk_kernel<kBF16><<<g, 256, 0, s>>>(X, row0, n, dpad, out);
     prof_end(tok, s);
     check_launch("row_norms_blk");
 }
 
-void launch_normalize_rows_blk(float* X, int64_t row0, int64_t n, int dpad, hipStream_t s) {
+void launch_gather_rows_blk(const void* X, const int* idx, int n, int dpad, int storage, void* dst,
+                            hipStream_t s) {
     if (n <= 0) return;
-    void* tok;
-    prof_begin(kFamNorms, s, &tok);
-    normalize_rows_blk_kernel<<<(int)((n + 255) / 256), 256, 0, s>>>(X, row0, n, dpad);
-    prof_end(tok, s);
-    check_launch("normalize_rows_blk");
-}
-
-void launch_gather_rows_blk(const float* X, const int* idx, int n, int dpad, float* dst, hipStream_t s) {
-    if (n <= 0) return;
+    check_storage(storage);
     void* tok;
     prof_begin(kFamPrep, s, &tok);
-    gather_rows_blk_kernel<<<grid_for((int64_t)n * dpad / 4, 256), 256, 0, s>>>(X, idx, n, dpad, dst);
+    const int g = grid_for((int64_t)n * dpad / 4, 256);
+    if (storage == kF32) gather_rows_blk_kernel<kF32><<<g, 256, 0, s>>>(X, idx, n, dpad, dst);
+    else if (storage == kF16) gather_rows_blk_kernel<kF16><<<g, 256, 0, s>>>(X, idx, n, dpad, dst);
+    else gather_rows_blk_kernel<kBF16><<<g, 256, 0, s>>>(X, idx, n, dpad, dst);
     prof_end(tok, s);
     check_launch("gather_rows_blk");
 }
 
-void launch_gather_rows(const float* src, const int* idx, int n, int dpad, float* dst,
+void launch_gather_rows(const void* src, const int* idx, int n, int row_bytes, void* dst,
                         int64_t n_pad, hipStream_t s) {
     if (n_pad <= 0) return;
+    if (row_bytes % 16 != 0) throw std::runtime_error("gather_rows: row size not a multiple of 16 bytes");
     void* tok;
     prof_begin(kFamPrep, s, &tok);
-    gather_rows_kernel<<<grid_for(n_pad * dpad, 256), 256, 0, s>>>(src, idx, n, dpad, dst, n_pad);
+    const int pieces = row_bytes / 16;
+    gather_rows_kernel<<<grid_for(n_pad * pieces, 256), 256, 0, s>>>((const fx4*)src, idx, n, pieces,
+                                                                      (fx4*)dst, n_pad);
     prof_end(tok, s);
     check_launch("gather_rows");
 }
@@ -1103,42 +1252,66 @@ void launch_max_norm(const float* xn, int64_t n, unsigned* out, hipStream_t s) {
     check_launch("max_norm");
 }
 
-template <int M, int NQB, int G>
+template <int S, int M, int NQB, int G>
 static void launch_small_g(const ScanParams& p, int pass, int g, size_t lds, hipStream_t s) {
-    if (pass == kPassSample) scan_small_kernel<M, NQB, kPassSample, G><<<g, 256, lds, s>>>(p);
-    else if (pass == kPassRetry) scan_small_kernel<M, NQB, kPassRetry, G><<<g, 256, lds, s>>>(p);
-    else scan_small_kernel<M, NQB, kPassFull, G><<<g, 256, lds, s>>>(p);
+    if (pass == kPassSample) scan_small_kernel<S, M, NQB, kPassSample, G><<<g, 256, lds, s>>>(p);
+    else if (pass == kPassRetry) scan_small_kernel<S, M, NQB, kPassRetry, G><<<g, 256, lds, s>>>(p);
+    else scan_small_kernel<S, M, NQB, kPassFull, G><<<g, 256, lds, s>>>(p);
 }
-template <int M, int NQB>
+template <int S, int M, int NQB>
 static void launch_small(const ScanParams& p, int pass, int g, size_t lds, hipStream_t s) {
-    if (p.dpad == 96) launch_small_g<M, NQB, 3>(p, pass, g, lds, s);
-    else if (p.dpad == 128) launch_small_g<M, NQB, 4>(p, pass, g, lds, s);
-    else launch_small_g<M, NQB, 0>(p, pass, g, lds, s);
+    if (p.dpad == 96) launch_small_g<S, M, NQB, 3>(p, pass, g, lds, s);
+    else if (p.dpad == 128) launch_small_g<S, M, NQB, 4>(p, pass, g, lds, s);
+    else launch_small_g<S, M, NQB, 0>(p, pass, g, lds, s);
+}
+template <int S, int M>
+static void launch_small_m(const ScanParams& p, int pass, int nqb16, size_t lds, hipStream_t s) {
+    if (nqb16 == 1) launch_small<S, M, 1>(p, pass, p.nsplit, lds, s);
+    else if (nqb16 == 2) launch_small<S, M, 2>(p, pass, p.nsplit, lds, s);
+    else launch_small<S, M, 4>(p, pass, p.nsplit, lds, s);
+}
+template <int S>
+static void launch_small_s(const ScanParams& p, int metric, int pass, int nqb16, size_t lds, hipStream_t s) {
+    if (metric == 0) launch_small_m<S, 0>(p, pass, nqb16, lds, s);
+    else launch_small_m<S, 1>(p, pass, nqb16, lds, s);
+}
+template <int S, int M>
+static void launch_tiled(const ScanParams& p, int pass, int g, hipStream_t s) {
+    if (pass == kPassSample) scan_filter_kernel<S, M, kPassSample><<<g, 256, 0, s>>>(p);
+    else if (pass == kPassRetry) scan_filter_kernel<S, M, kPassRetry><<<g, 256, 0, s>>>(p);
+    else if (pass == kPassArgmin) scan_filter_kernel<S, M, kPassArgmin><<<g, 256, 0, s>>>(p);
+    else scan_filter_kernel<S, M, kPassFull><<<g, 256, 0, s>>>(p);
+}
+template <int S>
+static void launch_tiled_s(const ScanParams& p, int metric, int pass, int g, hipStream_t s) {
+    if (metric == 0) launch_tiled<S, 0>(p, pass, g, s);
+    else launch_tiled<S, 1>(p, pass, g, s);
 }
 
-bool small_scan_fits(int nq, int dpad) {
+static size_t small_lds_bytes(int nq, int dpad, int storage) {
     const int nqb16 = nq <= 16 ? 1 : nq <= 32 ? 2 : 4;
-    return nq >= 1 && nq <= kSmallMaxQ && (size_t)16 * nqb16 * (dpad + 4) * 4 <= kSmallMaxLds;
+    const int es = elem_bytes(storage);
+    return (size_t)16 * nqb16 * (dpad + 16 / es) * es;
 }
 
-void launch_scan_filter(const ScanParams& p, int metric, int pass, hipStream_t s) {
-    if (pass != kPassArgmin && small_scan_fits(p.nq, p.dpad)) {
+bool small_scan_fits(int nq, int dpad, int storage) {
+    return nq >= 1 && nq <= kSmallMaxQ && small_lds_bytes(nq, dpad, storage) <= kSmallMaxLds;
+}
+
+void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, hipStream_t s) {
+    if (storage != kF32 && storage != kF16 && storage != kBF16)
+        throw std::runtime_error("scan_filter: unknown storage type");
+    if (pass != kPassArgmin && small_scan_fits(p.nq, p.dpad, storage)) {
         if (p.nsplit <= 0) return;
-        if (p.rows_per_split % kBM != 0 || p.cap < 1)
+        if (p.rows_per_split % kBM != 0 || p.cap < 1 || p.dpad % kBK != 0)
             throw std::runtime_error("scan_small: bad tiling parameters");
         const int nqb16 = p.nq <= 16 ? 1 : p.nq <= 32 ? 2 : 4;
-        const size_t lds = (size_t)16 * nqb16 * (p.dpad + 4) * sizeof(float);
+        const size_t lds = small_lds_bytes(p.nq, p.dpad, storage);
         void* tok;
         prof_begin(pass == kPassSample ? kFamScanSample : pass == kPassRetry ? kFamScanRetry : kFamScan, s, &tok);
-        if (metric == 0) {
-            if (nqb16 == 1) launch_small<0, 1>(p, pass, p.nsplit, lds, s);
-            else if (nqb16 == 2) launch_small<0, 2>(p, pass, p.nsplit, lds, s);
-            else launch_small<0, 4>(p, pass, p.nsplit, lds, s);
-        } else {
-            if (nqb16 == 1) launch_small<1, 1>(p, pass, p.nsplit, lds, s);
-            else if (nqb16 == 2) launch_small<1, 2>(p, pass, p.nsplit, lds, s);
-            else launch_small<1, 4>(p, pass, p.nsplit, lds, s);
-        }
+        if (storage == kF32) launch_small_s<kF32>(p, metric, pass, nqb16, lds, s);
+        else if (storage == kF16) launch_small_s<kF16>(p, metric, pass, nqb16, lds, s);
+        else launch_small_s<kBF16>(p, metric, pass, nqb16, lds, s);
         prof_end(tok, s);
         check_launch("scan_small");
         return;
@@ -1152,17 +1325,9 @@ void launch_scan_filter(const ScanParams& p, int metric, int pass, hipStream_t s
     prof_begin(pass == kPassSample ? kFamScanSample : pass == kPassRetry ? kFamScanRetry
                : pass == kPassArgmin ? kFamArgmin : kFamScan, s, &tok);
     const int g = (int)grid;
-    if (metric == 0) {
-        if (pass == kPassSample) scan_filter_kernel<0, kPassSample><<<g, 256, 0, s>>>(p);
-        else if (pass == kPassRetry) scan_filter_kernel<0, kPassRetry><<<g, 256, 0, s>>>(p);
-        else if (pass == kPassArgmin) scan_filter_kernel<0, kPassArgmin><<<g, 256, 0, s>>>(p);
-        else scan_filter_kernel<0, kPassFull><<<g, 256, 0, s>>>(p);
-    } else {
-        if (pass == kPassSample) scan_filter_kernel<1, kPassSample><<<g, 256, 0, s>>>(p);
-        else if (pass == kPassRetry) scan_filter_kernel<1, kPassRetry><<<g, 256, 0, s>>>(p);
-        else if (pass == kPassArgmin) scan_filter_kernel<1, kPassArgmin><<<g, 256, 0, s>>>(p);
-        else scan_filter_kernel<1, kPassFull><<<g, 256, 0, s>>>(p);
-    }
+    if (storage == kF32) launch_tiled_s<kF32>(p, metric, pass, g, s);
+    else if (storage == kF16) launch_tiled_s<kF16>(p, metric, pass, g, s);
+    else launch_tiled_s<kBF16>(p, metric, pass, g, s);
     prof_end(tok, s);
     check_launch("scan_filter");
 }

@@ -1,19 +1,28 @@
 // SPDX-License-Identifier: Apache-2.0
 // kernels.hpp -- device kernels of the flat-search hot path and their launchers.
 //
-// Data layout in HBM (all fp32):
-//   database  X, rows_pad = roundup(nb, kBM) rows of dpad = roundup(dim, kBK) columns,
-//             in 32 x 32 chunks ordered the way MFMA lanes consume them
-//             (blk_off below): a 32-row block occupies 32*dpad floats like a
-//             row-major block would, so row offsets of blocks are unchanged, but
-//             inside it each 4 KB chunk (32 rows x 32 columns) is laid out as
-//             [row half hh][float4 e][quarter q][row r16][4], i.e. element
-//             (row 16 hh + r16, column 8 q + 4 e + c). Lane q*16 + r16 of a wave
-//             then reads its operand float4 with one linear 1 KB load per
-//             (hh, e). Pad rows and pad columns are zero.
+// Storage types: the database and the queries of a search are held in one
+// element type, fp32 or (reduced-precision variants) fp16 / bf16 rounded to
+// nearest-even from the caller's fp32. Dots always accumulate in fp32; norms
+// are double sums of the stored values.
+//
+// Data layout in HBM:
+//   database  X, rows_pad = roundup(nb, kBM) rows of dpad = roundup(dim, 32)
+//             columns in 32 x 32 chunks ordered the way MFMA lanes consume them:
+//             a 32-row block occupies 32*dpad elements like a row-major block
+//             would, so row offsets of blocks are unchanged, but inside it each
+//             chunk (32 rows x 32 columns: 4 KB fp32, 2 KB fp16/bf16) is laid
+//             out so that lane q*16 + r16 of a wave reads a 16-byte operand
+//             piece of row (16 hh + r16) with one linear 1 KB load per piece:
+//               fp32       [row half hh][float4 e][quarter q][row r16][4]
+//                          = element (16 hh + r16, 8 q + 4 e + c)
+//               fp16/bf16  [row half hh][quarter q][row r16][8]
+//                          = element (16 hh + r16, 8 q + c)
+//             (blk_off / blk_off_h below). Pad rows and pad columns are zero.
 //   row norms xn[rows_pad]        ||x||^2, double-accumulated (reference
 //                                 src/Distance.h:40-47), pad entries zero
-//   queries   Q[nqb*kBN][dpad]    row-major, zero padded, qn[] likewise
+//   queries   Q[nqb*kBN][dpad]    row-major in the storage type, zero padded;
+//                                 qn[] (fp32) likewise
 //   candidates cand[nq][nsplit][cap] of (key bits, id), cnt[nq][nsplit]
 //
 // Ranking key (smaller = nearer), the value the reference's merge kernel ranks
@@ -32,12 +41,17 @@ namespace mflat_amd {
 
 constexpr int kBM = 128;   // database rows per scan tile
 constexpr int kBN = 128;   // queries per scan tile
-constexpr int kBK = 32;    // dimension chunk staged through LDS
+constexpr int kBK = 32;    // dpad granularity; fp32 columns per LDS-staged chunk
 constexpr int kSelLds = 4096;   // candidates a select block holds in LDS
 constexpr int kTopMax = 1024;   // largest k (== MFLAT_MAX_K)
 constexpr int kMaxSplit = 16384;  // most database splits one select block indexes
 constexpr int kSmallMaxQ = 64;                 // scan_small serves batches up to this size
 constexpr size_t kSmallMaxLds = 64 * 1024;     // ... whose query tile fits this much LDS
+
+// Element type of the stored database and of the queries (the ABI's
+// mflat_storage_t values).
+enum Storage { kF32 = 0, kF16 = 1, kBF16 = 2 };
+inline int elem_bytes(int storage) { return storage == kF32 ? 4 : 2; }
 
 enum KernelFamily {
     kFamScan = 0, kFamScanSample = 1, kFamScanRetry = 2, kFamSelect = 3, kFamArgmin = 4,
@@ -48,7 +62,7 @@ enum KernelFamily {
 // candidate regions, and the bound is each lane's running best.
 enum ScanPass { kPassFull = 0, kPassSample = 1, kPassRetry = 2, kPassArgmin = 3 };
 
-// Float offset of element (row, col) of the database in the chunked layout.
+// Element offset of (row, col) of an fp32 database in the chunked layout.
 __host__ __device__ inline int64_t blk_off(int64_t row, int col, int dpad) {
     const int64_t b = row >> 5;
     const int rr = (int)(row & 31);
@@ -56,16 +70,23 @@ __host__ __device__ inline int64_t blk_off(int64_t row, int col, int dpad) {
     return ((b * (dpad >> 5) + t) << 10) +
            ((((rr >> 4) * 2 + ((cc >> 2) & 1)) * 64 + (cc >> 3) * 16 + (rr & 15)) << 2) + (cc & 3);
 }
+// Element offset of (row, col) of an fp16 / bf16 database in the chunked layout.
+__host__ __device__ inline int64_t blk_off_h(int64_t row, int col, int dpad) {
+    const int64_t b = row >> 5;
+    const int rr = (int)(row & 31);
+    const int t = col >> 5, cc = col & 31;
+    return ((b * (dpad >> 5) + t) << 10) + ((((rr >> 4) * 4 + (cc >> 3)) * 16 + (rr & 15)) << 3) + (cc & 7);
+}
 
 struct ScanParams {
-    const float* X;          // database tile source (see layout above)
+    const void* X;           // database (storage type, chunked layout above)
     const float* xnorm;      // per-row ||x||^2 (L2 only)
     float xnorm_max;         // >= every finite ||x||^2 of the pass (L2 fast-reject margin)
     int64_t nrows;           // valid rows; rows >= nrows are padding
     int64_t rows_per_split;  // multiple of kBM
     int nsplit;              // database splits (grid = nqb * nsplit)
     int id_stride;           // reported id = row * id_stride (sample passes)
-    const float* Q;          // queries
+    const void* Q;           // queries (storage type, row-major)
     const float* qnorm;      // per-query ||q||^2 (L2 only)
     int nq;                  // valid queries
     int nqb;                 // query blocks of kBN
@@ -103,18 +124,24 @@ struct SelectParams {
 
 // Launchers (kernels.hip). All are asynchronous on `s` and bracket the launch
 // with the process-wide kernel timer when it is enabled.
-// row-major (queries)
+// row-major fp32 (queries)
 void launch_pack_rows(const float* src, int64_t n, int dim, float* dst, int64_t n_pad, int dpad,
                       hipStream_t s);
-void launch_row_norms(const float* v, int64_t n, int dpad, float* out, hipStream_t s);
 void launch_normalize_rows(float* v, int64_t n, int dpad, hipStream_t s);
-// chunked database layout: rows [row0, row0 + n) of X
-void launch_store_rows_blk(const float* src, int64_t n, int dim, float* X, int64_t row0, int dpad,
-                           hipStream_t s);
-void launch_row_norms_blk(const float* X, int64_t row0, int64_t n, int dpad, float* out, hipStream_t s);
-void launch_normalize_rows_blk(float* X, int64_t row0, int64_t n, int dpad, hipStream_t s);
-void launch_gather_rows_blk(const float* X, const int* idx, int n, int dpad, float* dst, hipStream_t s);
-void launch_gather_rows(const float* src, const int* idx, int n, int dpad, float* dst,
+// row-major storage-type rows: fp32 -> storage rounding, ||row||^2 of stored values
+void launch_round_rows(const float* src, int64_t count, int storage, void* dst, hipStream_t s);
+void launch_row_norms(const void* v, int64_t n, int dpad, int storage, float* out, hipStream_t s);
+// inv[r] = float(1 / sqrt(sum_c src[r][c]^2)) (double sum), 1 for zero rows
+void launch_row_inv_norms(const float* src, int64_t n, int dim, float* inv, hipStream_t s);
+// chunked database layout: rows [row0, row0 + n) of X; inv (nullable) scales row r first
+void launch_store_rows_blk(const float* src, int64_t n, int dim, const float* inv, void* X, int64_t row0,
+                           int dpad, int storage, hipStream_t s);
+void launch_row_norms_blk(const void* X, int64_t row0, int64_t n, int dpad, int storage, float* out,
+                          hipStream_t s);
+void launch_gather_rows_blk(const void* X, const int* idx, int n, int dpad, int storage, void* dst,
+                            hipStream_t s);
+// row-major rows of row_bytes (a multiple of 16): dst row r = src row idx[r], zero for n <= r < n_pad
+void launch_gather_rows(const void* src, const int* idx, int n, int row_bytes, void* dst,
                         int64_t n_pad, hipStream_t s);
 void launch_gather_f32(const float* src, const int* idx, int n, float* dst, hipStream_t s);
 struct TauSources {   // three per-query bound arrays a retry can draw from
@@ -128,8 +155,8 @@ void launch_fill_empty(int32_t* ids, float* vals, int64_t count, float empty, hi
 void launch_max_norm(const float* xn, int64_t n, unsigned* out, hipStream_t s);
 // Dispatches to scan_small (small batches, HBM-streaming) when small_scan_fits,
 // else to the MFMA-tiled scan_filter.
-bool small_scan_fits(int nq, int dpad);
-void launch_scan_filter(const ScanParams& p, int metric, int pass, hipStream_t s);
+bool small_scan_fits(int nq, int dpad, int storage);
+void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, hipStream_t s);
 void launch_select(const SelectParams& p, hipStream_t s);
 void launch_argmin_finalize(const unsigned long long* best, int nq, int metric, int32_t* ids, float* vals,
                             hipStream_t s);

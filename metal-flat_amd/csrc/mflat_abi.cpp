@@ -68,7 +68,7 @@ mflat_status_t guarded(F&& f) {
 struct mflat_flat_index {
     FlatIndex idx;
     std::mutex mu;
-    mflat_flat_index(int d, Metric m) : idx(d, m) {}
+    mflat_flat_index(int d, Metric m, mflat_amd::Storage st) : idx(d, m, st) {}
 };
 
 extern "C" {
@@ -103,13 +103,15 @@ MFLAT_API mflat_log_level_t mflat_log_level(void) {
     return static_cast<mflat_log_level_t>(mflat_amd::logLevel());
 }
 
-MFLAT_API mflat_flat_index_t* mflat_flat_create(int dim, mflat_metric_t metric, mflat_status_t* st) {
-    if (dim <= 0) {
+MFLAT_API mflat_flat_index_t* mflat_flat_create_ex(int dim, mflat_metric_t metric, mflat_storage_t storage,
+                                                   mflat_status_t* st) {
+    if (dim <= 0 || (storage != MFLAT_STORAGE_F32 && storage != MFLAT_STORAGE_F16 &&
+                     storage != MFLAT_STORAGE_BF16)) {
         if (st) *st = MFLAT_ERR_BAD_ARG;
         return nullptr;
     }
     try {
-        auto* h = new mflat_flat_index(dim, conv(metric));
+        auto* h = new mflat_flat_index(dim, conv(metric), static_cast<mflat_amd::Storage>(storage));
         if (st) *st = MFLAT_OK;
         return h;
     } catch (const std::bad_alloc&) {
@@ -119,6 +121,14 @@ MFLAT_API mflat_flat_index_t* mflat_flat_create(int dim, mflat_metric_t metric, 
         if (st) *st = MFLAT_ERR_INTERNAL;
         return nullptr;
     }
+}
+
+MFLAT_API mflat_flat_index_t* mflat_flat_create(int dim, mflat_metric_t metric, mflat_status_t* st) {
+    return mflat_flat_create_ex(dim, metric, MFLAT_STORAGE_F32, st);
+}
+
+MFLAT_API mflat_storage_t mflat_flat_storage(const mflat_flat_index_t* h) {
+    return h ? static_cast<mflat_storage_t>(h->idx.storage()) : MFLAT_STORAGE_F32;
 }
 
 MFLAT_API void mflat_flat_free(mflat_flat_index_t* h) { delete h; }

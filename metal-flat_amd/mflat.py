@@ -21,6 +21,11 @@ MFLAT_METRIC_L2 = 0
 MFLAT_METRIC_INNER_PRODUCT = 1
 MFLAT_METRIC_COSINE = 2
 
+MFLAT_STORAGE_F32 = 0
+MFLAT_STORAGE_F16 = 1
+MFLAT_STORAGE_BF16 = 2
+STORAGE_NAMES = {"f32": MFLAT_STORAGE_F32, "f16": MFLAT_STORAGE_F16, "bf16": MFLAT_STORAGE_BF16}
+
 MFLAT_OK = 0
 MFLAT_ERR_NULL_ARG = 1
 MFLAT_ERR_BAD_ARG = 2
@@ -41,6 +46,8 @@ SIGNATURES = {
     "mflat_set_log_level": (None, [c_int]),
     "mflat_log_level": (c_int, []),
     "mflat_flat_create": (c_void_p, [c_int, c_int, POINTER(c_int)]),
+    "mflat_flat_create_ex": (c_void_p, [c_int, c_int, c_int, POINTER(c_int)]),
+    "mflat_flat_storage": (c_int, [c_void_p]),
     "mflat_flat_free": (None, [c_void_p]),
     "mflat_flat_ready": (c_int, [c_void_p]),
     "mflat_flat_size": (c_int, [c_void_p]),
@@ -95,14 +102,20 @@ def _f32(a) -> np.ndarray:
 class FlatIndex:
     """Python view of one mflat_flat_index_t (reference FlatIndex.h:37-77)."""
 
-    def __init__(self, dim: int, metric: int = MFLAT_METRIC_L2):
+    def __init__(self, dim: int, metric: int = MFLAT_METRIC_L2, storage: int = MFLAT_STORAGE_F32):
+        """storage: MFLAT_STORAGE_F32 (the reference's mflat_flat_create) or a
+        reduced-precision type (mflat_flat_create_ex)."""
         lib = load()
         st = c_int(-1)
-        self._h = lib.mflat_flat_create(int(dim), int(metric), ctypes.byref(st))
+        if storage == MFLAT_STORAGE_F32:
+            self._h = lib.mflat_flat_create(int(dim), int(metric), ctypes.byref(st))
+        else:
+            self._h = lib.mflat_flat_create_ex(int(dim), int(metric), int(storage), ctypes.byref(st))
         if not self._h:
             raise MflatError(st.value, "mflat_flat_create")
         self.dim = int(dim)
         self.metric = int(metric)
+        self.storage = int(storage)
 
     def close(self) -> None:
         if getattr(self, "_h", None):

@@ -125,3 +125,47 @@ def brute_lex(db, q, k):
     lib().orc_brute_lex(db.ctypes.data, db.shape[0], db.shape[1], q.ctypes.data, q.shape[0], k,
                         ids.ctypes.data, vals.ctypes.data)
     return ids, vals
+
+
+# ---- reduced-precision storage (fp16 / bf16) --------------------------------
+# The reference stores fp32 only; the library's fp16 / bf16 storage variants are
+# checked against this oracle run on identically rounded inputs: the fp32
+# values rounded to nearest even (after the Cosine normalisation, in fp32),
+# then searched exactly in fp32.
+
+STORAGE_F32, STORAGE_F16, STORAGE_BF16 = 0, 1, 2
+
+
+def round_f16(x):
+    """fp32 -> IEEE binary16 (numpy's round-to-nearest-even cast) -> fp32."""
+    with np.errstate(over="ignore"):
+        return _f32(x).astype(np.float16).astype(np.float32)
+
+
+def round_bf16(x):
+    """fp32 -> bfloat16, round to nearest even on the upper 16 bits of the
+    pattern; NaN -> the quiet NaN 0x7fc0 -> fp32."""
+    x = _f32(x)
+    u = x.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32)
+    r[np.isnan(x)] = 0x7FC0
+    return (r << 16).astype(np.uint32).view(np.float32).reshape(x.shape)
+
+
+def round_storage(x, storage):
+    if storage == STORAGE_F32:
+        return _f32(x)
+    if storage == STORAGE_F16:
+        return round_f16(x)
+    if storage == STORAGE_BF16:
+        return round_bf16(x)
+    raise ValueError(storage)
+
+
+def storage_inputs(db, q, metric, storage):
+    """(db', q', metric') such that flat_search(db', q', k, metric') is the
+    exact answer for an index of this storage type: Cosine rows and queries are
+    normalised (reference rule) before rounding and then compared by dot."""
+    if metric == 2:
+        return (round_storage(normalize_rows(db), storage), round_storage(normalize_rows(q), storage), 1)
+    return round_storage(db, storage), round_storage(q, storage), metric

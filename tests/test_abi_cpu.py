@@ -53,6 +53,25 @@ def test_create_arguments():
     lib.mflat_flat_free(None)   # NULL is a no-op
 
 
+def test_create_ex_storage_arguments():
+    """Additive reduced-precision constructor: same checks as create, plus the
+    storage type, which must be one of the three defined values."""
+    lib = mflat.load()
+    st = ctypes.c_int(-1)
+    for bad in (-1, 3, 7):
+        assert not lib.mflat_flat_create_ex(8, 0, bad, ctypes.byref(st)) and st.value == mflat.MFLAT_ERR_BAD_ARG
+    assert not lib.mflat_flat_create_ex(0, 0, mflat.MFLAT_STORAGE_F16, ctypes.byref(st))
+    assert st.value == mflat.MFLAT_ERR_BAD_ARG
+    for storage in (mflat.MFLAT_STORAGE_F32, mflat.MFLAT_STORAGE_F16, mflat.MFLAT_STORAGE_BF16):
+        h = lib.mflat_flat_create_ex(5, 1, storage, ctypes.byref(st))
+        assert h and st.value == 0 and lib.mflat_flat_storage(h) == storage and lib.mflat_flat_dim(h) == 5
+        lib.mflat_flat_free(h)
+    h = lib.mflat_flat_create(5, 0, None)
+    assert lib.mflat_flat_storage(h) == mflat.MFLAT_STORAGE_F32
+    lib.mflat_flat_free(h)
+    assert lib.mflat_flat_storage(None) == mflat.MFLAT_STORAGE_F32
+
+
 def test_null_handles_and_arguments():
     lib = mflat.load()
     x = np.zeros((2, 4), np.float32)

@@ -193,3 +193,53 @@ def test_golden_flat_fixture():
         ids, vals = oracle.flat_search(x, q, k, metric=metric)
         assert np.array_equal(ids, g[name + "__ids"]), name
         assert np.array_equal(vals.view(np.uint32), g[name + "__vals"].view(np.uint32)), name
+
+
+# ---- reduced-precision rounding (oracle inputs for fp16 / bf16 storage) -------
+
+def test_round_bf16_matches_torch_and_closed_forms():
+    """bf16 rounding against torch's CPU conversion (round to nearest even) on
+    random values across magnitudes and on the cases a slip would break: exact
+    ties to even, overflow to inf, subnormals, signed zero, inf and NaN."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(21)
+    x = (rng.standard_normal(200_000) * np.exp(rng.uniform(-60, 60, 200_000))).astype(np.float32)
+    special = np.array([0.0, -0.0, 1.0, 1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, 1.0 + 2.0 ** -8 + 2.0 ** -20,
+                        3.3895314e38, 3.4e38, -3.4e38, np.inf, -np.inf, 1e-40, -1e-45, 2.0 ** -126],
+                       dtype=np.float32)
+    for v in (x, special):
+        a = oracle.round_bf16(v)
+        b = torch.from_numpy(v).to(torch.bfloat16).float().numpy()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    r = oracle.round_bf16(special)
+    assert r[3] == 1.0                      # tie -> even (mantissa 0)
+    assert r[4] == 1.0 + 2.0 ** -6          # tie -> even (rounds up)
+    assert r[5] == 1.0 + 2.0 ** -7          # above the tie -> up
+    assert np.isinf(r[7]) and r[7] > 0 and np.isinf(r[8]) and r[8] < 0
+    assert np.signbit(r[1]) and r[1] == 0.0
+    n = oracle.round_bf16(np.array([np.nan, -np.nan], np.float32))
+    assert np.all(n.view(np.uint32) == 0x7FC00000)
+
+
+def test_round_f16_closed_forms():
+    v = np.array([1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, 65504.0, 65519.0, 65520.0, 2.0 ** -24,
+                  2.0 ** -25, 255.0, -0.0], dtype=np.float32)
+    r = oracle.round_f16(v)
+    assert r[0] == 1.0 and r[1] == 1.0 + 2.0 ** -9       # ties to even
+    assert r[2] == 65504.0 and r[3] == 65504.0 and np.isinf(r[4])
+    assert r[5] == 2.0 ** -24 and r[6] == 0.0            # smallest subnormal; tie -> 0
+    assert r[7] == 255.0 and np.signbit(r[8])
+
+
+def test_storage_inputs_integer_data_is_identity():
+    """Integers 0..255 are exact in fp16 and bf16, so the storage oracle on C1-like
+    data is the fp32 oracle itself (the GPU's bit-exact reduced-precision tests
+    rest on this)."""
+    rng = np.random.default_rng(5)
+    x = rng.integers(0, 256, size=(500, 24)).astype(np.float32)
+    q = rng.integers(0, 256, size=(9, 24)).astype(np.float32)
+    for st in (oracle.STORAGE_F16, oracle.STORAGE_BF16):
+        xs, qs, m = oracle.storage_inputs(x, q, 0, st)
+        assert m == 0 and np.array_equal(xs, x) and np.array_equal(qs, q)
+    xs, qs, m = oracle.storage_inputs(x, q, 2, oracle.STORAGE_BF16)
+    assert m == 1 and np.array_equal(xs, oracle.round_bf16(oracle.normalize_rows(x)))
