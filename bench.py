@@ -14,9 +14,10 @@ roofline: the dominant kernel is scan_filter (fused MFMA distance tile +
 threshold filter over the full database, one launch per step). achieved =
 2 * nq * nb * d algorithmic FLOP per launch / its mean duration, timed with HIP
 events on the launch stream over the timed steps, against the dense MFMA peak
-of the storage type (fp32 157.3, fp16/bf16 2516.6 TFLOP/s); for HBM-bound
-small batches (C4, nq <= 16) the algorithmic bytes (database in its storage
-type + queries + results) per launch against 8 TB/s.
+of the storage type (fp32 157.3, fp16/bf16 2516.6 TFLOP/s) -- or, where the
+algorithmic bytes (database in its storage type + queries + results) at 8 TB/s
+take longer than the FLOP at peak (C4 fp32 nq <= 16, C4 fp16 at every nq),
+those bytes per launch against 8 TB/s.
 
 --storage f16 / bf16 runs the reduced-precision variant (database and queries
 rounded to that type, fp32 accumulation; mflat_flat_create_ex).
@@ -42,10 +43,19 @@ PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_F16_MFMA_TFLOPS = 2516.6   # dense fp16 / bf16
 PEAK_HBM_GBS = 8000.0
 
-# HBM bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE + WRITE_SIZE
-# runs scaled by a plain-copy calibration (profiles/scan_filter_c2.md). Reported as
-# roofline.traffic for the configuration it was measured on; null otherwise.
-MEASURED_TRAFFIC_BYTES = {"C2": 5.69e9}
+# Bytes per launch of the dominant kernel through L2's memory side, from rocprofv3
+# FETCH_SIZE + WRITE_SIZE runs scaled by a plain-copy calibration (x2.0, x1.0), as
+# committed under profiles/. Keyed by (config, nq, storage); reported as
+# roofline.traffic for the configuration it was measured on, null otherwise.
+MEASURED_TRAFFIC_BYTES = {
+    ("C2", 10_000, "f32"): 5.69e9,
+    ("C2", 10_000, "f16"): 2.167e9,
+    ("C3", 10_000, "f32"): 286.5e9,
+    ("C4", 1, "f32"): 3.880e9,
+    ("C4", 1, "f16"): 1.960e9,
+    ("C4", 64, "f16"): 1.972e9,
+    ("C5", 2_000_000, "f32"): 513.7e9,
+}
 
 WORKLOADS = {
     "C1": ("C1: flat L2, nb=100,000 x d=128 integer-valued U{0..255}, nq=1,000, k=10, seed 0", 0, 10),
@@ -76,8 +86,19 @@ def make_data(cfg, nq_override):
     raise SystemExit(f"unknown config {cfg}")
 
 
-def cpu_baseline(x, q, k, metric, gpu_ids, storage=0, seconds_target=12.0):
-    """Times the oracle (one core) on a prefix of the queries sized to ~10-15 s.
+def host_threads():
+    """Host cores this process may use (the GPU box grants 16 per GPU)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def cpu_baseline(x, q, k, metric, gpu_ids, storage=0, threads=1, seconds_target=12.0):
+    """Times the oracle on `threads` host cores (1 = the reference's serial
+    cpuSearch; more = parallel over queries, as the reference's bench,
+    bench/bench.mm:134-156) on a prefix of the queries sized to ~10-15 s.
     Reduced-precision storage: the oracle runs on the identically rounded inputs."""
     import numpy as np
     import oracle
@@ -86,22 +107,23 @@ def cpu_baseline(x, q, k, metric, gpu_ids, storage=0, seconds_target=12.0):
         x, q, metric = oracle.storage_inputs(x, q[:4096], metric, storage)
 
     nb, d = x.shape
-    # per-query cost ~ nb*d sequential fp32 steps; calibrate on one query
+    # per-query cost ~ nb*d sequential fp32 steps; calibrate on one query per thread
     t0 = time.perf_counter()
-    oracle.flat_search(x, q[:1], k, metric=metric, threads=1)
-    one = max(time.perf_counter() - t0, 1e-6)
+    oracle.flat_search(x, q[:threads], k, metric=metric, threads=threads)
+    one = max(time.perf_counter() - t0, 1e-6) / threads
     n = int(max(1, min(q.shape[0], seconds_target / one)))
     t0 = time.perf_counter()
-    oi, _ = oracle.flat_search(x, q[:n], k, metric=metric, threads=1)
+    oi, _ = oracle.flat_search(x, q[:n], k, metric=metric, threads=threads)
     dt = time.perf_counter() - t0
     recall = float(np.mean([len(set(oi[r].tolist()) & set(gpu_ids[r].tolist())) / k for r in range(n)]))
+    where = "one host core" if threads == 1 else f"{threads} host threads (queries split across them)"
     return {
         "value": n / dt,
         "unit": "queries/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
         "sample": f"first {n} of the {q.shape[0]} queries against all {nb} rows (d={d}, k={k}), "
-                  f"{dt:.1f} s on one host core; GPU/oracle id agreement on the sample {recall:.5f}",
+                  f"{dt:.1f} s on {where}; GPU/oracle id agreement on the sample {recall:.5f}",
     }
 
 
@@ -195,17 +217,19 @@ def main():
     # time (a search may be split into several launches when the query batch is
     # larger than the candidate workspace, e.g. C5).
     scan_s = scan["total_ms"] / 1000.0
-    if args.config == "C4" and nq <= 16:
-        byts = (nb * d * esize + nq * d * esize + nq * k * 8) * args.steps
-        ach = byts / scan_s / 1e9
+    # Bound: whichever of FLOP / peak and algorithmic bytes / HBM bandwidth is
+    # longer (database in its storage type + queries + ids and values out).
+    byts = nb * d * esize + nq * d * esize + nq * k * 8
+    peak = PEAK_FP32_MFMA_TFLOPS if esize == 4 else PEAK_F16_MFMA_TFLOPS
+    traffic = MEASURED_TRAFFIC_BYTES.get((args.config, nq, args.storage))
+    if byts / (PEAK_HBM_GBS * 1e9) > flop / (peak * 1e12):
+        ach = byts * args.steps / scan_s / 1e9
         roof = {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None}
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": traffic}
     else:
         ach = flop * args.steps / scan_s / 1e12
-        peak = PEAK_FP32_MFMA_TFLOPS if esize == 4 else PEAK_F16_MFMA_TFLOPS
         roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
-                "frac": round(ach / peak, 4),
-                "traffic": MEASURED_TRAFFIC_BYTES.get(args.config) if args.nq == 0 and esize == 4 else None}
+                "frac": round(ach / peak, 4), "traffic": traffic}
 
     out = {
         "metric": "QPS + % of MFMA/HBM roofline, flat L2 d=128 nb=1M k=100 (1 GPU)",
@@ -227,9 +251,22 @@ def main():
         "roofline": roof,
         "kernels": kern,
     }
+    # The reference's own host-pointer entry point on the same batch: includes
+    # the H2D copy of the queries and the D2H copy of ids and values (PCIe).
+    idx.search(q, k)   # first call sizes the host-entry staging buffers
+    t0 = time.perf_counter()
+    for _ in range(2):
+        idx.search(q, k)
+    host_ms = (time.perf_counter() - t0) * 1000.0 / 2
+    out["host_api"] = {"entry": "mflat_flat_search (host buffers, PCIe copies included)",
+                       "ms_per_step": round(host_ms, 4), "queries_per_s": round(nq * 1000.0 / host_ms, 2)}
+    log(f"[bench] host entry {host_ms:.3f} ms/step")
     if not args.no_cpu_baseline:
-        log("[bench] cpu baseline ...")
+        log("[bench] cpu baseline (1 core) ...")
         out["cpu_baseline"] = cpu_baseline(x, q, k, metric, gpu_ids, storage)
+        nt = host_threads()
+        log(f"[bench] cpu baseline ({nt} threads) ...")
+        out["cpu_baseline_all_cores"] = cpu_baseline(x, q, k, metric, gpu_ids, storage, threads=nt)
         log("[bench] cpu baseline done")
     idx.close()
     print(json.dumps(out), flush=True)

@@ -127,6 +127,14 @@ mflat_flat_create_ex(int dim, mflat_metric_t metric, mflat_storage_t storage, mf
 /* storage type of the index (MFLAT_STORAGE_F32 for NULL) */
 MFLAT_API mflat_storage_t mflat_flat_storage(const mflat_flat_index_t*);
 
+/* ---------------- Additive: 64-bit ids ----------------------------------- */
+/* No counterpart in the reference (its ids are int32, c/include/mflat.h:84-90).
+   Same arguments, checks, status codes and results as mflat_flat_search, with
+   the ids widened to int64 (-1 padding stays -1), for callers whose id type is
+   64-bit. */
+MFLAT_API mflat_status_t mflat_flat_search_i64(mflat_flat_index_t*, const float* queries,
+        int m, int k, int64_t* out_ids, float* out_distances, int* out_k_used);
+
 /* ---------------- Additive: device-resident data ------------------------- */
 /* No counterpart in the reference (its buffers are unified memory,
    src/FlatIndex.mm:163-171). For callers whose data already lives in HBM.

@@ -5,10 +5,12 @@
 // the engine plus a std::mutex that serialises add / reset / search per handle;
 // every entry point is a try/catch that maps exceptions to status codes;
 // results are copied into caller-owned buffers with row stride k_used.
+#include <algorithm>
 #include <atomic>
 #include <cstring>
 #include <mutex>
 #include <new>
+#include <vector>
 
 #include "../../include/mflat.h"
 #include "flat_index.hpp"
@@ -166,6 +168,26 @@ MFLAT_API mflat_status_t mflat_flat_search(mflat_flat_index_t* h, const float* q
     return guarded([&] {
         std::lock_guard<std::mutex> lk(h->mu);
         const int used = h->idx.search(q, m, k, oi, od);
+        if (ok) *ok = used;
+        return MFLAT_OK;
+    });
+}
+
+MFLAT_API mflat_status_t mflat_flat_search_i64(mflat_flat_index_t* h, const float* q, int m, int k,
+                                               int64_t* oi, float* od, int* ok) {
+    if (!h || !q) return MFLAT_ERR_NULL_ARG;
+    if (m < 0 || k < 1) return MFLAT_ERR_BAD_ARG;
+    if (m == 0) {
+        if (ok) *ok = 0;
+        return MFLAT_OK;
+    }
+    return guarded([&] {
+        std::lock_guard<std::mutex> lk(h->mu);
+        std::vector<int32_t> ids32;
+        if (oi) ids32.resize((size_t)m * std::min(std::max(k, 1), MFLAT_MAX_K));
+        const int used = h->idx.search(q, m, k, oi ? ids32.data() : nullptr, od);
+        if (oi)
+            for (size_t i = 0; i < (size_t)m * used; ++i) oi[i] = ids32[i];
         if (ok) *ok = used;
         return MFLAT_OK;
     });

@@ -55,6 +55,7 @@ SIGNATURES = {
     "mflat_flat_add": (c_int, [c_void_p, c_void_p, c_int]),
     "mflat_flat_reset": (c_int, [c_void_p]),
     "mflat_flat_search": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, POINTER(c_int)]),
+    "mflat_flat_search_i64": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, POINTER(c_int)]),
     "mflat_flat_search_device": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p,
                                          POINTER(c_int), c_void_p]),
     "mflat_flat_add_device": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
@@ -165,6 +166,20 @@ class FlatIndex:
         flat_i = ids.reshape(-1)[: m * ku].reshape(m, ku)
         flat_d = dist.reshape(-1)[: m * ku].reshape(m, ku)
         return flat_i.copy(), flat_d.copy(), ku
+
+    def search_i64(self, queries, k: int):
+        """mflat_flat_search_i64: as search, ids int64."""
+        q = _f32(queries).reshape(-1, self.dim)
+        m = q.shape[0]
+        kk = max(1, min(int(k), load().mflat_max_k()))
+        ids = np.full((max(m, 1), kk), -7, dtype=np.int64)
+        dist = np.full((max(m, 1), kk), np.nan, dtype=np.float32)
+        used = c_int(-1)
+        _check(load().mflat_flat_search_i64(self._h, q.ctypes.data, m, int(k), ids.ctypes.data,
+                                             dist.ctypes.data, ctypes.byref(used)), "mflat_flat_search_i64")
+        ku = used.value
+        return (ids.reshape(-1)[: m * ku].reshape(m, ku).copy(),
+                dist.reshape(-1)[: m * ku].reshape(m, ku).copy(), ku)
 
     # ---- device-pointer entry points ----
     # x / q / outputs: any object with .data_ptr() and .shape holding contiguous

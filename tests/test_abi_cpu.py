@@ -91,6 +91,13 @@ def test_null_handles_and_arguments():
         # m == 0: OK with k_used = 0 (reference c/mflat.cpp:44), before any device use
         assert lib.mflat_flat_search(h, x.ctypes.data, 0, 5, None, None, ctypes.byref(used)) == 0
         assert used.value == 0
+        for fn in (lib.mflat_flat_search, lib.mflat_flat_search_i64):   # same checks on the int64-id entry
+            assert fn(None, x.ctypes.data, 1, 1, None, None, None) == mflat.MFLAT_ERR_NULL_ARG
+            assert fn(h, None, 1, 1, None, None, None) == mflat.MFLAT_ERR_NULL_ARG
+            assert fn(h, x.ctypes.data, -1, 1, None, None, None) == mflat.MFLAT_ERR_BAD_ARG
+            assert fn(h, x.ctypes.data, 1, 0, None, None, None) == mflat.MFLAT_ERR_BAD_ARG
+            used.value = -1
+            assert fn(h, x.ctypes.data, 0, 5, None, None, ctypes.byref(used)) == 0 and used.value == 0
         assert lib.mflat_flat_search_device(h, None, 1, 1, None, None, None, None) == mflat.MFLAT_ERR_NULL_ARG
         assert lib.mflat_flat_search_device(h, x.ctypes.data, 1, 0, None, None, None, None) == mflat.MFLAT_ERR_BAD_ARG
         assert lib.mflat_flat_add_device(h, x.ctypes.data, -2, None) == mflat.MFLAT_ERR_BAD_ARG

@@ -175,6 +175,20 @@ def test_incremental_add_and_reset(gpu_ok):
         assert np.all(ri == -1)
 
 
+def test_int64_ids_match_int32(gpu_ok):
+    """mflat_flat_search_i64 returns the int32 entry's results widened, -1 padding kept."""
+    x, q = datagen.sift_like(nb=60, nq=9, seed=6)
+    with mflat.FlatIndex(x.shape[1], L2) as idx:
+        idx.add(x)
+        for k in (5, 100):
+            gi, gd, ku = idx.search(q, k)
+            li, ld, ku64 = idx.search_i64(q, k)
+            assert ku64 == ku and li.dtype == np.int64
+            assert np.array_equal(li, gi.astype(np.int64)) and np.array_equal(ld, gd)
+    oi, od = orc(x, q, 100, L2)
+    parity.exact(li.astype(np.int32), ld, oi, od)
+
+
 def test_device_entry_matches_host(gpu_ok):
     import hipmem
 
