@@ -627,6 +627,308 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// scan_resident: query tile resident in LDS, database streamed per wave
+// ---------------------------------------------------------------------------
+//
+// For batches of more than 64 queries whose 128-query tile fits in LDS (fp32
+// dpad <= 128, fp16/bf16 dpad <= 256). A workgroup owns one query block and
+// one split, as in scan_filter, but stages only the queries, once: they stay
+// in LDS for the workgroup's lifetime as the MFMA B operand. Each wave then
+// walks 64-row slices of the split on its own (slices w, w + 4, ...), loading
+// its A operand straight from the chunked database layout into registers, so
+// the main loop has no barriers and no LDS writes. A wave computes 64 rows x
+// 128 queries per slice as 2 x 4 blocks of 32 x 32 (v_mfma_f32_32x32x2_f32 or
+// v_mfma_f32_32x32x16_{f16,bf16}); lane l holds rows 8*(r/4) + 4*(l/32) +
+// (r%4) of query l%32 of each block, as in scan_filter, whose filter epilogue
+// this kernel shares.
+// Operand pieces (16 bytes, lane half h = l/32, row r32 = l%32):
+//   fp32, 8-column group g of a chunk: columns 8g + 4h .. +3 (MFMA step j
+//         pairs columns 8g + j and 8g + 4 + j), chunk piece
+//         ((r32/16)*2 + h)*64 + g*16 + r32%16 of blk_off's order;
+//   fp16/bf16, 16-column step s: columns 16s + 8h .. +7, chunk piece
+//         ((r32/16)*4 + 2s + h)*16 + r32%16 of blk_off_h's order.
+// G > 0 (fp16/bf16, dpad = 32 G <= 128): a whole slice is buffered in
+// registers and each chunk slot is refilled with the next slice's chunk as
+// soon as its MFMAs are issued (about one slice of prefetch: the fp16 MFMAs
+// consume a chunk in ~512 cycles, far less than a memory round trip). G == 0: one chunk
+// of prefetch (fp32, whose chunk takes ~8k cycles of MFMA, and larger dpad).
+// Prefetches are issued unconditionally (the last slice re-reads itself) so
+// every wait on them is a static count.
+template <int S, int METRIC, int PASS, int G>
+__global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
+    constexpr int ES = S == kF32 ? 4 : 2;
+    constexpr int NK = S == kF32 ? 4 : 2;          // operand pieces per row block per chunk
+    constexpr int KSTEP = S == kF32 ? 256 : 512;   // byte step between a lane's pieces in a chunk
+    constexpr int CB = 32 * 32 * ES;               // bytes per 32 x 32 chunk
+    extern __shared__ __attribute__((aligned(16))) float sQr[];   // [kBN][dpad + 16 / ES] elements
+    __shared__ __attribute__((aligned(16))) float sXn[4 * 64];    // per wave: its slice's row norms
+    __shared__ int sCnt[kBN];
+    __shared__ unsigned long long sBest[kBN];
+
+    // Workgroup -> (query block, split): the XCD grouping of scan_filter.
+    const int nwg = gridDim.x;
+    const int bid = blockIdx.x;
+    const int full = (nwg / 8) * 8;
+    const int v = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
+    const int grpSize = p.nqb < kQGroup ? p.nqb : kQGroup;
+    const int grp = v / (grpSize * p.nsplit);
+    const int r = v - grp * grpSize * p.nsplit;
+    const int inGrp = p.nqb - grp * grpSize < grpSize ? p.nqb - grp * grpSize : grpSize;
+    const int split = r / inGrp;
+    const int qb = grp * grpSize + (r - split * inGrp);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int r32 = lane & 31;
+    const int h = lane >> 5;
+    const int ldqB = (p.dpad + 16 / ES) * ES;   // LDS query row stride (bytes): 16 B of padding
+
+    {
+        const int rowP = p.dpad * ES / 16;
+        const fx4* qg = (const fx4*)p.Q + (int64_t)qb * kBN * rowP;
+        for (int i = tid; i < kBN * rowP; i += 256) {
+            const int row = i / rowP;
+            const int c = i - row * rowP;
+            *(fx4*)((char*)sQr + row * ldqB + c * 16) = qg[(int64_t)row * rowP + c];
+        }
+    }
+    if (tid < kBN) {
+        sCnt[tid] = 0;
+        sBest[tid] = ~0ull;
+    }
+
+    // Per-lane query state for its 4 query blocks; bounds as in scan_filter.
+    float tk[4], qn[4], ft[4];
+    int ti[4];
+    bool qv[4];
+#pragma unroll
+    for (int bn = 0; bn < 4; ++bn) {
+        const int q = qb * kBN + bn * 32 + r32;
+        qv[bn] = q < p.nq;
+        if (PASS == kPassArgmin) {
+            tk[bn] = INFINITY;
+            ti[bn] = -1;
+        } else {
+            tk[bn] = qv[bn] ? p.tau_key[q] : 0.0f;
+            ti[bn] = qv[bn] ? p.tau_id[q] : -1;
+        }
+        qn[bn] = (METRIC == 0 && qv[bn]) ? p.qnorm[q] : 0.0f;
+        if (METRIC == 0) {
+            const float m = 0x1p-20f * (tk[bn] + 2.0f * qn[bn] + 2.0f * p.xnorm_max);
+            ft[bn] = qv[bn] ? (tk[bn] - qn[bn]) + m : -INFINITY;
+        } else {
+            ft[bn] = qv[bn] ? -tk[bn] : INFINITY;
+        }
+    }
+    __syncthreads();
+
+    const int64_t rows_pad = (p.nrows + kBM - 1) / kBM * kBM;
+    const int64_t rowBeg = (int64_t)split * p.rows_per_split;
+    int64_t rowEnd = rowBeg + p.rows_per_split;
+    if (rowEnd > rows_pad) rowEnd = rows_pad;
+    const int nsl = rowEnd > rowBeg ? (int)((rowEnd - rowBeg) / 64) : 0;
+    const int nchunk = p.dpad / 32;
+    const int64_t blkB = (int64_t)32 * p.dpad * ES;
+    const char* xw = (const char*)p.X + rowBeg * p.dpad * ES +
+                     (S == kF32 ? ((r32 >> 4) * 2 + h) * 1024 : ((r32 >> 4) * 4 + h) * 256) + (r32 & 15) * 16;
+    const char* qlds = (const char*)sQr + r32 * ldqB + h * 16;
+    auto lda = [&](int sl, int bm, int t, int k) -> fx4 {
+        return __builtin_nontemporal_load((const fx4*)(xw + (int64_t)(2 * sl + bm) * blkB + t * CB + k * KSTEP));
+    };
+    auto ldb = [&](int bn, int t, int k) -> fx4 {
+        return *(const fx4*)(qlds + bn * 32 * ldqB + t * 32 * ES + k * 32);
+    };
+
+    fx16 acc[2][4];
+    // One chunk of MFMAs from operand pieces a[bm][k]; a slice's first chunk
+    // starts every accumulator from an inline zero.
+    auto mma = [&](const fx4 (&a)[2][NK], int t, auto zeroTag) {
+        constexpr bool ZERO = decltype(zeroTag)::value;
+        const fx16 z = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f,
+                        0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            fx4 b[4];
+#pragma unroll
+            for (int bn = 0; bn < 4; ++bn) b[bn] = ldb(bn, t, k);
+            if constexpr (S == kF32) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+                        for (int bn = 0; bn < 4; ++bn)
+                            acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                                a[bm][k][j], b[bn][j], (ZERO && k == 0 && j == 0) ? z : acc[bm][bn], 0, 0, 0);
+            } else {
+#pragma unroll
+                for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+                    for (int bn = 0; bn < 4; ++bn)
+                        acc[bm][bn] = mfma32x32x16<S>(a[bm][k], b[bn], (ZERO && k == 0) ? z : acc[bm][bn]);
+            }
+        }
+    };
+
+    // Filter epilogue of slice sl (rows rowBeg + 64 sl ..), whose row norms
+    // this lane holds for row `lane` in xnv.
+    auto epilogue = [&](int sl, float xnv) {
+        if (METRIC == 0) {
+            sXn[wave * 64 + lane] = xnv;
+            __builtin_amdgcn_wave_barrier();
+        }
+#pragma unroll
+        for (int bm = 0; bm < 2; ++bm) {
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int rl = bm * 32 + g4 * 8 + h * 4;
+                const int64_t r0 = rowBeg + (int64_t)sl * 64 + rl;
+                fx4 xn4 = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (METRIC == 0) xn4 = *(const fx4*)(sXn + wave * 64 + rl);
+#pragma unroll
+                for (int bp = 0; bp < 2; ++bp) {
+                    bool f[4][2];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int b = 0; b < 2; ++b) {
+                            const float dot = acc[bm][2 * bp + b][g4 * 4 + i];
+                            f[i][b] = METRIC == 0 ? fmaf(-2.0f, dot, xn4[i]) <= ft[2 * bp + b] : dot >= ft[2 * bp + b];
+                        }
+                    const bool any = f[0][0] | f[0][1] | f[1][0] | f[1][1] | f[2][0] | f[2][1] |
+                                     f[3][0] | f[3][1];
+                    if (!any) continue;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int64_t row = r0 + i;
+                        const bool rv = row < p.nrows;
+                        const int id = (int)(row * p.id_stride);
+#pragma unroll
+                        for (int b = 0; b < 2; ++b) {
+                            const int bn = 2 * bp + b;
+                            if (!f[i][b]) continue;
+                            const float dot = acc[bm][bn][g4 * 4 + i];
+                            float key;
+                            if (METRIC == 0) {
+                                const float t = fmaf(-2.0f, dot, qn[bn] + xn4[i]);
+                                key = (t < 0.0f ? 0.0f : t) + 0.0f;
+                            } else {
+                                key = -dot + 0.0f;
+                            }
+                            if (PASS == kPassArgmin) {
+                                if (rv && qv[bn] && (key < tk[bn] || (key == tk[bn] && id < ti[bn]))) {
+                                    tk[bn] = key;
+                                    ti[bn] = id;
+                                    ft[bn] = METRIC == 0
+                                        ? (key - qn[bn]) + 0x1p-20f * (key + 2.0f * qn[bn] + 2.0f * p.xnorm_max)
+                                        : -key;
+                                }
+                                continue;
+                            }
+                            const bool pass = rv && qv[bn] && (key < tk[bn] || (key == tk[bn] && id <= ti[bn]));
+                            if (pass) {
+                                const int ql = bn * 32 + r32;
+                                const int slot = atomicAdd(&sCnt[ql], 1);
+                                if (slot < p.cap) {
+                                    const int64_t q = (int64_t)qb * kBN + ql;
+                                    p.cand[(q * p.nsplit + split) * p.cap + slot] =
+                                        make_uint2(__float_as_uint(key), (unsigned)id);
+                                }
+                            }
+                        }
+                    }
+                }
+            }
+        }
+    };
+
+    auto norm = [&](int sl) -> float {
+        return METRIC == 0 ? p.xnorm[rowBeg + (int64_t)sl * 64 + lane] : 0.0f;
+    };
+
+    if constexpr (G > 0) {
+        fx4 buf[G][2][NK];
+        float xnv = 0.0f;
+        if (wave < nsl) {
+            xnv = norm(wave);
+#pragma unroll
+            for (int t = 0; t < G; ++t)
+#pragma unroll
+                for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+                    for (int k = 0; k < NK; ++k) buf[t][bm][k] = lda(wave, bm, t, k);
+        }
+        for (int sl = wave; sl < nsl; sl += 4) {
+            const int nx = sl + 4 < nsl ? sl + 4 : sl;
+            const float xnNext = norm(nx);
+#pragma unroll
+            for (int t = 0; t < G; ++t) {
+                if (t == 0) mma(buf[t], t, std::true_type{});
+                else mma(buf[t], t, std::false_type{});
+#pragma unroll
+                for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+                    for (int k = 0; k < NK; ++k) buf[t][bm][k] = lda(nx, bm, t, k);
+            }
+            epilogue(sl, xnv);
+            xnv = xnNext;
+        }
+    } else {
+        fx4 cur[2][NK];
+        float xnv = 0.0f;
+        if (wave < nsl) {
+            xnv = norm(wave);
+#pragma unroll
+            for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+                for (int k = 0; k < NK; ++k) cur[bm][k] = lda(wave, bm, 0, k);
+        }
+        for (int sl = wave; sl < nsl; sl += 4) {
+            const int nxs = sl + 4 < nsl ? sl + 4 : sl;
+            const float xnNext = norm(nxs);
+            for (int t = 0; t < nchunk; ++t) {
+                const bool lastT = t + 1 == nchunk;
+                const int ns = lastT ? nxs : sl;
+                const int ntc = lastT ? 0 : t + 1;
+                fx4 nxt[2][NK];
+#pragma unroll
+                for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+                    for (int k = 0; k < NK; ++k) nxt[bm][k] = lda(ns, bm, ntc, k);
+                if (t == 0) mma(cur, t, std::true_type{});
+                else mma(cur, t, std::false_type{});
+#pragma unroll
+                for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+                    for (int k = 0; k < NK; ++k) cur[bm][k] = nxt[bm][k];
+            }
+            epilogue(sl, xnv);
+            xnv = xnNext;
+        }
+    }
+
+    if (PASS == kPassArgmin) {
+#pragma unroll
+        for (int bn = 0; bn < 4; ++bn)
+            if (ti[bn] >= 0)
+                atomicMin(&sBest[bn * 32 + r32],
+                          ((unsigned long long)key_to_ord(__float_as_uint(tk[bn])) << 32) | (unsigned)ti[bn]);
+        __syncthreads();
+        if (tid < kBN) {
+            const int q = qb * kBN + tid;
+            if (q < p.nq && sBest[tid] != ~0ull) atomicMin(&p.best[q], sBest[tid]);
+        }
+        return;
+    }
+    __syncthreads();
+    if (tid < kBN) {
+        const int q = qb * kBN + tid;
+        if (q < p.nq) p.cnt[(int64_t)q * p.nsplit + split] = sCnt[tid];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // scan_small: the same filter for small batches (nq <= 64), HBM-streaming
 // ---------------------------------------------------------------------------
 //
@@ -1275,6 +1577,50 @@ static void launch_small_s(const ScanParams& p, int metric, int pass, int nqb16,
     if (metric == 0) launch_small_m<S, 0>(p, pass, nqb16, lds, s);
     else launch_small_m<S, 1>(p, pass, nqb16, lds, s);
 }
+// Raises a kernel's dynamic-LDS limit to kResidentMaxLds (needed above the
+// default per-launch limit); throws if the runtime refuses.
+static void allow_resident_lds(const void* f) {
+    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kResidentMaxLds) != hipSuccess)
+        throw std::runtime_error("scan_resident: cannot raise the dynamic LDS limit");
+}
+template <int S, int M, int P, int G>
+static void launch_resident_p(const ScanParams& p, int g, size_t lds, hipStream_t s) {
+    static const bool ok = (allow_resident_lds((const void*)scan_resident_kernel<S, M, P, G>), true);
+    (void)ok;
+    scan_resident_kernel<S, M, P, G><<<g, 256, lds, s>>>(p);
+}
+template <int S, int M, int G>
+static void launch_resident_g(const ScanParams& p, int pass, int g, size_t lds, hipStream_t s) {
+    if (pass == kPassSample) launch_resident_p<S, M, kPassSample, G>(p, g, lds, s);
+    else if (pass == kPassRetry) launch_resident_p<S, M, kPassRetry, G>(p, g, lds, s);
+    else launch_resident_p<S, M, kPassFull, G>(p, g, lds, s);
+}
+// k = 1 keeps a running best per lane instead of stores; it always takes the
+// one-chunk-prefetch loop.
+template <int S, int M>
+static void launch_resident(const ScanParams& p, int pass, int g, size_t lds, hipStream_t s) {
+    if (pass == kPassArgmin) return launch_resident_p<S, M, kPassArgmin, 0>(p, g, lds, s);
+    if constexpr (S != kF32) {
+        if (p.dpad == 96) return launch_resident_g<S, M, 3>(p, pass, g, lds, s);
+        if (p.dpad == 128) return launch_resident_g<S, M, 4>(p, pass, g, lds, s);
+    }
+    launch_resident_g<S, M, 0>(p, pass, g, lds, s);
+}
+template <int S>
+static void launch_resident_s(const ScanParams& p, int metric, int pass, int g, size_t lds, hipStream_t s) {
+    if (metric == 0) launch_resident<S, 0>(p, pass, g, lds, s);
+    else launch_resident<S, 1>(p, pass, g, lds, s);
+}
+
+static size_t resident_lds_bytes(int dpad, int storage) {
+    const int es = elem_bytes(storage);
+    return (size_t)kBN * (dpad + 16 / es) * es;
+}
+
+bool resident_scan_fits(int dpad, int storage) {
+    return resident_lds_bytes(dpad, storage) <= kResidentMaxLds;
+}
+
 template <int S, int M>
 static void launch_tiled(const ScanParams& p, int pass, int g, hipStream_t s) {
     if (pass == kPassSample) scan_filter_kernel<S, M, kPassSample><<<g, 256, 0, s>>>(p);
@@ -1325,6 +1671,15 @@ void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, 
     prof_begin(pass == kPassSample ? kFamScanSample : pass == kPassRetry ? kFamScanRetry
                : pass == kPassArgmin ? kFamArgmin : kFamScan, s, &tok);
     const int g = (int)grid;
+    if (resident_scan_fits(p.dpad, storage)) {
+        const size_t lds = resident_lds_bytes(p.dpad, storage);
+        if (storage == kF32) launch_resident_s<kF32>(p, metric, pass, g, lds, s);
+        else if (storage == kF16) launch_resident_s<kF16>(p, metric, pass, g, lds, s);
+        else launch_resident_s<kBF16>(p, metric, pass, g, lds, s);
+        prof_end(tok, s);
+        check_launch("scan_resident");
+        return;
+    }
     if (storage == kF32) launch_tiled_s<kF32>(p, metric, pass, g, s);
     else if (storage == kF16) launch_tiled_s<kF16>(p, metric, pass, g, s);
     else launch_tiled_s<kBF16>(p, metric, pass, g, s);

@@ -47,6 +47,7 @@ constexpr int kTopMax = 1024;   // largest k (== MFLAT_MAX_K)
 constexpr int kMaxSplit = 16384;  // most database splits one select block indexes
 constexpr int kSmallMaxQ = 64;                 // scan_small serves batches up to this size
 constexpr size_t kSmallMaxLds = 64 * 1024;     // ... whose query tile fits this much LDS
+constexpr size_t kResidentMaxLds = 76 * 1024;  // scan_resident: largest resident query tile
 
 // Element type of the stored database and of the queries (the ABI's
 // mflat_storage_t values).
@@ -154,8 +155,10 @@ void launch_fill_tau_none(float* key, int* id, int n, hipStream_t s);
 void launch_fill_empty(int32_t* ids, float* vals, int64_t count, float empty, hipStream_t s);
 void launch_max_norm(const float* xn, int64_t n, unsigned* out, hipStream_t s);
 // Dispatches to scan_small (small batches, HBM-streaming) when small_scan_fits,
-// else to the MFMA-tiled scan_filter.
+// else to scan_resident when the 128-query tile fits in LDS
+// (resident_scan_fits), else to the LDS-tiled scan_filter.
 bool small_scan_fits(int nq, int dpad, int storage);
+bool resident_scan_fits(int dpad, int storage);
 void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, hipStream_t s);
 void launch_select(const SelectParams& p, hipStream_t s);
 void launch_argmin_finalize(const unsigned long long* best, int nq, int metric, int32_t* ids, float* vals,
