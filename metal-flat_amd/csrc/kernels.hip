@@ -653,7 +653,10 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
 // consume a chunk in ~512 cycles, far less than a memory round trip). G == 0: one chunk
 // of prefetch (fp32, whose chunk takes ~8k cycles of MFMA, and larger dpad).
 // Prefetches are issued unconditionally (the last slice re-reads itself) so
-// every wait on them is a static count.
+// every wait on them is a static count. Database loads are ordinary (cached):
+// the workgroups of up to kQGroup query blocks resident on one XCD read the
+// same split at about the same time and share it through that XCD's L2 (a
+// non-temporal hint here cost 7% at d = 128 fp32 and 16% with fp16 storage).
 template <int S, int METRIC, int PASS, int G>
 __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     constexpr int ES = S == kF32 ? 4 : 2;
@@ -734,7 +737,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
                      (S == kF32 ? ((r32 >> 4) * 2 + h) * 1024 : ((r32 >> 4) * 4 + h) * 256) + (r32 & 15) * 16;
     const char* qlds = (const char*)sQr + r32 * ldqB + h * 16;
     auto lda = [&](int sl, int bm, int t, int k) -> fx4 {
-        return __builtin_nontemporal_load((const fx4*)(xw + (int64_t)(2 * sl + bm) * blkB + t * CB + k * KSTEP));
+        return *(const fx4*)(xw + (int64_t)(2 * sl + bm) * blkB + t * CB + k * KSTEP);
     };
     auto ldb = [&](int bn, int t, int k) -> fx4 {
         return *(const fx4*)(qlds + bn * 32 * ldqB + t * 32 * ES + k * 32);
