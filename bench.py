@@ -48,13 +48,13 @@ PEAK_HBM_GBS = 8000.0
 # committed under profiles/. Keyed by (config, nq, storage); reported as
 # roofline.traffic for the configuration it was measured on, null otherwise.
 MEASURED_TRAFFIC_BYTES = {
-    ("C2", 10_000, "f32"): 5.69e9,
-    ("C2", 10_000, "f16"): 2.167e9,
+    ("C2", 10_000, "f32"): 4.82e9,
+    ("C2", 10_000, "f16"): 2.457e9,
     ("C3", 10_000, "f32"): 286.5e9,
     ("C4", 1, "f32"): 3.880e9,
     ("C4", 1, "f16"): 1.960e9,
     ("C4", 64, "f16"): 1.972e9,
-    ("C5", 2_000_000, "f32"): 513.7e9,
+    ("C5", 2_000_000, "f32"): 34.27e9,
 }
 
 WORKLOADS = {
