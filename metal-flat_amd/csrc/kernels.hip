@@ -667,6 +667,16 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     __shared__ __attribute__((aligned(16))) float sXn[4 * 64];    // per wave: its slice's row norms
     __shared__ int sCnt[kBN];
     __shared__ unsigned long long sBest[kBN];
+    // Per-wave survivor ring (fp32 full and retry passes): (key, id, query)
+    // staged in LDS and written to the candidate regions half a ring at a
+    // time, so the next slices' prefetch waits rarely wait on survivor stores
+    // (1.4% at C2). The fp16/bf16 instantiations hold a whole slice of
+    // operands in registers and lose more to the extra register pressure.
+    constexpr bool RING = S == kF32 && (PASS == kPassFull || PASS == kPassRetry);
+    __shared__ uint32_t sRingKey[RING ? 4 * kRing : 1];
+    __shared__ int sRingId[RING ? 4 * kRing : 1];
+    __shared__ int sRingQ[RING ? 4 * kRing : 1];
+    __shared__ int sRingN[4];
 
     // Workgroup -> (query block, split): the XCD grouping of scan_filter.
     const int nwg = gridDim.x;
@@ -700,6 +710,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
         sCnt[tid] = 0;
         sBest[tid] = ~0ull;
     }
+    if (tid < 4) sRingN[tid] = 0;
 
     // Per-lane query state for its 4 query blocks; bounds as in scan_filter.
     float tk[4], qn[4], ft[4];
@@ -832,11 +843,18 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
                             const bool pass = rv && qv[bn] && (key < tk[bn] || (key == tk[bn] && id <= ti[bn]));
                             if (pass) {
                                 const int ql = bn * 32 + r32;
-                                const int slot = atomicAdd(&sCnt[ql], 1);
-                                if (slot < p.cap) {
-                                    const int64_t q = (int64_t)qb * kBN + ql;
-                                    p.cand[(q * p.nsplit + split) * p.cap + slot] =
-                                        make_uint2(__float_as_uint(key), (unsigned)id);
+                                const int pos = RING ? atomicAdd(&sRingN[wave], 1) : kRing;
+                                if (pos < kRing) {
+                                    sRingKey[wave * kRing + pos] = __float_as_uint(key);
+                                    sRingId[wave * kRing + pos] = id;
+                                    sRingQ[wave * kRing + pos] = ql;
+                                } else {   // ring full (or not used): store directly
+                                    const int slot = atomicAdd(&sCnt[ql], 1);
+                                    if (slot < p.cap) {
+                                        const int64_t q = (int64_t)qb * kBN + ql;
+                                        p.cand[(q * p.nsplit + split) * p.cap + slot] =
+                                            make_uint2(__float_as_uint(key), (unsigned)id);
+                                    }
                                 }
                             }
                         }
@@ -848,6 +866,29 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
 
     auto norm = [&](int sl) -> float {
         return METRIC == 0 ? p.xnorm[rowBeg + (int64_t)sl * 64 + lane] : 0.0f;
+    };
+
+    // Writes the wave's staged survivors to their candidate regions once at
+    // least `atLeast` are staged (atLeast = 1: at the end).
+    auto flush = [&](int atLeast) {
+        if constexpr (RING) {
+            __builtin_amdgcn_wave_barrier();
+            const int n0 = sRingN[wave];
+            const int n = n0 < kRing ? n0 : kRing;
+            if (n < atLeast) return;
+            for (int e = lane; e < n; e += 64) {
+                const int ql = sRingQ[wave * kRing + e];
+                const int slot = atomicAdd(&sCnt[ql], 1);
+                if (slot < p.cap) {
+                    const int64_t q = (int64_t)qb * kBN + ql;
+                    p.cand[(q * p.nsplit + split) * p.cap + slot] =
+                        make_uint2(sRingKey[wave * kRing + e], (unsigned)sRingId[wave * kRing + e]);
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (lane == 0) sRingN[wave] = 0;
+            __builtin_amdgcn_wave_barrier();
+        }
     };
 
     if constexpr (G > 0) {
@@ -875,6 +916,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
                     for (int k = 0; k < NK; ++k) buf[t][bm][k] = lda(nx, bm, t, k);
             }
             epilogue(sl, xnv);
+            flush(kRing / 2);
             xnv = xnNext;
         }
     } else {
@@ -907,10 +949,12 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
                     for (int k = 0; k < NK; ++k) cur[bm][k] = nxt[bm][k];
             }
             epilogue(sl, xnv);
+            flush(kRing / 2);
             xnv = xnNext;
         }
     }
 
+    flush(1);
     if (PASS == kPassArgmin) {
 #pragma unroll
         for (int bn = 0; bn < 4; ++bn)

@@ -47,7 +47,8 @@ constexpr int kTopMax = 1024;   // largest k (== MFLAT_MAX_K)
 constexpr int kMaxSplit = 16384;  // most database splits one select block indexes
 constexpr int kSmallMaxQ = 64;                 // scan_small serves batches up to this size
 constexpr size_t kSmallMaxLds = 64 * 1024;     // ... whose query tile fits this much LDS
-constexpr size_t kResidentMaxLds = 76 * 1024;  // scan_resident: largest resident query tile
+constexpr size_t kResidentMaxLds = 68 * 1024;  // scan_resident: largest resident query tile
+constexpr int kRing = 192;                     // scan_resident: staged survivors per wave
 
 // Element type of the stored database and of the queries (the ABI's
 // mflat_storage_t values).
