@@ -91,6 +91,25 @@ def test_adversarial_order_retries(gpu_ok):
     parity.exact(gi, gd, oi, od)
 
 
+def test_loose_bound_many_survivors(gpu_ok):
+    """Every row on the sample's stride (nb = 50,000 -> 896 sample rows, stride 55)
+    is far from the queries and 3,000 near rows lie off the stride, so the
+    speculative bound is loose: the full pass stores > 2,048 candidates per query,
+    more than the one-wave select holds, and those queries take the workgroup
+    select. Integer data: bit-exact."""
+    rng = np.random.default_rng(17)
+    nb, d = 50_000, 16
+    x = (rng.integers(0, 4, size=(nb, d)) + 100).astype(np.float32)
+    off = np.setdiff1d(np.arange(nb), np.arange(0, nb, 55))
+    near = rng.choice(off, size=3000, replace=False)
+    x[near] -= 100.0
+    q = rng.integers(0, 4, size=(70, d)).astype(np.float32)
+    for k in (100, 256):
+        gi, gd, _ = run(x, q, k, L2)
+        oi, od = orc(x, q, k, L2)
+        parity.exact(gi, gd, oi, od)
+
+
 def test_clamp_k(gpu_ok):
     x, q = datagen.sift_like(nb=3000, nq=4, seed=5)
     gi, gd, ku = run(x, q, 5000, L2)
