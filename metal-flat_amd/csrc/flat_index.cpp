@@ -125,6 +125,13 @@ struct Plan {
     int j2 = 1;           // second, looser speculative rank (first retry)
     int64_t rps0 = 0;
     int nsplit0 = 1, cap0 = 1;
+    // optional second sample (0 rows: none), scanned with the first one's
+    // speculative bound; its jb-th best is the full pass's speculative bound
+    int64_t Rb = 0;
+    int strideb = 1;
+    int jb = 1;
+    int64_t rpsb = 0;
+    int nsplitb = 1, capb = 1;
     int64_t rps1 = 0;
     int nsplit1 = 1, cap1 = 1;
     size_t perQuery = 0;  // candidate entries per query (max over levels)
@@ -149,15 +156,20 @@ struct FlatIndex::Impl {
     DevBuf maxBits;
 
     // strided sample of the database (L0)
-    int64_t sampleR = 0;
-    int sampleStride = 0;
-    int64_t sampleNb = -1;
-    DevBuf sX, sXn, sIdx;
+    // strided samples of the database (L0, and the optional second level)
+    struct RowSample {
+        DevBuf X, xn, idx;
+        int64_t R = 0;
+        int stride = 0;
+        int64_t nb = -1;   // database size it was gathered at
+        void release() { X.release(); xn.release(); idx.release(); nb = -1; }
+    };
+    RowSample smp[2];
 
     // per-search workspace
     DevBuf stage, inv, qin, outIds, outVals;
     DevBuf qbuf, qh, qnorm, cand, cnt;
-    DevBuf tauSk, tauSi, tauS2k, tauS2i, tauGk, tauGi, tauKk, tauKi, status;
+    DevBuf tauSk, tauSi, tauS2k, tauS2i, tauGk, tauGi, tauKk, tauKi, tauBk, tauBi, status;
     DevBuf cQ, cQn, cTk, cTi, cIdx, cSel;
     DevBuf best;
 
@@ -208,8 +220,46 @@ struct FlatIndex::Impl {
         const double e1 = (double)pl.j * (double)nb / (double)r;   // expected survivors
         const int64_t perSplit = (int64_t)(2.0 * e1 / pl.nsplit1) + 64;
         pl.cap1 = std::max<int>({2 * k, 64, pow2ceil(perSplit)});
-        pl.perQuery = std::max((size_t)pl.nsplit0 * pl.cap0, (size_t)pl.nsplit1 * pl.cap1);
+        planSecondSample(pl, mb, k, r);
+        pl.perQuery = std::max({(size_t)pl.nsplit0 * pl.cap0, (size_t)pl.nsplit1 * pl.cap1,
+                                pl.Rb ? (size_t)pl.nsplitb * pl.capb : (size_t)0});
         return pl;
+    }
+
+    // Second sample level. The full pass's survivors scale with the speculative
+    // bound's rank over its sample size (j nb / R0 per query); a larger sample
+    // Rb, scanned with the first sample's bound (few candidates), gives the
+    // rank jb for Rb and ~jb nb / Rb survivors. It pays where a survivor's exact
+    // test and store cost more than the extra MFMA work: fp16/bf16 storage at
+    // small d. The cost model uses measured rates of this part (C2 shape):
+    // fp32 ~60 TMAC/s, fp16/bf16 ~420 TMAC/s resident (~330 tiled), ~0.15 ns
+    // per survivor, ~15 ns per query for the extra select.
+    void planSecondSample(Plan& pl, int64_t mb, int k, int64_t r) const {
+        if (small_scan_fits((int)std::min<int64_t>(mb, 1 << 30), dpad, storage)) return;
+        const double tMac = storage == kF32 ? 1.0 / 60e12
+                            : resident_scan_fits(dpad, storage) ? 1.0 / 420e12 : 1.0 / 330e12;
+        const double tSurv = 0.15e-9, tSelQ = 15e-9;
+        double best = 0.0;
+        for (int f = 2; f <= 16; f *= 2) {
+            const int64_t Rb = roundUp(f * r, kBM);
+            if (2 * Rb > nb) break;
+            const int jb = chooseJ(k, (double)k * (double)Rb / (double)nb, 0.01);
+            const double saved = (double)mb * ((double)pl.j * nb / r - (double)jb * nb / Rb) * tSurv;
+            const double cost = (double)mb * (double)Rb * dpad * tMac + (double)mb * tSelQ;
+            if (saved > 1.5 * cost && saved - cost > best) {   // clear wins only: the rates are estimates
+                best = saved - cost;
+                pl.Rb = Rb;
+                pl.jb = jb;
+            }
+        }
+        if (!pl.Rb) return;
+        pl.strideb = (int)(nb / pl.Rb);
+        splitPlan(pl.Rb, (int)mb, dpad, storage, pl.rpsb, pl.nsplitb);
+        const double eb = (double)pl.j * (double)pl.Rb / (double)r;   // expected stored per query
+        pl.capb = std::max<int>(32, pow2ceil((int64_t)(4.0 * eb / pl.nsplitb) + 16));
+        // the full pass now expects jb nb / Rb survivors
+        const double e1 = (double)pl.jb * (double)nb / (double)pl.Rb;
+        pl.cap1 = std::max<int>({2 * k, 64, pow2ceil((int64_t)(2.0 * e1 / pl.nsplit1) + 64)});
     }
 
     void growRows(int64_t need, hipStream_t s) {
@@ -273,20 +323,21 @@ struct FlatIndex::Impl {
         nb += n;
     }
 
-    void ensureSample(const Plan& pl, hipStream_t s) {
-        if (sampleNb == nb && sampleR == pl.R0 && sampleStride == pl.stride) return;
-        std::vector<int> idx((size_t)pl.R0);
-        for (int64_t r = 0; r < pl.R0; ++r) idx[(size_t)r] = (int)(r * pl.stride);
-        sIdx.ensure(idx.size() * sizeof(int));
-        sX.ensure((size_t)pl.R0 * dpad * esize);
-        sXn.ensure((size_t)pl.R0 * sizeof(float));
-        HIPC(hipMemcpyAsync(sIdx.p, idx.data(), idx.size() * sizeof(int), hipMemcpyHostToDevice, s));
-        launch_gather_rows_blk(X.p, sIdx.as<int>(), (int)pl.R0, dpad, storage, sX.p, s);
-        launch_gather_f32(xn.as<float>(), sIdx.as<int>(), (int)pl.R0, sXn.as<float>(), s);
+    // Sample row r is database row r * stride (R is a multiple of kBM).
+    void ensureSample(RowSample& sm, int64_t R, int stride, hipStream_t s) {
+        if (sm.nb == nb && sm.R == R && sm.stride == stride) return;
+        std::vector<int> idx((size_t)R);
+        for (int64_t r = 0; r < R; ++r) idx[(size_t)r] = (int)(r * stride);
+        sm.idx.ensure(idx.size() * sizeof(int));
+        sm.X.ensure((size_t)R * dpad * esize);
+        sm.xn.ensure((size_t)R * sizeof(float));
+        HIPC(hipMemcpyAsync(sm.idx.p, idx.data(), idx.size() * sizeof(int), hipMemcpyHostToDevice, s));
+        launch_gather_rows_blk(X.p, sm.idx.as<int>(), (int)R, dpad, storage, sm.X.p, s);
+        launch_gather_f32(xn.as<float>(), sm.idx.as<int>(), (int)R, sm.xn.as<float>(), s);
         HIPC(hipStreamSynchronize(s));
-        sampleNb = nb;
-        sampleR = pl.R0;
-        sampleStride = pl.stride;
+        sm.nb = nb;
+        sm.R = R;
+        sm.stride = stride;
     }
 
     void scan(const void* Xs, const float* xns, int64_t nrows, int64_t rps, int nsplit, int idStride,
@@ -350,14 +401,15 @@ struct FlatIndex::Impl {
             return;
         }
 
-        ensureSample(pl, s);
+        ensureSample(smp[0], pl.R0, pl.stride, s);
+        if (pl.Rb) ensureSample(smp[1], pl.Rb, pl.strideb, s);
         if (traceOn())
             std::fprintf(stderr, "[mflat trace] mb=%d k=%d nb=%lld R0=%lld stride=%d j=%d j2=%d "
-                         "L0 %dx%d L1 splits=%d cap=%d\n", mb, k, (long long)nb, (long long)pl.R0,
-                         pl.stride, pl.j, pl.j2, pl.nsplit0, pl.cap0, pl.nsplit1, pl.cap1);
+                         "L0 %dx%d Rb=%lld jb=%d L1 splits=%d cap=%d\n", mb, k, (long long)nb, (long long)pl.R0,
+                         pl.stride, pl.j, pl.j2, pl.nsplit0, pl.cap0, (long long)pl.Rb, pl.jb, pl.nsplit1, pl.cap1);
         // L0: sample, no bound -> speculative (j-th) and guaranteed (k-th) bounds
         launch_fill_tau_none(tauSk.as<float>(), tauSi.as<int>(), mb, s);
-        scan(sX.p, sXn.as<float>(), pl.R0, pl.rps0, pl.nsplit0, pl.stride, Q, qn, mb,
+        scan(smp[0].X.p, smp[0].xn.as<float>(), pl.R0, pl.rps0, pl.nsplit0, pl.stride, Q, qn, mb,
              tauSk.as<float>(), tauSi.as<int>(), pl.cap0, s, kPassSample);
         {
             SelectParams sp = selectParams(mb, pl.nsplit0, pl.cap0, k, pl.j);
@@ -366,6 +418,17 @@ struct FlatIndex::Impl {
             sp.tau_j2_key = tauS2k.as<float>(); sp.tau_j2_id = tauS2i.as<int>();
             sp.tau_k_key = tauGk.as<float>(); sp.tau_k_id = tauGi.as<int>();
             launch_select(sp, s);
+        }
+        // L0b (optional): the second sample under the first one's speculative
+        // bound; its jb-th best, where it stored that many, tightens the bound
+        if (pl.Rb) {
+            scan(smp[1].X.p, smp[1].xn.as<float>(), pl.Rb, pl.rpsb, pl.nsplitb, pl.strideb, Q, qn, mb,
+                 tauSk.as<float>(), tauSi.as<int>(), pl.capb, s, kPassSample);
+            tauBk.ensure((size_t)mb * 4); tauBi.ensure((size_t)mb * 4);
+            SelectParams sp = selectParams(mb, pl.nsplitb, pl.capb, pl.jb, pl.jb);
+            sp.tau_k_key = tauBk.as<float>(); sp.tau_k_id = tauBi.as<int>();
+            launch_select(sp, s);
+            launch_tau_min(tauSk.as<float>(), tauSi.as<int>(), tauBk.as<float>(), tauBi.as<int>(), mb, s);
         }
         // L1: full database with the speculative bound
         scan(X.p, xn.as<float>(), nb, pl.rps1, pl.nsplit1, 1, Q, qn, mb,
@@ -520,9 +583,10 @@ FlatIndex::~FlatIndex() {
     if (!d_) return;
     if (d_->device >= 0) (void)hipSetDevice(d_->device);
     if (d_->stream) (void)hipStreamSynchronize(d_->stream);
-    for (DevBuf* b : {&d_->X, &d_->xn, &d_->sX, &d_->sXn, &d_->sIdx, &d_->stage, &d_->inv, &d_->qin, &d_->outIds,
+    for (auto& sm : d_->smp) sm.release();
+    for (DevBuf* b : {&d_->X, &d_->xn, &d_->stage, &d_->inv, &d_->qin, &d_->outIds,
                       &d_->outVals, &d_->qbuf, &d_->qh, &d_->qnorm, &d_->cand, &d_->cnt, &d_->tauSk, &d_->tauSi, &d_->tauS2k, &d_->tauS2i, &d_->maxBits,
-                      &d_->tauGk, &d_->tauGi, &d_->tauKk, &d_->tauKi, &d_->status, &d_->cQ, &d_->cQn,
+                      &d_->tauGk, &d_->tauGi, &d_->tauKk, &d_->tauKi, &d_->tauBk, &d_->tauBi, &d_->status, &d_->cQ, &d_->cQn,
                       &d_->cTk, &d_->cTi, &d_->cIdx, &d_->cSel, &d_->best})
         b->release();
     if (d_->stream) (void)hipStreamDestroy(d_->stream);
@@ -552,7 +616,7 @@ void FlatIndex::reset() {
     d_->capRows = 0;
     d_->nb = 0;
     d_->xnMax = 0.0f;
-    d_->sampleNb = -1;
+    for (auto& sm : d_->smp) sm.nb = -1;
 }
 
 int FlatIndex::search(const float* q, int m, int k, int32_t* ids, float* dists) {

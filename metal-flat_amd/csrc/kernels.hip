@@ -270,6 +270,15 @@ __global__ void fill_tau_none_kernel(float* __restrict__ key, int* __restrict__ 
     if (i < n) { key[i] = INFINITY; id[i] = -1; }
 }
 
+__global__ void tau_min_kernel(float* __restrict__ ka, int* __restrict__ ia, const float* __restrict__ kb,
+                               const int* __restrict__ ib, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float k = kb[i];
+    const int id = ib[i];
+    if (k < ka[i] || (k == ka[i] && id < ia[i])) { ka[i] = k; ia[i] = id; }
+}
+
 __global__ void fill_empty_kernel(int32_t* __restrict__ ids, float* __restrict__ vals,
                                   int64_t count, float empty) {
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < count;
@@ -1581,6 +1590,15 @@ void launch_fill_tau_none(float* key, int* id, int n, hipStream_t s) {
     fill_tau_none_kernel<<<(n + 255) / 256, 256, 0, s>>>(key, id, n);
     prof_end(tok, s);
     check_launch("fill_tau_none");
+}
+
+void launch_tau_min(float* key_a, int* id_a, const float* key_b, const int* id_b, int n, hipStream_t s) {
+    if (n <= 0) return;
+    void* tok;
+    prof_begin(kFamPrep, s, &tok);
+    tau_min_kernel<<<(n + 255) / 256, 256, 0, s>>>(key_a, id_a, key_b, id_b, n);
+    prof_end(tok, s);
+    check_launch("tau_min");
 }
 
 void launch_fill_empty(int32_t* ids, float* vals, int64_t count, float empty, hipStream_t s) {

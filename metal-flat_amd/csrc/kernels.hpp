@@ -153,6 +153,8 @@ struct TauSources {   // three per-query bound arrays a retry can draw from
 void launch_gather_tau(const TauSources& src, const int* idx, const int* sel, int n, float* ko,
                        int* io, hipStream_t s);
 void launch_fill_tau_none(float* key, int* id, int n, hipStream_t s);
+// (key_a, id_a)[i] = lexicographic min of itself and (key_b, id_b)[i]
+void launch_tau_min(float* key_a, int* id_a, const float* key_b, const int* id_b, int n, hipStream_t s);
 void launch_fill_empty(int32_t* ids, float* vals, int64_t count, float empty, hipStream_t s);
 void launch_max_norm(const float* xn, int64_t n, unsigned* out, hipStream_t s);
 // Dispatches to scan_small (small batches, HBM-streaming) when small_scan_fits,
