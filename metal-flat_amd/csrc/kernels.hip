@@ -1220,6 +1220,7 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
     __shared__ int sWave[4];
     __shared__ uint64_t sT;
     __shared__ int sN;
+    __shared__ unsigned sRange[2][4];
 
     const int q = blockIdx.x;
     const int tid = threadIdx.x;
@@ -1228,33 +1229,41 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
     const int ns = p.nsplit;
     const int64_t qbase = (int64_t)q * ns;
 
-    // exclusive prefix of the stored (clamped) counts: sOff[s] .. sOff[s+1]
-    int carry = 0;
+    // exclusive prefix of the stored (clamped) counts: sOff[s] .. sOff[s+1].
+    // Thread t owns the contiguous splits [t per, (t + 1) per), so any split
+    // count costs one block scan (two barriers).
+    const int per = (ns + 255) / 256;
+    const int s0 = tid * per;
+    int local = 0;
     bool ovfLocal = false;
-    for (int base = 0; base < ns; base += 256) {
-        const int sidx = base + tid;
-        int v = 0;
+    for (int i = 0; i < per; ++i) {
+        const int sidx = s0 + i;
         if (sidx < ns) {
             const int n = p.cnt[qbase + sidx];
             ovfLocal |= n > p.cap;
-            v = n < p.cap ? n : p.cap;
+            local += n < p.cap ? n : p.cap;
         }
-        int x = v;
-        for (int off = 1; off < 64; off <<= 1) {
-            const int t = __shfl_up(x, off, 64);
-            if (lane >= off) x += t;
+    }
+    int x = local;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(x, off, 64);
+        if (lane >= off) x += t;
+    }
+    if (lane == 63) sWave[wave] = x;
+    __syncthreads();
+    int run = x - local;
+    for (int w = 0; w < wave; ++w) run += sWave[w];
+    for (int i = 0; i < per; ++i) {
+        const int sidx = s0 + i;
+        if (sidx < ns) {
+            const int n = p.cnt[qbase + sidx];
+            run += n < p.cap ? n : p.cap;
+            sOff[sidx + 1] = run;
         }
-        if (lane == 63) sWave[wave] = x;
-        __syncthreads();
-        int wpre = 0;
-        for (int w = 0; w < wave; ++w) wpre += sWave[w];
-        if (sidx < ns) sOff[sidx + 1] = carry + wpre + x;
-        carry += sWave[0] + sWave[1] + sWave[2] + sWave[3];
-        __syncthreads();
     }
     if (tid == 0) sOff[0] = 0;
     const bool ovf = __syncthreads_or(ovfLocal);
-    const int c = carry;
+    const int c = sWave[0] + sWave[1] + sWave[2] + sWave[3];
     const bool inLds = c <= kSelLds;
 
     // flat index -> candidate (binary search over the split offsets)
@@ -1267,7 +1276,20 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
         return composite(p.cand[(qbase + lo) * p.cap + (e - sOff[lo])]);
     };
     if (inLds) {
-        for (int e = tid; e < c; e += 256) sBuf[e] = fetch(e);
+        if (ns >= 256) {
+            // many splits with few candidates each (small batches): every
+            // thread copies its own splits; no offset search per element
+            for (int i = 0; i < per; ++i) {
+                const int sidx = s0 + i;
+                if (sidx >= ns) break;
+                const int n = min(p.cnt[qbase + sidx], p.cap);
+                const int o = sOff[sidx];
+                const uint2* src = p.cand + (qbase + sidx) * p.cap;
+                for (int e = 0; e < n; ++e) sBuf[o + e] = composite(src[e]);
+            }
+        } else {
+            for (int e = tid; e < c; e += 256) sBuf[e] = fetch(e);
+        }
     }
     __syncthreads();
 
@@ -1280,44 +1302,116 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
     };
 
     const int k = p.k;
+    // Bucket of the histogram sHist holding rank kr (1-based) of the counted
+    // elements -> sSel = {bucket, rank within it, bucket size}.
+    auto findBucket = [&](unsigned kr) {
+        __syncthreads();
+        if (tid < 64) {
+            const unsigned h0 = sHist[4 * tid], h1 = sHist[4 * tid + 1];
+            const unsigned h2 = sHist[4 * tid + 2], h3 = sHist[4 * tid + 3];
+            const unsigned s4 = h0 + h1 + h2 + h3;
+            unsigned incl = s4;
+            for (int off = 1; off < 64; off <<= 1) {
+                const unsigned t = __shfl_up(incl, off, 64);
+                if (tid >= off) incl += t;
+            }
+            const unsigned excl = incl - s4;
+            if (excl < kr && kr <= incl) {
+                unsigned cum = excl;
+                unsigned b = 4 * tid, hb = h0;
+                if (cum + h0 < kr) {
+                    cum += h0; b += 1; hb = h1;
+                    if (cum + h1 < kr) {
+                        cum += h1; b += 1; hb = h2;
+                        if (cum + h2 < kr) { cum += h2; b += 1; hb = h3; }
+                    }
+                }
+                sSel[0] = b;
+                sSel[1] = kr - cum;
+                sSel[2] = hb;
+            }
+        }
+        __syncthreads();
+    };
+    // ascending bitonic sort of sTop[0, P), P a power of two
+    auto sortTop = [&](int P) {
+        for (int size = 2; size <= P; size <<= 1) {
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                for (int i = tid; i < (P >> 1); i += 256) {
+                    const int lo = 2 * i - (i & (stride - 1));
+                    const int hi = lo + stride;
+                    const bool asc = (lo & size) == 0;
+                    const uint64_t a = sTop[lo], b = sTop[hi];
+                    if ((a > b) == asc) { sTop[lo] = b; sTop[hi] = a; }
+                }
+                __syncthreads();
+            }
+        }
+    };
+
     uint64_t T = ~0ull;   // take everything when c <= k
     if (c > k) {
+        bool found = false;
+        // One histogram over the key ordinals' actual range [omin, omax] (keys
+        // of one query usually span a narrow range, which would put most of
+        // them in one bin of a fixed-digit radix pass): the k-th composite lies
+        // in bucket b, whose members (composites order by key first) are the
+        // only ones that need sorting.
+        unsigned omin = ~0u, omax = 0u;
+        for_each([&](uint64_t x) {
+            const unsigned o = (unsigned)(x >> 32);
+            omin = o < omin ? o : omin;
+            omax = o > omax ? o : omax;
+        });
+        for (int off = 32; off > 0; off >>= 1) {
+            const unsigned a = (unsigned)__shfl_xor((int)omin, off, 64);
+            const unsigned b = (unsigned)__shfl_xor((int)omax, off, 64);
+            omin = a < omin ? a : omin;
+            omax = b > omax ? b : omax;
+        }
+        if (lane == 0) { sRange[0][wave] = omin; sRange[1][wave] = omax; }
+        __syncthreads();
+        omin = sRange[0][0]; omax = sRange[1][0];
+        for (int w = 1; w < 4; ++w) {
+            omin = sRange[0][w] < omin ? sRange[0][w] : omin;
+            omax = sRange[1][w] > omax ? sRange[1][w] : omax;
+        }
+        if (omax > omin) {
+            const int bits = 32 - __clz((int)(omax - omin));   // bits of the largest offset
+            const int sh = bits > 8 ? bits - 8 : 0;
+            sHist[tid] = 0;
+            __syncthreads();
+            for_each([&](uint64_t x) { atomicAdd(&sHist[((unsigned)(x >> 32) - omin) >> sh], 1u); });
+            findBucket((unsigned)k);
+            const unsigned b = sSel[0], kr = sSel[1], hb = sSel[2];
+            if (hb <= (unsigned)kTopMax) {
+                if (tid == 0) sN = 0;
+                __syncthreads();
+                for_each([&](uint64_t x) {
+                    if ((((unsigned)(x >> 32) - omin) >> sh) == b) sTop[atomicAdd(&sN, 1)] = x;
+                });
+                __syncthreads();
+                int P = 1;
+                while (P < (int)hb) P <<= 1;
+                for (int i = (int)hb + tid; i < P; i += 256) sTop[i] = ~0ull;
+                __syncthreads();
+                sortTop(P);
+                T = sTop[kr - 1];
+                found = true;
+                __syncthreads();
+            }
+        }
+        // Fallback (all keys equal, or an overfull bucket): radix select on
+        // 8-bit digits of the composite.
         uint64_t prefix = 0, mask = 0;
         unsigned kr = (unsigned)k;
-        bool found = false;
-        for (int shift = 56; shift >= 0; shift -= 8) {
+        for (int shift = 56; shift >= 0 && !found; shift -= 8) {
             sHist[tid] = 0;
             __syncthreads();
             for_each([&](uint64_t x) {
                 if ((x & mask) == prefix) atomicAdd(&sHist[(unsigned)(x >> shift) & 255u], 1u);
             });
-            __syncthreads();
-            if (tid < 64) {
-                const unsigned h0 = sHist[4 * tid], h1 = sHist[4 * tid + 1];
-                const unsigned h2 = sHist[4 * tid + 2], h3 = sHist[4 * tid + 3];
-                const unsigned s4 = h0 + h1 + h2 + h3;
-                unsigned incl = s4;
-                for (int off = 1; off < 64; off <<= 1) {
-                    const unsigned t = __shfl_up(incl, off, 64);
-                    if (tid >= off) incl += t;
-                }
-                const unsigned excl = incl - s4;
-                if (excl < kr && kr <= incl) {
-                    unsigned cum = excl;
-                    unsigned b = 4 * tid, hb = h0;
-                    if (cum + h0 < kr) {
-                        cum += h0; b += 1; hb = h1;
-                        if (cum + h1 < kr) {
-                            cum += h1; b += 1; hb = h2;
-                            if (cum + h2 < kr) { cum += h2; b += 1; hb = h3; }
-                        }
-                    }
-                    sSel[0] = b;
-                    sSel[1] = kr - cum;
-                    sSel[2] = hb;
-                }
-            }
-            __syncthreads();
+            findBucket(kr);
             const unsigned b = sSel[0];
             kr = sSel[1];
             const unsigned hb = sSel[2];
@@ -1331,7 +1425,6 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
                 __syncthreads();
                 T = sT;
                 found = true;
-                break;
             }
         }
         if (!found) T = prefix;
@@ -1351,20 +1444,7 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
     while (P < nsel) P <<= 1;
     for (int i = nsel + tid; i < P; i += 256) sTop[i] = ~0ull;
     __syncthreads();
-
-    // bitonic sort, ascending
-    for (int size = 2; size <= P; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = tid; i < (P >> 1); i += 256) {
-                const int lo = 2 * i - (i & (stride - 1));
-                const int hi = lo + stride;
-                const bool asc = (lo & size) == 0;
-                const uint64_t a = sTop[lo], b = sTop[hi];
-                if ((a > b) == asc) { sTop[lo] = b; sTop[hi] = a; }
-            }
-            __syncthreads();
-        }
-    }
+    sortTop(P);
 
     const int orow = p.qmap ? p.qmap[q] : q;
     if (p.out_ids || p.out_vals) {
