@@ -60,6 +60,7 @@ constexpr int64_t kTargetWG = 2048;             // scan_filter workgroups wanted
 constexpr int64_t kTargetWGSmall = 4096;        // scan_small workgroups (HBM streaming)
 constexpr size_t kCandBudget = size_t(1536) << 20;  // candidate workspace per batch
 constexpr size_t kStageBytes = size_t(256) << 20;   // host->device staging chunk
+constexpr int64_t kRetryMinTiles = 2;   // tiles per split in the retries of a large batch
 
 int64_t roundUp(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
@@ -95,16 +96,20 @@ int chooseJ(int k, double lambda, double tail) {
 
 // nq: queries of the launch (small batches go to scan_small, which streams the
 // database and wants many more, smaller workgroups).
-void splitPlan(int64_t nrows, int nq, int dpad, int storage, int64_t& rowsPerSplit, int& nsplit) {
+// minTiles: fewest kBM-row tiles per split (a scan_resident workgroup needs
+// two tiles to give each of its four waves a 64-row slice).
+void splitPlan(int64_t nrows, int nq, int dpad, int storage, int64_t& rowsPerSplit, int& nsplit,
+               bool allowSmall = true, int64_t minTiles = 1) {
     const int nqb = (nq + kBN - 1) / kBN;
     const int64_t ntiles = std::max<int64_t>(1, (nrows + kBM - 1) / kBM);
-    const int64_t target = small_scan_fits(nq, dpad, storage) ? kTargetWGSmall : kTargetWG;
+    const int64_t target = allowSmall && small_scan_fits(nq, dpad, storage) ? kTargetWGSmall : kTargetWG;
     int64_t want = std::max<int64_t>(1, (target + nqb - 1) / nqb);
     // keep a split's bytes addressable with 32-bit offsets
     const int64_t maxTiles =
         std::max<int64_t>(1, ((int64_t)1 << 31) / ((int64_t)kBM * dpad * elem_bytes(storage)) - 1);
     want = std::max(want, (ntiles + maxTiles - 1) / maxTiles);
     want = std::min<int64_t>(want, kMaxSplit);
+    want = std::min(want, std::max<int64_t>(1, ntiles / minTiles));
     want = std::min(want, ntiles);
     const int64_t tps = (ntiles + want - 1) / want;
     nsplit = (int)((ntiles + tps - 1) / tps);
@@ -342,7 +347,7 @@ struct FlatIndex::Impl {
 
     void scan(const void* Xs, const float* xns, int64_t nrows, int64_t rps, int nsplit, int idStride,
               const void* Q, const float* qn, int nq, const float* tk, const int* ti, int cap,
-              hipStream_t s, int pass = kPassFull) {
+              hipStream_t s, int pass = kPassFull, bool allowSmall = true) {
         const int nqb = (nq + kBN - 1) / kBN;
         cand.ensure((size_t)nq * nsplit * cap * sizeof(uint2));
         cnt.ensure((size_t)nq * nsplit * sizeof(int));
@@ -352,7 +357,7 @@ struct FlatIndex::Impl {
         p.Q = Q; p.qnorm = qn; p.nq = nq; p.nqb = nqb; p.dpad = dpad;
         p.tau_key = tk; p.tau_id = ti;
         p.cand = cand.as<uint2>(); p.cnt = cnt.as<int>(); p.cap = cap;
-        launch_scan_filter(p, kernMetric(), pass, storage, s);
+        launch_scan_filter(p, kernMetric(), pass, storage, s, allowSmall);
     }
 
     SelectParams selectParams(int nq, int nsplit, int cap, int k, int j) const {
@@ -441,6 +446,7 @@ struct FlatIndex::Impl {
             launch_select(sp, s);
         }
 
+        const bool batchSmall = small_scan_fits(mb, dpad, storage);
         // verification and retries. Per query, the bound used so far:
         //   0 = speculative (j-th of the sample), 1 = looser speculative (j2-th),
         //   2 = guaranteed (k-th of the sample or of a stored subset).
@@ -487,10 +493,13 @@ struct FlatIndex::Impl {
             launch_gather_tau(ts, cIdx.as<int>(), cSel.as<int>(), nf, cTk.as<float>(), cTi.as<int>(), s);
             int64_t rps;
             int nsplit;
-            splitPlan(nb, nf, dpad, storage, rps, nsplit);
+            // Retries run the kernel family of the passes their bounds came
+            // from (the whole batch's), so every bound is compared with keys
+            // computed the same way (a guaranteed bound must admit its own rows).
+            splitPlan(nb, nf, dpad, storage, rps, nsplit, batchSmall, batchSmall ? 1 : kRetryMinTiles);
             const int cap = std::max(2 * k, 64);
             scan(X.p, xn.as<float>(), nb, rps, nsplit, 1, cQ.p, cQn.as<float>(), nf,
-                 cTk.as<float>(), cTi.as<int>(), cap, s, kPassRetry);
+                 cTk.as<float>(), cTi.as<int>(), cap, s, kPassRetry, batchSmall);
             SelectParams sp = selectParams(nf, nsplit, cap, k, k);
             sp.qmap = cIdx.as<int>();
             sp.out_ids = oIds; sp.out_vals = oVals;

@@ -1789,10 +1789,10 @@ bool small_scan_fits(int nq, int dpad, int storage) {
     return nq >= 1 && nq <= kSmallMaxQ && small_lds_bytes(nq, dpad, storage) <= kSmallMaxLds;
 }
 
-void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, hipStream_t s) {
+void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, hipStream_t s, bool allowSmall) {
     if (storage != kF32 && storage != kF16 && storage != kBF16)
         throw std::runtime_error("scan_filter: unknown storage type");
-    if (pass != kPassArgmin && small_scan_fits(p.nq, p.dpad, storage)) {
+    if (allowSmall && pass != kPassArgmin && small_scan_fits(p.nq, p.dpad, storage)) {
         if (p.nsplit <= 0) return;
         if (p.rows_per_split % kBM != 0 || p.cap < 1 || p.dpad % kBK != 0)
             throw std::runtime_error("scan_small: bad tiling parameters");

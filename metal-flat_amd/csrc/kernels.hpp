@@ -157,12 +157,16 @@ void launch_fill_tau_none(float* key, int* id, int n, hipStream_t s);
 void launch_tau_min(float* key_a, int* id_a, const float* key_b, const int* id_b, int n, hipStream_t s);
 void launch_fill_empty(int32_t* ids, float* vals, int64_t count, float empty, hipStream_t s);
 void launch_max_norm(const float* xn, int64_t n, unsigned* out, hipStream_t s);
-// Dispatches to scan_small (small batches, HBM-streaming) when small_scan_fits,
-// else to scan_resident when the 128-query tile fits in LDS
-// (resident_scan_fits), else to the LDS-tiled scan_filter.
+// Dispatches to scan_small (small batches, HBM-streaming) when allowSmall and
+// small_scan_fits, else to scan_resident when the 128-query tile fits in LDS
+// (resident_scan_fits), else to the LDS-tiled scan_filter. scan_resident and
+// scan_filter compute bit-identical keys (same MFMA shape and column order);
+// scan_small's accumulation order differs, so passes whose bounds feed each
+// other must not mix it with the other two (allowSmall = false).
 bool small_scan_fits(int nq, int dpad, int storage);
 bool resident_scan_fits(int dpad, int storage);
-void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, hipStream_t s);
+void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, hipStream_t s,
+                        bool allowSmall = true);
 void launch_select(const SelectParams& p, hipStream_t s);
 void launch_argmin_finalize(const unsigned long long* best, int nq, int metric, int32_t* ids, float* vals,
                             hipStream_t s);
