@@ -135,6 +135,33 @@ MFLAT_API mflat_storage_t mflat_flat_storage(const mflat_flat_index_t*);
 MFLAT_API mflat_status_t mflat_flat_search_i64(mflat_flat_index_t*, const float* queries,
         int m, int k, int64_t* out_ids, float* out_distances, int* out_k_used);
 
+/* ---------------- Additive: k-means (IVF coarse-quantizer training) ------ */
+/* No C counterpart in the reference: its k-means is internal to IVF training
+   (CoarseQuantizer::train over detail::kmeansGpu, src/CoarseQuantizer.mm:104-159,
+   src/Internal.h:234-382). Trains nlist = min(nlist, n) L2 centroids on n
+   row-major points (host memory, borrowed for the call) with the whole loop on
+   the device: seeds are nlist distinct points of a uniform permutation drawn
+   from mt19937(12345); training uses the first min(n, max_points_per_centroid
+   * nlist) points of that permutation (0 = all points); each of `iters`
+   iterations assigns every training point to its nearest centroid (lowest
+   index on ties) and sets each centroid to float(double sum / count) of its
+   points summed in ascending order, an empty cell taking a training point
+   drawn from the same generator; a final pass assigns all n points.
+   Outputs (caller-allocated; all but out_centroids nullable):
+     out_centroids     nlist * dim floats
+     out_assign        n cell ids
+     out_cell_start    nlist + 1 offsets of each cell in out_order
+     out_order         n point ids grouped by cell, ascending within a cell
+     out_nlist         nlist used
+   The seeds differ from the reference's (its std::shuffle draws are specific to
+   its standard library); every step after seeding follows it.
+   NULL points / out_centroids -> MFLAT_ERR_NULL_ARG; n, dim, nlist < 1 or
+   iters, max_points_per_centroid < 0 -> MFLAT_ERR_BAD_ARG; no usable device ->
+   MFLAT_ERR_NOT_READY. */
+MFLAT_API mflat_status_t mflat_kmeans_train(const float* points, int n, int dim, int nlist, int iters,
+        int max_points_per_centroid, float* out_centroids, int32_t* out_assign,
+        int32_t* out_cell_start, int32_t* out_order, int* out_nlist);
+
 /* ---------------- Additive: device-resident data ------------------------- */
 /* No counterpart in the reference (its buffers are unified memory,
    src/FlatIndex.mm:163-171). For callers whose data already lives in HBM.

@@ -1,0 +1,122 @@
+// SPDX-License-Identifier: Apache-2.0
+// kmeans.cpp -- host side of the device k-means training loop (kmeans.hpp).
+// The assignment step is the flat index's fused k = 1 search (points as
+// queries, centroids as the database); the update runs in kmeans_kernels.hip.
+// Per iteration only the nlist cell counts cross to the host, to draw the
+// reseed rows of empty cells from the same generator stream as the reference.
+#include "kmeans.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <random>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "flat_index.hpp"
+#include "kmeans_kernels.hpp"
+
+namespace mflat_amd {
+namespace {
+
+void hipCheck(hipError_t e, const char* what) {
+    if (e == hipSuccess) return;
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) throw std::bad_alloc();
+    throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+#define HIPC(x) hipCheck((x), #x)
+
+struct DevMem {
+    void* p = nullptr;
+    explicit DevMem(size_t bytes) { HIPC(hipMalloc(&p, bytes ? bytes : 1)); }
+    ~DevMem() { if (p) (void)hipFree(p); }
+    DevMem(const DevMem&) = delete;
+    DevMem& operator=(const DevMem&) = delete;
+    template <class T> T* as() const { return static_cast<T*>(p); }
+};
+
+struct Stream {
+    hipStream_t s = nullptr;
+    Stream() { HIPC(hipStreamCreateWithFlags(&s, hipStreamNonBlocking)); }
+    ~Stream() { if (s) (void)hipStreamDestroy(s); }
+};
+
+uint32_t bounded(std::mt19937& rng, uint32_t range) {   // uniform in [0, range)
+    const uint64_t lim = (uint64_t(1) << 32) - ((uint64_t(1) << 32) % range);
+    uint64_t u;
+    do { u = rng(); } while (u >= lim);
+    return (uint32_t)(u % range);
+}
+
+}  // namespace
+
+int kmeansTrain(const float* points, int n, int dim, int nlistReq, int iters, int maxPointsPerCentroid,
+                float* centroids, int32_t* assign, int32_t* cellStart, int32_t* order) {
+    if (n < 1 || dim < 1 || nlistReq < 1 || iters < 0 || maxPointsPerCentroid < 0)
+        throw BadArg("kmeans: n, dim, nlist must be >= 1 and iters, max_points_per_centroid >= 0");
+    const int nlist = std::min(nlistReq, n);
+    FlatIndex assigner(dim, Metric::L2);
+    if (!assigner.ready()) throw NotReady("no usable HIP device: k-means needs a gfx950 GPU");
+
+    // seeding (reference src/Internal.h:238-248)
+    std::mt19937 rng(12345);
+    std::vector<int32_t> perm((size_t)n);
+    for (int i = 0; i < n; ++i) perm[(size_t)i] = i;
+    for (int i = n - 1; i > 0; --i) std::swap(perm[(size_t)i], perm[bounded(rng, (uint32_t)i + 1)]);
+    // training subsample: the first trainN entries of the permutation (:250-263)
+    int trainN = n;
+    if (maxPointsPerCentroid > 0 && (int64_t)maxPointsPerCentroid * nlist < n) trainN = maxPointsPerCentroid * nlist;
+
+    Stream st;
+    const hipStream_t s = st.s;
+    const size_t rowB = (size_t)dim * sizeof(float);
+    DevMem dData((size_t)n * rowB), dCent((size_t)nlist * rowB), dPerm((size_t)n * sizeof(int));
+    HIPC(hipMemcpyAsync(dData.p, points, (size_t)n * rowB, hipMemcpyHostToDevice, s));
+    HIPC(hipMemcpyAsync(dPerm.p, perm.data(), (size_t)n * sizeof(int), hipMemcpyHostToDevice, s));
+    launch_gather_points(dData.as<float>(), dPerm.as<int>(), nlist, dim, dCent.as<float>(), s);
+    const float* dTrain = dData.as<float>();
+    DevMem dTrainBuf(trainN < n ? (size_t)trainN * rowB : 0);
+    if (trainN < n) {
+        launch_gather_points(dData.as<float>(), dPerm.as<int>(), trainN, dim, dTrainBuf.as<float>(), s);
+        dTrain = dTrainBuf.as<float>();
+    }
+
+    DevMem dAssign((size_t)n * sizeof(int)), dOrder((size_t)n * sizeof(int)), dCounts((size_t)nlist * sizeof(int));
+    DevMem dStart((size_t)(nlist + 1) * sizeof(int)), dReseed((size_t)nlist * sizeof(int));
+    CellGrouping grouping;
+    std::vector<int> counts((size_t)nlist), start((size_t)nlist + 1), reseed((size_t)nlist);
+    auto assignAll = [&](const float* pts, int m) {
+        assigner.reset();
+        assigner.addDevice(dCent.as<float>(), nlist, s);
+        assigner.searchDevice(pts, m, 1, dAssign.as<int32_t>(), nullptr, s);
+        grouping.group(dAssign.as<int>(), m, nlist, dOrder.as<int>(), dCounts.as<int>(), s);
+        HIPC(hipMemcpyAsync(counts.data(), dCounts.p, (size_t)nlist * sizeof(int), hipMemcpyDeviceToHost, s));
+        HIPC(hipStreamSynchronize(s));
+        start[0] = 0;
+        for (int c = 0; c < nlist; ++c) start[(size_t)c + 1] = start[(size_t)c] + counts[(size_t)c];
+    };
+
+    for (int it = 0; it < iters; ++it) {
+        assignAll(dTrain, trainN);
+        // empty cells, in ascending order, take training point rng() % trainN
+        // (reference src/Internal.h:93-98)
+        for (int c = 0; c < nlist; ++c)
+            reseed[(size_t)c] = counts[(size_t)c] == 0 ? (int)(rng() % (uint32_t)trainN) : -1;
+        HIPC(hipMemcpyAsync(dStart.p, start.data(), start.size() * sizeof(int), hipMemcpyHostToDevice, s));
+        HIPC(hipMemcpyAsync(dReseed.p, reseed.data(), reseed.size() * sizeof(int), hipMemcpyHostToDevice, s));
+        launch_update_centroids(dTrain, dim, dOrder.as<int>(), dStart.as<int>(), dReseed.as<int>(), nlist,
+                                dCent.as<float>(), s);
+    }
+    // final assignment of every point (reference src/Internal.h:357-359) and its CSR
+    // (src/CoarseQuantizer.mm:135-145)
+    assignAll(dData.as<float>(), n);
+    HIPC(hipMemcpyAsync(centroids, dCent.p, (size_t)nlist * rowB, hipMemcpyDeviceToHost, s));
+    if (assign) HIPC(hipMemcpyAsync(assign, dAssign.p, (size_t)n * sizeof(int), hipMemcpyDeviceToHost, s));
+    if (order) HIPC(hipMemcpyAsync(order, dOrder.p, (size_t)n * sizeof(int), hipMemcpyDeviceToHost, s));
+    HIPC(hipStreamSynchronize(s));
+    if (cellStart) std::copy(start.begin(), start.end(), cellStart);
+    return nlist;
+}
+
+}  // namespace mflat_amd

@@ -14,6 +14,7 @@
 
 #include "../../include/mflat.h"
 #include "flat_index.hpp"
+#include "kmeans.hpp"
 #include "log.hpp"
 
 using mflat_amd::FlatIndex;
@@ -217,6 +218,17 @@ MFLAT_API mflat_status_t mflat_flat_add_device(mflat_flat_index_t* h, const floa
         if (n > 0 && !h->idx.ready())
             throw mflat_amd::NotReady("no usable HIP device: device-pointer add needs a gfx950 GPU");
         h->idx.addDevice(v, n, static_cast<hipStream_t>(stream));
+        return MFLAT_OK;
+    });
+}
+
+MFLAT_API mflat_status_t mflat_kmeans_train(const float* pts, int n, int dim, int nlist, int iters, int mpc,
+                                            float* oc, int32_t* oa, int32_t* ocs, int32_t* oo, int* onl) {
+    if (!pts || !oc) return MFLAT_ERR_NULL_ARG;
+    if (n < 1 || dim < 1 || nlist < 1 || iters < 0 || mpc < 0) return MFLAT_ERR_BAD_ARG;
+    return guarded([&] {
+        const int used = mflat_amd::kmeansTrain(pts, n, dim, nlist, iters, mpc, oc, oa, ocs, oo);
+        if (onl) *onl = used;
         return MFLAT_OK;
     });
 }

@@ -59,6 +59,8 @@ SIGNATURES = {
     "mflat_flat_search_device": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p,
                                          POINTER(c_int), c_void_p]),
     "mflat_flat_add_device": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
+    "mflat_kmeans_train": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
+                                   c_void_p, c_void_p, POINTER(c_int)]),
     "mflat_profile_enable": (None, [c_int]),
     "mflat_profile_reset": (None, []),
     "mflat_profile_read": (c_int, [c_char_p, POINTER(c_double), POINTER(c_longlong)]),
@@ -197,6 +199,24 @@ class FlatIndex:
             out_dist.data_ptr() if out_dist is not None else None,
             ctypes.byref(used), _stream_ptr(stream)), "mflat_flat_search_device")
         return used.value
+
+
+def kmeans_train(points, nlist: int, iters: int, max_points_per_centroid: int = 256):
+    """mflat_kmeans_train: returns (centroids [nlist_used, dim] float32,
+    assign [n] int32, cell_start [nlist_used + 1] int32, order [n] int32)."""
+    x = _f32(points)
+    n, d = x.shape
+    nl = min(int(nlist), n)
+    cent = np.empty((max(int(nlist), 1), d), np.float32)
+    assign = np.empty(n, np.int32)
+    start = np.empty(max(int(nlist), 1) + 1, np.int32)
+    order = np.empty(n, np.int32)
+    used = c_int(-1)
+    _check(load().mflat_kmeans_train(x.ctypes.data, n, d, int(nlist), int(iters), int(max_points_per_centroid),
+                                     cent.ctypes.data, assign.ctypes.data, start.ctypes.data, order.ctypes.data,
+                                     ctypes.byref(used)), "mflat_kmeans_train")
+    assert used.value == nl
+    return cent[:nl].copy(), assign, start[: nl + 1].copy(), order
 
 
 def _stream_ptr(stream):

@@ -22,6 +22,10 @@
  *                        (k = 1 assignment; must agree with orc_cpu_search k=1)
  *   orc_brute_lex        bench/bench.mm:52-64 cpuTopkL2: partial sort of
  *                        (dist, id) pairs -- an independent cross-check
+ *   orc_kmeans_update    src/CoarseQuantizer.mm:44-66 (k-means update): per-cell
+ *                        double sums over the points in ascending index order,
+ *                        centroid = float(sum / count); an empty cell copies
+ *                        the row its reseed entry names
  *
  * Build with -ffp-contract=off so no multiply-add is fused: the sums are the
  * plain sequential fp32 sums the reference's C++ source spells out.
@@ -220,4 +224,27 @@ int orc_brute_lex(const float* db, int64_t nb, int dim, const float* q, int64_t 
     }
     free(all);
     return 0;
+}
+
+void orc_kmeans_update(const float* pts, int64_t n, int dim, const int32_t* assign, int nlist,
+                       const int32_t* reseed, float* centroids) {
+    double* sums = (double*)calloc((size_t)nlist * dim, sizeof(double));
+    int64_t* counts = (int64_t*)calloc((size_t)nlist, sizeof(int64_t));
+    if (!sums || !counts) { free(sums); free(counts); return; }
+    for (int64_t i = 0; i < n; ++i) {
+        const float* v = pts + i * dim;
+        double* sc = sums + (int64_t)assign[i] * dim;
+        for (int d = 0; d < dim; ++d) sc[d] += v[d];
+        ++counts[assign[i]];
+    }
+    for (int c = 0; c < nlist; ++c) {
+        float* ce = centroids + (int64_t)c * dim;
+        if (counts[c] > 0) {
+            for (int d = 0; d < dim; ++d) ce[d] = (float)(sums[(int64_t)c * dim + d] / (double)counts[c]);
+        } else {
+            memcpy(ce, pts + (int64_t)reseed[c] * dim, (size_t)dim * sizeof(float));
+        }
+    }
+    free(sums);
+    free(counts);
 }

@@ -42,6 +42,8 @@ def lib():
             f.argtypes = [c_void_p, c_int64, c_int, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_int]
         o.orc_argmin_l2.restype = None
         o.orc_argmin_l2.argtypes = [c_void_p, c_int64, c_void_p, c_int64, c_int, c_void_p, c_void_p]
+        o.orc_kmeans_update.restype = None
+        o.orc_kmeans_update.argtypes = [c_void_p, c_int64, c_int, c_void_p, c_int, c_void_p, c_void_p]
         o.orc_brute_lex.restype = c_int
         o.orc_brute_lex.argtypes = [c_void_p, c_int64, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p]
         _o = o
@@ -169,3 +171,82 @@ def storage_inputs(db, q, metric, storage):
     if metric == 2:
         return (round_storage(normalize_rows(db), storage), round_storage(normalize_rows(q), storage), 1)
     return round_storage(db, storage), round_storage(q, storage), metric
+
+
+# ---- k-means training (the device k-means loop's checker) --------------------
+# Restates the loop of the reference's CoarseQuantizer::train over
+# detail::kmeansGpu (src/CoarseQuantizer.mm:104-159, src/Internal.h:234-382)
+# with the scalar update of src/CoarseQuantizer.mm:44-66, and the library's
+# documented seeding shuffle (the reference's std::shuffle draws are specific to
+# its standard library).
+
+class MT19937Stream:
+    """Raw 32-bit outputs of std::mt19937(seed): numpy's legacy RandomState with
+    an integer seed is the same generator (pinned against the standard's known
+    answer in tests/test_oracle.py)."""
+
+    def __init__(self, seed):
+        self._rs = np.random.RandomState(seed)
+        self._buf = np.empty(0, np.uint32)
+        self._pos = 0
+
+    def __call__(self):
+        if self._pos == self._buf.size:
+            self._buf = np.frombuffer(self._rs.bytes(4 * 4096), dtype="<u4")
+            self._pos = 0
+        v = int(self._buf[self._pos])
+        self._pos += 1
+        return v
+
+
+def bounded(rng, r):
+    """Uniform in [0, r): redraw while u >= 2^32 - 2^32 mod r, then u mod r."""
+    lim = (1 << 32) - ((1 << 32) % r)
+    while True:
+        u = rng()
+        if u < lim:
+            return u % r
+
+
+def seed_permutation(n, rng):
+    """Fisher-Yates from the top with bounded() draws."""
+    perm = list(range(n))
+    for i in range(n - 1, 0, -1):
+        j = bounded(rng, i + 1)
+        perm[i], perm[j] = perm[j], perm[i]
+    return np.array(perm, dtype=np.int64)
+
+
+def kmeans_update(pts, assign, nlist, cent, reseed):
+    pts = _f32(pts)
+    assign = np.ascontiguousarray(assign, np.int32)
+    reseed = np.ascontiguousarray(reseed, np.int32)
+    out = _f32(cent).copy()
+    lib().orc_kmeans_update(pts.ctypes.data, pts.shape[0], pts.shape[1], assign.ctypes.data, nlist,
+                            reseed.ctypes.data, out.ctypes.data)
+    return out
+
+
+def kmeans_train(points, nlist, iters, max_points_per_centroid=256):
+    """Returns (centroids, assign, cell_start, order) as the library's
+    mflat_kmeans_train defines them."""
+    points = _f32(points)
+    n, d = points.shape
+    nlist = min(nlist, n)
+    rng = MT19937Stream(12345)
+    perm = seed_permutation(n, rng)
+    cent = points[perm[:nlist]].copy()
+    train_n = n
+    if max_points_per_centroid > 0 and max_points_per_centroid * nlist < n:
+        train_n = max_points_per_centroid * nlist
+    train = points[perm[:train_n]].copy() if train_n < n else points
+    for _ in range(iters):
+        a, _ = argmin_l2(train, cent)
+        counts = np.bincount(a, minlength=nlist)
+        reseed = np.array([rng() % train_n if counts[c] == 0 else -1 for c in range(nlist)], np.int32)
+        cent = kmeans_update(train, a, nlist, cent, reseed)
+    a, _ = argmin_l2(points, cent)
+    counts = np.bincount(a, minlength=nlist)
+    start = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    order = np.argsort(a, kind="stable").astype(np.int32)
+    return cent, a.astype(np.int32), start, order

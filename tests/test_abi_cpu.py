@@ -157,3 +157,22 @@ def test_profile_names():
         assert ms == 0.0 and n == 0
     with pytest.raises(KeyError):
         mflat.profile_read("nope")
+
+
+def test_kmeans_arguments():
+    lib = mflat.load()
+    x = np.zeros((10, 4), np.float32)
+    c = np.zeros((3, 4), np.float32)
+    used = ctypes.c_int(-1)
+    f = lib.mflat_kmeans_train
+    assert f(None, 10, 4, 3, 1, 0, c.ctypes.data, None, None, None, None) == mflat.MFLAT_ERR_NULL_ARG
+    assert f(x.ctypes.data, 10, 4, 3, 1, 0, None, None, None, None, None) == mflat.MFLAT_ERR_NULL_ARG
+    for n, d, nl, it, mpc in ((0, 4, 3, 1, 0), (10, 0, 3, 1, 0), (10, 4, 0, 1, 0), (10, 4, 3, -1, 0),
+                              (10, 4, 3, 1, -5)):
+        assert f(x.ctypes.data, n, d, nl, it, mpc, c.ctypes.data, None, None, None,
+                 ctypes.byref(used)) == mflat.MFLAT_ERR_BAD_ARG
+    rc = f(x.ctypes.data, 10, 4, 3, 1, 0, c.ctypes.data, None, None, None, ctypes.byref(used))
+    idx = mflat.FlatIndex(4)
+    if not idx.ready():
+        assert rc == mflat.MFLAT_ERR_NOT_READY
+    idx.close()

@@ -243,3 +243,50 @@ def test_storage_inputs_integer_data_is_identity():
         assert m == 0 and np.array_equal(xs, x) and np.array_equal(qs, q)
     xs, qs, m = oracle.storage_inputs(x, q, 2, oracle.STORAGE_BF16)
     assert m == 1 and np.array_equal(xs, oracle.round_bf16(oracle.normalize_rows(x)))
+
+
+# ---- k-means oracle ------------------------------------------------------------
+
+def test_mt19937_stream_known_answers():
+    """The C++ standard fixes the 10000th output of a default-seeded mt19937
+    (seed 5489) at 4123659995 ([rand.predef]); its first output is 3499211612."""
+    r = oracle.MT19937Stream(5489)
+    v = [r() for _ in range(10000)]
+    assert v[0] == 3499211612 and v[-1] == 4123659995
+
+
+def test_bounded_draw_rejects_the_biased_tail():
+    """bounded(r) redraws u >= 2^32 - 2^32 mod r: with r = 3 the largest u
+    (2^32 - 1) is rejected, the next draw 5 gives 5 mod 3."""
+    seq = iter([2 ** 32 - 1, 5, 7])
+    assert oracle.bounded(lambda: next(seq), 3) == 2
+    seq = iter([2 ** 32 - 2, 1])
+    assert oracle.bounded(lambda: next(seq), 3) == (2 ** 32 - 2) % 3
+    r = oracle.MT19937Stream(1)
+    draws = np.array([oracle.bounded(r, 7) for _ in range(70_000)])
+    counts = np.bincount(draws, minlength=7)
+    assert counts.size == 7 and np.all(np.abs(counts - 10_000) < 500)
+    p = oracle.seed_permutation(1000, oracle.MT19937Stream(12345))
+    assert np.array_equal(np.sort(p), np.arange(1000)) and not np.array_equal(p, np.arange(1000))
+
+
+def test_kmeans_update_is_sequential_double_mean():
+    rng = np.random.default_rng(8)
+    pts = (rng.standard_normal((5000, 12)) * 100).astype(np.float32)
+    a = rng.integers(0, 30, 5000).astype(np.int32)
+    a[a == 7] = 8                                  # cell 7 empty -> reseeded from row 123
+    reseed = np.full(30, -1, np.int32)
+    reseed[7] = 123
+    got = oracle.kmeans_update(pts, a, 30, np.zeros((30, 12), np.float32), reseed)
+    for c in range(30):
+        if c == 7:
+            assert np.array_equal(got[c], pts[123])
+            continue
+        rows = pts[a == c].astype(np.float64)
+        seq = np.cumsum(rows, axis=0)[-1]          # sequential, ascending index
+        assert np.array_equal(got[c], (seq / rows.shape[0]).astype(np.float32))
+    ints = rng.integers(-50, 50, size=(400, 5)).astype(np.float32)
+    ai = (np.arange(400) % 4).astype(np.int32)
+    m = oracle.kmeans_update(ints, ai, 4, np.zeros((4, 5), np.float32), np.full(4, -1, np.int32))
+    for c in range(4):
+        assert np.array_equal(m[c], (ints[ai == c].astype(np.float64).sum(0) / 100).astype(np.float32))
