@@ -127,6 +127,35 @@ def cpu_baseline(x, q, k, metric, gpu_ids, storage=0, threads=1, seconds_target=
     }
 
 
+def kmeans_bench(iters):
+    """ms per device k-means iteration (assignment of every training point + the
+    centroid update) on C5's 2,000,000 x 128 points with 65,536 cells, taken as
+    (T(iters) - T(0)) / iters so the upload, seeding and final assignment cancel."""
+    import datagen
+    import mflat
+
+    mflat.load()
+    cents, pts = datagen.kmeans_assign()
+    nlist = cents.shape[0]
+    del cents
+    log(f"[bench] kmeans: {pts.shape[0]} x {pts.shape[1]} points, {nlist} cells, {iters} iterations")
+    mflat.kmeans_train(pts[:100_000], 1024, 1, 256)   # warm-up (kernel loading)
+    t = []
+    for it in (0, iters):
+        t0 = time.perf_counter()
+        mflat.kmeans_train(pts, nlist, it, 256)
+        t.append(time.perf_counter() - t0)
+        log(f"[bench] kmeans iters={it}: {t[-1]:.3f}s")
+    per = (t[1] - t[0]) * 1000.0 / iters
+    flop = 2.0 * pts.shape[0] * nlist * pts.shape[1]
+    print(json.dumps({"metric": "ms per device k-means iteration (assign + update)", "value": round(per, 3),
+                      "unit": "ms", "higher_is_better": False, "n_gpus": 1, "iters": iters,
+                      "config": {"workload": "C5 points (2,000,000 x 128 GMM(4096, sigma 0.5)), 65,536 cells, "
+                                             "max 256 points per cell (all points train), seed 4"},
+                      "assign_tflops_equiv": round(flop / (per / 1000.0) / 1e12, 2),
+                      "total_s": {"iters_0": round(t[0], 3), f"iters_{iters}": round(t[1], 3)}}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -137,6 +166,9 @@ def main():
     ap.add_argument("--storage", default="f32", choices=["f32", "f16", "bf16"],
                     help="element type of the stored database and the queries")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kmeans", type=int, default=0, metavar="ITERS",
+                    help="time the device k-means loop (mflat_kmeans_train) on C5's points and centroid "
+                         "count instead: one JSON line with ms per training iteration")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 3 device-to-device copies of MIB MiB (counter calibration)")
     args = ap.parse_args()
@@ -152,6 +184,10 @@ def main():
             hipmem.check(hipmem.hip().hipMemcpy(dst.ptr, src.ptr, n, hipmem.D2D), "hipMemcpy D2D")
         hipmem.synchronize()
         print(json.dumps({"copy_probe_bytes": n, "copies": 3}), flush=True)
+        return
+
+    if args.kmeans:
+        kmeans_bench(args.kmeans)
         return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
