@@ -309,6 +309,64 @@ __global__ void max_norm_kernel(const float* __restrict__ xn, int64_t n, unsigne
 }
 
 // ---------------------------------------------------------------------------
+// filter epilogue shared by the MFMA scan kernels
+// ---------------------------------------------------------------------------
+//
+// One group of a lane's 32 x 32 accumulators: rows r0 .. r0 + 3 (register
+// g4*4 + i of each block, row norms xn4) against the lane's query slots b0 and
+// b0 + 1 (acc[b0 + b], per-query state tk/ti/qn/ft/qv). Eight fast tests
+// without branches, then one wave-level branch: a group rarely holds a
+// survivor in any of the 64 lanes. Only survivors take the exact
+// lexicographic test; they go to emit(slot, key, id), or, for k = 1, replace
+// the slot's running best.
+template <int METRIC, int PASS, int NB, class Emit>
+__device__ __forceinline__ void filter_group(const fx16 (&acc)[NB], int g4, int b0, const fx4& xn4, int64_t r0,
+                                             const ScanParams& p, float (&tk)[NB], int (&ti)[NB],
+                                             const float (&qn)[NB], float (&ft)[NB], const bool (&qv)[NB],
+                                             Emit&& emit) {
+    bool f[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const float dot = acc[b0 + b][g4 * 4 + i];
+            f[i][b] = METRIC == 0 ? fmaf(-2.0f, dot, xn4[i]) <= ft[b0 + b] : dot >= ft[b0 + b];
+        }
+    const bool any = f[0][0] | f[0][1] | f[1][0] | f[1][1] | f[2][0] | f[2][1] | f[3][0] | f[3][1];
+    if (!any) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t row = r0 + i;
+        const bool rv = row < p.nrows;
+        const int id = (int)(row * p.id_stride);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int bn = b0 + b;
+            if (!f[i][b]) continue;
+            const float dot = acc[bn][g4 * 4 + i];
+            float key;
+            if (METRIC == 0) {
+                const float t = fmaf(-2.0f, dot, qn[bn] + xn4[i]);
+                key = (t < 0.0f ? 0.0f : t) + 0.0f;
+            } else {
+                key = -dot + 0.0f;
+            }
+            if (PASS == kPassArgmin) {
+                // k = 1: keep the lexicographically smallest (key, id)
+                if (rv && qv[bn] && (key < tk[bn] || (key == tk[bn] && id < ti[bn]))) {
+                    tk[bn] = key;
+                    ti[bn] = id;
+                    ft[bn] = METRIC == 0 ? (key - qn[bn]) + 0x1p-20f * (key + 2.0f * qn[bn] + 2.0f * p.xnorm_max)
+                                         : -key;
+                }
+                continue;
+            }
+            if (rv && qv[bn] && (key < tk[bn] || (key == tk[bn] && id <= ti[bn]))) emit(bn, key, id);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // scan_filter: MFMA distance tile + threshold filter
 // ---------------------------------------------------------------------------
 //
@@ -551,59 +609,16 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
                     const int64_t r0 = tileRow0 + rl;
                     fx4 xn4 = {0.0f, 0.0f, 0.0f, 0.0f};
                     if (METRIC == 0) xn4 = xnr[bm][g4];
-                    // 8 fast tests without branches, then one wave-level branch:
-                    // a group rarely holds a survivor in any of the 64 lanes.
-                    bool f[4][2];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-#pragma unroll
-                        for (int bn = 0; bn < 2; ++bn) {
-                            const float dot = acc[bm][bn][g4 * 4 + i];
-                            f[i][bn] = METRIC == 0 ? fmaf(-2.0f, dot, xn4[i]) <= ft[bn] : dot >= ft[bn];
+                    filter_group<METRIC, PASS, 2>(acc[bm], g4, 0, xn4, r0, p, tk, ti, qn, ft, qv,
+                                                  [&](int bn, float key, int id) {
+                        const int ql = wn * 64 + bn * 32 + r32;
+                        const int slot = atomicAdd(&sCnt[ql], 1);
+                        if (slot < p.cap) {
+                            const int64_t q = (int64_t)qb * kBN + ql;
+                            p.cand[(q * p.nsplit + split) * p.cap + slot] =
+                                make_uint2(__float_as_uint(key), (unsigned)id);
                         }
-                    const bool any = f[0][0] | f[0][1] | f[1][0] | f[1][1] | f[2][0] | f[2][1] |
-                                     f[3][0] | f[3][1];
-                    if (!any) continue;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int64_t row = r0 + i;
-                        const bool rv = row < p.nrows;
-                        const int id = (int)(row * p.id_stride);
-#pragma unroll
-                        for (int bn = 0; bn < 2; ++bn) {
-                            if (!f[i][bn]) continue;
-                            const float dot = acc[bm][bn][g4 * 4 + i];
-                            float key;
-                            if (METRIC == 0) {
-                                const float t = fmaf(-2.0f, dot, qn[bn] + xn4[i]);
-                                key = (t < 0.0f ? 0.0f : t) + 0.0f;
-                            } else {
-                                key = -dot + 0.0f;
-                            }
-                            if (PASS == kPassArgmin) {
-                                // k = 1: keep the lexicographically smallest (key, id)
-                                if (rv && qv[bn] && (key < tk[bn] || (key == tk[bn] && id < ti[bn]))) {
-                                    tk[bn] = key;
-                                    ti[bn] = id;
-                                    ft[bn] = METRIC == 0
-                                        ? (key - qn[bn]) + 0x1p-20f * (key + 2.0f * qn[bn] + 2.0f * p.xnorm_max)
-                                        : -key;
-                                }
-                                continue;
-                            }
-                            const bool pass = rv && qv[bn] &&
-                                              (key < tk[bn] || (key == tk[bn] && id <= ti[bn]));
-                            if (pass) {
-                                const int ql = wn * 64 + bn * 32 + r32;
-                                const int slot = atomicAdd(&sCnt[ql], 1);
-                                if (slot < p.cap) {
-                                    const int64_t q = (int64_t)qb * kBN + ql;
-                                    p.cand[(q * p.nsplit + split) * p.cap + slot] =
-                                        make_uint2(__float_as_uint(key), (unsigned)id);
-                                }
-                            }
-                        }
-                    }
+                    });
                 }
             }
         }
@@ -810,65 +825,24 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
                 fx4 xn4 = {0.0f, 0.0f, 0.0f, 0.0f};
                 if (METRIC == 0) xn4 = *(const fx4*)(sXn + wave * 64 + rl);
 #pragma unroll
-                for (int bp = 0; bp < 2; ++bp) {
-                    bool f[4][2];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-#pragma unroll
-                        for (int b = 0; b < 2; ++b) {
-                            const float dot = acc[bm][2 * bp + b][g4 * 4 + i];
-                            f[i][b] = METRIC == 0 ? fmaf(-2.0f, dot, xn4[i]) <= ft[2 * bp + b] : dot >= ft[2 * bp + b];
-                        }
-                    const bool any = f[0][0] | f[0][1] | f[1][0] | f[1][1] | f[2][0] | f[2][1] |
-                                     f[3][0] | f[3][1];
-                    if (!any) continue;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int64_t row = r0 + i;
-                        const bool rv = row < p.nrows;
-                        const int id = (int)(row * p.id_stride);
-#pragma unroll
-                        for (int b = 0; b < 2; ++b) {
-                            const int bn = 2 * bp + b;
-                            if (!f[i][b]) continue;
-                            const float dot = acc[bm][bn][g4 * 4 + i];
-                            float key;
-                            if (METRIC == 0) {
-                                const float t = fmaf(-2.0f, dot, qn[bn] + xn4[i]);
-                                key = (t < 0.0f ? 0.0f : t) + 0.0f;
-                            } else {
-                                key = -dot + 0.0f;
-                            }
-                            if (PASS == kPassArgmin) {
-                                if (rv && qv[bn] && (key < tk[bn] || (key == tk[bn] && id < ti[bn]))) {
-                                    tk[bn] = key;
-                                    ti[bn] = id;
-                                    ft[bn] = METRIC == 0
-                                        ? (key - qn[bn]) + 0x1p-20f * (key + 2.0f * qn[bn] + 2.0f * p.xnorm_max)
-                                        : -key;
-                                }
-                                continue;
-                            }
-                            const bool pass = rv && qv[bn] && (key < tk[bn] || (key == tk[bn] && id <= ti[bn]));
-                            if (pass) {
-                                const int ql = bn * 32 + r32;
-                                const int pos = RING ? atomicAdd(&sRingN[wave], 1) : kRing;
-                                if (pos < kRing) {
-                                    sRingKey[wave * kRing + pos] = __float_as_uint(key);
-                                    sRingId[wave * kRing + pos] = id;
-                                    sRingQ[wave * kRing + pos] = ql;
-                                } else {   // ring full (or not used): store directly
-                                    const int slot = atomicAdd(&sCnt[ql], 1);
-                                    if (slot < p.cap) {
-                                        const int64_t q = (int64_t)qb * kBN + ql;
-                                        p.cand[(q * p.nsplit + split) * p.cap + slot] =
-                                            make_uint2(__float_as_uint(key), (unsigned)id);
-                                    }
-                                }
+                for (int bp = 0; bp < 2; ++bp)
+                    filter_group<METRIC, PASS, 4>(acc[bm], g4, 2 * bp, xn4, r0, p, tk, ti, qn, ft, qv,
+                                                  [&](int bn, float key, int id) {
+                        const int ql = bn * 32 + r32;
+                        const int pos = RING ? atomicAdd(&sRingN[wave], 1) : kRing;
+                        if (pos < kRing) {
+                            sRingKey[wave * kRing + pos] = __float_as_uint(key);
+                            sRingId[wave * kRing + pos] = id;
+                            sRingQ[wave * kRing + pos] = ql;
+                        } else {   // ring full (or not used): store directly
+                            const int slot = atomicAdd(&sCnt[ql], 1);
+                            if (slot < p.cap) {
+                                const int64_t q = (int64_t)qb * kBN + ql;
+                                p.cand[(q * p.nsplit + split) * p.cap + slot] =
+                                    make_uint2(__float_as_uint(key), (unsigned)id);
                             }
                         }
-                    }
-                }
+                    });
             }
         }
     };
@@ -1856,6 +1830,15 @@ void launch_select(const SelectParams& p, hipStream_t s) {
     if (p.k < 1 || p.k > kTopMax || p.j < 1 || p.j > p.k || p.j2 < 1 || p.j2 > p.k)
         throw std::runtime_error("select: bad k/j");
     if (p.nsplit < 1 || p.nsplit > kMaxSplit) throw std::runtime_error("select: bad nsplit");
+    // the split offsets (dynamic LDS) reach (kMaxSplit + 1) ints, above the
+    // default dynamic-LDS limit of a launch
+    static const bool attr = [] {
+        if (hipFuncSetAttribute((const void*)select_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)((kMaxSplit + 1) * sizeof(int))) != hipSuccess)
+            throw std::runtime_error("select: cannot raise the dynamic LDS limit");
+        return true;
+    }();
+    (void)attr;
     void* tok;
     prof_begin(kFamSelect, s, &tok);
     select_kernel<<<p.nq, 256, (size_t)(p.nsplit + 1) * sizeof(int), s>>>(p);
