@@ -19,8 +19,12 @@
  *    created and filled (mflat_flat_ready() == 0) but mflat_flat_search
  *    returns MFLAT_ERR_NOT_READY (reference: exact CPU path,
  *    src/FlatIndex.mm:317-321).
- *  - The IVF / IVF-PQ entry points (reference c/include/mflat.h:92-129) are
- *    not part of this library.
+ *  - The IVF entry points (reference c/include/mflat.h:92-105) are here,
+ *    with the same argument checks and result layout; IVF search serves
+ *    k <= MFLAT_MAX_K and nprobe <= MFLAT_MAX_K on the device (the reference
+ *    serves k > 64 on its CPU path, src/IvfIndex.mm:762-764), and the fine
+ *    scan needs dim <= 128 (fp32) or <= 256 (fp16 / bf16 storage). The IVF-PQ
+ *    entry points (c/include/mflat.h:107-129) are not part of this library.
  *  - Additive entry points (reduced-precision storage, device-pointer
  *    search/add, kernel timing) follow the flat block; they have no
  *    counterpart in the reference.
@@ -105,6 +109,37 @@ MFLAT_API mflat_status_t mflat_flat_reset(mflat_flat_index_t*);
 MFLAT_API mflat_status_t mflat_flat_search(mflat_flat_index_t*, const float* queries,
         int m, int k, int32_t* out_ids, float* out_distances, int* out_k_used);
 
+/* ---------------- IvfIndex (approximate) ---------------------------------- */
+/* reference c/include/mflat.h:92-105, c/mflat.cpp:131-159, src/IvfIndex.mm.
+   build() trains nlist k-means cells (12 iterations, at most 256 training
+   points per centroid; nlist clamped to n) and files every row under its
+   nearest centroid; search() takes each query's nprobe nearest centroids
+   (nprobe clamped to [1, nlist]) and returns the exact top-k over the rows of
+   those cells: ids are the caller's row indices, values as for the flat
+   index, ties in scan order (cells nearest first, rows in ascending id within
+   a cell), -1 / +-inf padding when the probed cells hold fewer than k rows. */
+typedef struct mflat_ivf_index mflat_ivf_index_t;      /* opaque */
+
+/* reference c/mflat.cpp:132-137: dim <= 0 or nlist <= 0 -> NULL + BAD_ARG */
+MFLAT_API mflat_ivf_index_t*
+mflat_ivf_create(int dim, mflat_metric_t metric, int nlist, mflat_status_t* out_status);
+MFLAT_API void mflat_ivf_free(mflat_ivf_index_t*);      /* NULL is a no-op */
+
+MFLAT_API int mflat_ivf_ready(const mflat_ivf_index_t*);  /* 1 after build() */
+MFLAT_API int mflat_ivf_size (const mflat_ivf_index_t*);
+MFLAT_API int mflat_ivf_dim  (const mflat_ivf_index_t*);
+MFLAT_API int mflat_ivf_nlist(const mflat_ivf_index_t*);  /* requested, then trained */
+
+/* reference c/mflat.cpp:144-150: NULL -> NULL_ARG, n <= 0 -> BAD_ARG; rows
+   are host memory, borrowed for the call; a rebuild replaces the index.
+   No usable device -> MFLAT_ERR_NOT_READY (no CPU fallback). */
+MFLAT_API mflat_status_t mflat_ivf_build(mflat_ivf_index_t*, const float* vectors, int n);
+/* reference c/mflat.cpp:151-159: NULL -> NULL_ARG; m < 0, k < 1 or
+   nprobe < 1 -> BAD_ARG; not built -> NOT_READY; m == 0 -> OK, k_used 0.
+   Outputs hold m * k elements with row stride k_used. */
+MFLAT_API mflat_status_t mflat_ivf_search(mflat_ivf_index_t*, const float* queries,
+        int m, int k, int nprobe, int32_t* out_ids, float* out_distances, int* out_k_used);
+
 /* ---------------- Additive: reduced-precision storage --------------------- */
 /* No counterpart in the reference (its FlatIndex stores fp32 only,
    src/FlatIndex.mm:236-245). The index holds its database, and each search
@@ -175,6 +210,27 @@ MFLAT_API mflat_status_t mflat_flat_search_device(mflat_flat_index_t*, const flo
         void* stream);
 MFLAT_API mflat_status_t mflat_flat_add_device(mflat_flat_index_t*, const float* d_vectors,
         int n, void* stream);
+
+/* ---------------- Additive: IVF extensions ------------------------------- */
+/* No C counterpart in the reference. mflat_ivf_create_ex: as mflat_ivf_create
+   with the fine scan's storage type (the rows and the queries of the fine scan
+   rounded as for mflat_flat_create_ex; the coarse probe stays fp32).
+   mflat_ivf_search_device: as mflat_ivf_search on device pointers (as
+   mflat_flat_search_device). mflat_ivf_probe: the coarse stage alone, the
+   m * nprobe nearest cells, nearest first (CoarseQuantizer::probeCells,
+   src/CoarseQuantizer.mm:170-188). mflat_ivf_coarse: the coarse layer after
+   build (CoarseQuantizer accessors, src/CoarseQuantizer.h): out_centroids
+   nlist * dim, out_cell_start nlist + 1, out_reordered_ids size() row ids in
+   cell order; each nullable. */
+MFLAT_API mflat_ivf_index_t*
+mflat_ivf_create_ex(int dim, mflat_metric_t metric, int nlist, mflat_storage_t storage, mflat_status_t* out_status);
+MFLAT_API mflat_storage_t mflat_ivf_storage(const mflat_ivf_index_t*);
+MFLAT_API mflat_status_t mflat_ivf_search_device(mflat_ivf_index_t*, const float* d_queries, int m, int k,
+        int nprobe, int32_t* d_out_ids, float* d_out_distances, int* out_k_used, void* stream);
+MFLAT_API mflat_status_t mflat_ivf_probe(mflat_ivf_index_t*, const float* queries, int m, int nprobe,
+        int32_t* out_cells);
+MFLAT_API mflat_status_t mflat_ivf_coarse(const mflat_ivf_index_t*, float* out_centroids,
+        int32_t* out_cell_start, int32_t* out_reordered_ids);
 
 /* ---------------- Additive: kernel timing -------------------------------- */
 /* No counterpart in the reference. When enabled, every launch of the library's

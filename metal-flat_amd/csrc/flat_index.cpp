@@ -352,6 +352,7 @@ struct FlatIndex::Impl {
         cand.ensure((size_t)nq * nsplit * cap * sizeof(uint2));
         cnt.ensure((size_t)nq * nsplit * sizeof(int));
         ScanParams p;
+        std::memset(&p, 0, sizeof p);
         p.X = Xs; p.xnorm = xns; p.xnorm_max = xnMax; p.nrows = nrows; p.rows_per_split = rps; p.nsplit = nsplit;
         p.id_stride = idStride;
         p.Q = Q; p.qnorm = qn; p.nq = nq; p.nqb = nqb; p.dpad = dpad;

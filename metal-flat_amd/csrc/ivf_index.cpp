@@ -1,0 +1,511 @@
+// SPDX-License-Identifier: Apache-2.0
+// ivf_index.cpp -- host side of the IVF index on one MI355X.
+//
+// Build (reference src/IvfIndex.mm:480-516, src/CoarseQuantizer.mm:104-159):
+// Cosine rows normalised; device k-means (kmeansTrainDevice: 12 iterations,
+// 256 training points per centroid); the rows stored cell-major in the flat
+// scan's chunked layout, each cell padded to a multiple of kBM rows (zero rows,
+// never reported); the centroids go to an fp32 L2 FlatIndex, the coarse probe.
+//
+// Search of a batch (reference src/IvfIndex.mm:759-879 and searchCpu :518-560):
+//   probe    the coarse FlatIndex's top-nprobe over the centroids (nearest
+//            first, ties to the lower cell id: the reference's FlatIndex probe
+//            and its partial_sort over (distance, cell), CoarseQuantizer.mm:170-188)
+//   A bound  each query's nearest cell alone, no bound; the k-th best (key,
+//            scan position) of what it stored is a GUARANTEED bound -- the k-th
+//            best over a subset of the probed rows is never better than the
+//            k-th best over all of them (skipped for nprobe = 1)
+//   B scan   all probed cells with that bound; select the k best of the
+//            stored survivors. Exact unless a candidate region overflowed.
+//   retry    overflowed queries rerun B with the k-th best of what they
+//            stored as the bound, into regions that hold a whole cell each
+//            (no overflow is possible), so one retry is final.
+//   finalize scan positions -> original row ids.
+// The ranking key and the bound test are the flat index's (kernels.hpp), so a
+// row's key is the same in every pass of a search.
+#include "ivf_index.hpp"
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "ivf_kernels.hpp"
+#include "kernels.hpp"
+#include "kmeans.hpp"
+#include "log.hpp"
+
+namespace mflat_amd {
+namespace {
+
+void hipCheck(hipError_t e, const char* what) {
+    if (e == hipSuccess) return;
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) throw std::bad_alloc();
+    throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+#define HIPC(x) hipCheck((x), #x)
+
+constexpr int kTrainIters = 12;            // reference src/IvfIndex.mm:493
+constexpr int kPointsPerCentroid = 256;    // reference src/CoarseQuantizer.mm:116-117
+constexpr size_t kCandBudget = size_t(3) << 30;   // candidate regions per batch
+constexpr int kCapAMax = 4096;             // bound pass: entries stored per query
+
+int64_t roundUp(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+int pow2ceil(int64_t x) {
+    int p = 1;
+    while (p < x) p <<= 1;
+    return p;
+}
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    ~DevBuf() { release(); }
+    void ensure(size_t b) {
+        if (b <= bytes) return;
+        release();
+        const size_t want = std::max(b, bytes + bytes / 2);
+        HIPC(hipMalloc(&p, want));
+        bytes = want;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+    template <class T> T* as() const { return static_cast<T*>(p); }
+};
+
+}  // namespace
+
+struct IvfIndex::Impl {
+    int dim = 0, dpad = 0;
+    Metric metric = Metric::L2;
+    int storage = kF32;
+    int esize = 4;
+    int nlistReq = 1;
+    int nlist = 0;
+    int64_t n = 0;
+    int64_t rowsPad = 0;   // stored rows, cells padded to kBM
+    int maxCell = 0;
+    bool built = false;
+    bool devOk = false;
+    bool warnedK = false;
+    int device = -1;
+    hipStream_t stream = nullptr;
+
+    std::unique_ptr<FlatIndex> coarse;
+    DevBuf X, xn, maxBits;
+    float xnMax = 0.0f;
+    DevBuf dCellSize, dCellPad, dCellStart, dRid, dCellOrder;
+    std::vector<float> hCent;
+    std::vector<int> hStart, hRid;
+
+    // per-search workspace
+    DevBuf qin, outIds, outVals, qbuf, qh, qnorm, qrm, probe, pos, posOut, cand, cnt;
+    DevBuf tauAk, tauAi, tauKk, tauKi, status;
+    DevBuf cQ, cQn, cTk, cTi, cIdx, cProbe, cPos;
+    IvfWorkTable wt;
+
+    int kernMetric() const { return metric == Metric::L2 ? 0 : 1; }
+    float emptyValue() const { return metric == Metric::L2 ? INFINITY : -INFINITY; }
+    void setDevice() const {
+        if (device >= 0) HIPC(hipSetDevice(device));
+    }
+
+    void buildFrom(const float* src, int nrows, hipMemcpyKind kind, hipStream_t s) {
+        if (nrows <= 0) return;   // reference src/IvfIndex.mm:481: nothing to build
+        if (!devOk) throw NotReady("no usable HIP device: IVF build needs a gfx950 GPU");
+        setDevice();
+        const size_t rowB = (size_t)dim * sizeof(float);
+        // the caller's rows are borrowed: a device copy, normalised for Cosine
+        // (reference src/IvfIndex.mm:486-487, src/Distance.h:50-60)
+        DevBuf data, inv;
+        data.ensure((size_t)nrows * rowB);
+        HIPC(hipMemcpyAsync(data.p, src, (size_t)nrows * rowB, kind, s));
+        if (metric == Metric::Cosine) {
+            inv.ensure((size_t)nrows * sizeof(float));
+            launch_row_inv_norms(data.as<float>(), nrows, dim, inv.as<float>(), s);
+            launch_scale_rows(data.as<float>(), nrows, dim, inv.as<float>(), s);
+        }
+        // coarse quantizer: k-means and the CSR of the final assignment
+        const int nlMax = std::min(nlistReq, nrows);
+        DevBuf cent, order;
+        cent.ensure((size_t)nlMax * rowB);
+        order.ensure((size_t)nrows * sizeof(int));
+        std::vector<int> start((size_t)nlMax + 1);
+        const int nl = kmeansTrainDevice(data.as<float>(), nrows, dim, nlistReq, kTrainIters, kPointsPerCentroid,
+                                         cent.as<float>(), nullptr, order.as<int>(), start.data(), s);
+        std::vector<int> rid((size_t)nrows);
+        std::vector<float> centH((size_t)nl * dim);
+        HIPC(hipMemcpyAsync(rid.data(), order.p, (size_t)nrows * sizeof(int), hipMemcpyDeviceToHost, s));
+        HIPC(hipMemcpyAsync(centH.data(), cent.p, centH.size() * sizeof(float), hipMemcpyDeviceToHost, s));
+        HIPC(hipStreamSynchronize(s));
+
+        // cell-major layout: cell c at rows [pad[c], pad[c] + size[c]) of X
+        std::vector<int> size((size_t)nl), cellOrder((size_t)nl);
+        std::vector<int64_t> pad((size_t)nl);
+        int64_t P = 0;
+        int mc = 0;
+        for (int c = 0; c < nl; ++c) {
+            size[(size_t)c] = start[(size_t)c + 1] - start[(size_t)c];
+            pad[(size_t)c] = P;
+            P += roundUp(size[(size_t)c], kBM);
+            mc = std::max(mc, size[(size_t)c]);
+        }
+        P = std::max<int64_t>(P, kBM);
+        std::vector<int> slotSrc((size_t)P, -1);
+        for (int c = 0; c < nl; ++c)
+            for (int i = 0; i < size[(size_t)c]; ++i)
+                slotSrc[(size_t)(pad[(size_t)c] + i)] = rid[(size_t)start[(size_t)c] + i];
+        // work items run in decreasing cell size (the largest first), ties by cell
+        std::iota(cellOrder.begin(), cellOrder.end(), 0);
+        std::stable_sort(cellOrder.begin(), cellOrder.end(),
+                         [&](int a, int b) { return size[(size_t)a] > size[(size_t)b]; });
+
+        DevBuf slot, tmp;
+        slot.ensure((size_t)P * sizeof(int));
+        tmp.ensure((size_t)P * rowB);
+        HIPC(hipMemcpyAsync(slot.p, slotSrc.data(), (size_t)P * sizeof(int), hipMemcpyHostToDevice, s));
+        launch_gather_rows_or_zero(data.as<float>(), slot.as<int>(), P, dim, tmp.as<float>(), s);
+        X.release();
+        xn.release();
+        X.ensure((size_t)P * dpad * esize);
+        xn.ensure((size_t)P * sizeof(float));
+        HIPC(hipMemsetAsync(X.p, 0, (size_t)P * dpad * esize, s));
+        launch_store_rows_blk(tmp.as<float>(), P, dim, nullptr, X.p, 0, dpad, storage, s);
+        launch_row_norms_blk(X.p, 0, P, dpad, storage, xn.as<float>(), s);
+        maxBits.ensure(sizeof(unsigned));
+        HIPC(hipMemsetAsync(maxBits.p, 0, sizeof(unsigned), s));
+        launch_max_norm(xn.as<float>(), P, maxBits.as<unsigned>(), s);
+        float xm = 0.0f;
+        HIPC(hipMemcpyAsync(&xm, maxBits.p, sizeof(float), hipMemcpyDeviceToHost, s));
+
+        dCellSize.ensure((size_t)nl * sizeof(int));
+        dCellPad.ensure((size_t)nl * sizeof(int64_t));
+        dCellStart.ensure(((size_t)nl + 1) * sizeof(int));
+        dRid.ensure((size_t)nrows * sizeof(int));
+        dCellOrder.ensure((size_t)nl * sizeof(int));
+        HIPC(hipMemcpyAsync(dCellSize.p, size.data(), (size_t)nl * sizeof(int), hipMemcpyHostToDevice, s));
+        HIPC(hipMemcpyAsync(dCellPad.p, pad.data(), (size_t)nl * sizeof(int64_t), hipMemcpyHostToDevice, s));
+        HIPC(hipMemcpyAsync(dCellStart.p, start.data(), ((size_t)nl + 1) * sizeof(int), hipMemcpyHostToDevice, s));
+        HIPC(hipMemcpyAsync(dRid.p, order.p, (size_t)nrows * sizeof(int), hipMemcpyDeviceToDevice, s));
+        HIPC(hipMemcpyAsync(dCellOrder.p, cellOrder.data(), (size_t)nl * sizeof(int), hipMemcpyHostToDevice, s));
+
+        coarse.reset(new FlatIndex(dim, Metric::L2, kF32));
+        coarse->addDevice(cent.as<float>(), nl, s);
+        HIPC(hipStreamSynchronize(s));
+
+        xnMax = xm;
+        nlist = nl;
+        n = nrows;
+        rowsPad = P;
+        maxCell = mc;
+        hCent.swap(centH);
+        start.resize((size_t)nl + 1);
+        hStart.swap(start);
+        hRid.swap(rid);
+        built = true;
+    }
+
+    // One fine-scan pass over the work table wt (built for nq queries).
+    void scanPass(int pass, int nq, int ranks, int nprobe, int nreg, int cap, const void* Q, const float* qn,
+                  const float* tk, const int* ti, const int* posb, hipStream_t s) {
+        cand.ensure((size_t)nq * nreg * cap * sizeof(uint2));
+        cnt.ensure((size_t)nq * nreg * sizeof(int));
+        // every region a work item covers gets its count from it; the others
+        // (entries without a cell) stay empty
+        HIPC(hipMemsetAsync(cnt.p, 0, (size_t)nq * nreg * sizeof(int), s));
+        ScanParams p;
+        std::memset(&p, 0, sizeof p);
+        p.X = X.p; p.xnorm = xn.as<float>(); p.xnorm_max = xnMax; p.nrows = rowsPad;
+        p.rows_per_split = kBM; p.nsplit = 1; p.id_stride = 1;
+        p.Q = Q; p.qnorm = qn; p.nq = nq; p.nqb = (nq + kBN - 1) / kBN; p.dpad = dpad;
+        p.tau_key = tk; p.tau_id = ti;
+        p.cand = cand.as<uint2>(); p.cnt = cnt.as<int>(); p.cap = cap;
+        p.ivf_work = wt.work; p.ivf_nwork = wt.nwork; p.ivf_ent = wt.ent; p.ivf_pos = posb;
+        p.ivf_cell_pad = dCellPad.as<int64_t>(); p.ivf_cell_size = dCellSize.as<int>();
+        p.ivf_nprobe = nprobe; p.ivf_nreg = nreg;
+        launch_scan_ivf(p, kernMetric(), pass, storage, wt.maxWork(nq, ranks, nlist), s);
+    }
+
+    SelectParams selectParams(int nq, int nsplit, int cap, int k) const {
+        SelectParams sp;
+        std::memset(&sp, 0, sizeof sp);
+        sp.cand = cand.as<uint2>(); sp.cnt = cnt.as<int>();
+        sp.nsplit = nsplit; sp.cap = cap; sp.nq = nq; sp.k = k; sp.j = k; sp.j2 = k;
+        sp.metric = kernMetric();
+        sp.out_stride = k;
+        return sp;
+    }
+
+    // Region capacities. capA: bound pass, per query; capB: full pass, per
+    // (query, probe rank) -- a whole cell when nprobe = 1 (no bound, every row
+    // stored); capR: retries, a whole cell.
+    int capA(int k) const { return (int)std::max<int64_t>(k, std::min<int64_t>(roundUp(std::max(maxCell, 1), 64), kCapAMax)); }
+    int capR() const { return (int)roundUp(std::max(maxCell, 1), 64); }
+    // MFLAT_IVF_CAP_B (diagnostics) overrides capB to exercise the retries;
+    // the results never depend on it, only the work done.
+    int capB(int k, int nprobe) const {
+        if (const char* e = std::getenv("MFLAT_IVF_CAP_B")) {
+            const int v = std::atoi(e);
+            if (v >= 1) return v;
+        }
+        return nprobe == 1 ? capR() : pow2ceil(std::max(2 * k, 128));
+    }
+
+    // Search mb staged queries (qbuf / qh, norms in qnorm, probes in probe).
+    void searchBatch(int mb, int k, int nprobe, int32_t* oIds, float* oVals, hipStream_t s) {
+        const void* Q = storage == kF32 ? qbuf.p : qh.p;
+        const float* qn = qnorm.as<float>();
+        pos.ensure((size_t)mb * nprobe * sizeof(int));
+        launch_ivf_positions(probe.as<int>(), mb, nprobe, dCellSize.as<int>(), pos.as<int>(), s);
+        tauAk.ensure((size_t)mb * 4); tauAi.ensure((size_t)mb * 4);
+        tauKk.ensure((size_t)mb * 4); tauKi.ensure((size_t)mb * 4);
+        status.ensure((size_t)mb * 4);
+        launch_fill_tau_none(tauAk.as<float>(), tauAi.as<int>(), mb, s);
+        if (nprobe > 1) {
+            // A: the nearest cell of every query, no bound -> guaranteed bound
+            const int ca = capA(k);
+            wt.build(probe.as<int>(), mb, nprobe, 1, nlist, dCellOrder.as<int>(), s);
+            scanPass(kPassSample, mb, 1, nprobe, 1, ca, Q, qn, tauAk.as<float>(), tauAi.as<int>(), pos.as<int>(), s);
+            SelectParams sp = selectParams(mb, 1, ca, k);
+            sp.tau_k_key = tauAk.as<float>(); sp.tau_k_id = tauAi.as<int>();
+            launch_select(sp, s);
+        }
+        // B: every probed cell under the bound
+        const int cb = capB(k, nprobe);
+        int32_t* posIds = oIds;
+        if (!posIds) {
+            posOut.ensure((size_t)mb * k * sizeof(int32_t));
+            posIds = posOut.as<int32_t>();
+        }
+        wt.build(probe.as<int>(), mb, nprobe, nprobe, nlist, dCellOrder.as<int>(), s);
+        scanPass(kPassFull, mb, nprobe, nprobe, nprobe, cb, Q, qn, tauAk.as<float>(), tauAi.as<int>(), pos.as<int>(),
+                 s);
+        {
+            SelectParams sp = selectParams(mb, nprobe, cb, k);
+            sp.out_ids = posIds; sp.out_vals = oVals;
+            sp.tau_k_key = tauKk.as<float>(); sp.tau_k_id = tauKi.as<int>();
+            sp.status = status.as<int>();
+            launch_select(sp, s);
+        }
+        std::vector<int> st((size_t)mb);
+        HIPC(hipMemcpyAsync(st.data(), status.p, (size_t)mb * 4, hipMemcpyDeviceToHost, s));
+        HIPC(hipStreamSynchronize(s));
+        std::vector<int> over;
+        for (int i = 0; i < mb; ++i)
+            if (st[(size_t)i] & 1) over.push_back(i);
+        if (!over.empty()) {
+            // retries: bound = k-th of the stored survivors, whole-cell regions
+            const int cr = capR();
+            const size_t perQ = (size_t)nprobe * cr * sizeof(uint2);
+            const int chunk = (int)std::max<size_t>(1, std::min<size_t>(over.size(), kCandBudget / perQ));
+            if (std::getenv("MFLAT_TRACE"))
+                std::fprintf(stderr, "[mflat trace] ivf: %d of %d queries overflowed (cap %d), retried with cap %d\n",
+                             (int)over.size(), mb, cb, cr);
+            for (size_t o = 0; o < over.size(); o += (size_t)chunk) {
+                const int nf = (int)std::min<size_t>((size_t)chunk, over.size() - o);
+                const int nfPad = (int)roundUp(nf, kBN);
+                cIdx.ensure((size_t)nf * 4);
+                cQ.ensure((size_t)nfPad * dpad * esize); cQn.ensure((size_t)nfPad * 4);
+                cTk.ensure((size_t)nf * 4); cTi.ensure((size_t)nf * 4);
+                cProbe.ensure((size_t)nf * nprobe * 4); cPos.ensure((size_t)nf * nprobe * 4);
+                HIPC(hipMemcpyAsync(cIdx.p, over.data() + o, (size_t)nf * 4, hipMemcpyHostToDevice, s));
+                launch_gather_rows(Q, cIdx.as<int>(), nf, dpad * esize, cQ.p, nfPad, s);
+                launch_gather_f32(qn, cIdx.as<int>(), nf, cQn.as<float>(), s);
+                launch_gather_f32(tauKk.as<float>(), cIdx.as<int>(), nf, cTk.as<float>(), s);
+                launch_gather_i32(tauKi.as<int>(), cIdx.as<int>(), nf, 1, cTi.as<int>(), s);
+                launch_gather_i32(probe.as<int>(), cIdx.as<int>(), nf, nprobe, cProbe.as<int>(), s);
+                launch_gather_i32(pos.as<int>(), cIdx.as<int>(), nf, nprobe, cPos.as<int>(), s);
+                wt.build(cProbe.as<int>(), nf, nprobe, nprobe, nlist, dCellOrder.as<int>(), s);
+                scanPass(kPassFull, nf, nprobe, nprobe, nprobe, cr, cQ.p, cQn.as<float>(), cTk.as<float>(),
+                         cTi.as<int>(), cPos.as<int>(), s);
+                SelectParams sp = selectParams(nf, nprobe, cr, k);
+                sp.qmap = cIdx.as<int>();
+                sp.out_ids = posIds; sp.out_vals = oVals;
+                launch_select(sp, s);
+                HIPC(hipStreamSynchronize(s));
+            }
+        }
+        if (oIds)
+            launch_ivf_finalize(oIds, mb, k, pos.as<int>(), probe.as<int>(), nprobe, dCellStart.as<int>(),
+                                dRid.as<int>(), s);
+    }
+
+    int searchDev(const float* dq, int m, int k, int nprobe, int32_t* ids, float* vals, hipStream_t s) {
+        if (!devOk) throw NotReady("no usable HIP device: IVF search needs a gfx950 GPU");
+        if (!built) throw NotReady("IVF index is not built");
+        if (m <= 0) return 0;
+        if (k < 1) k = 1;
+        if (k > kMaxK) {
+            if (!warnedK) {
+                MFLAT_LOG_WARN("k=%d clamped to MFLAT_MAX_K=%d", k, kMaxK);
+                warnedK = true;
+            }
+            k = kMaxK;
+        }
+        // reference src/IvfIndex.mm:766-767
+        if (nprobe < 1) nprobe = 1;
+        if (nprobe > nlist) nprobe = nlist;
+        if (nprobe > kMaxProbe) throw BadArg("IVF search: nprobe above 1024 is not supported");
+        if (!resident_scan_fits(dpad, storage))
+            throw BadArg("IVF search: the fine scan holds a 128-query tile in LDS (fp32 dim <= 128, fp16/bf16 dim <= 256)");
+        setDevice();
+        // batch the queries so the candidate regions stay bounded
+        const size_t perQuery = std::max<size_t>(nprobe > 1 ? (size_t)capA(k) : 0, (size_t)nprobe * capB(k, nprobe)) *
+                                sizeof(uint2);
+        int64_t mb = std::max<int64_t>(1, (int64_t)(kCandBudget / perQuery));
+        if (mb >= kBN) mb = mb / kBN * kBN;
+        mb = std::min<int64_t>(mb, m);
+        for (int64_t b0 = 0; b0 < m; b0 += mb) {
+            const int nb = (int)std::min<int64_t>(mb, m - b0);
+            const int64_t nPad = roundUp(nb, kBN);
+            const float* src = dq + b0 * dim;
+            qbuf.ensure((size_t)nPad * dpad * sizeof(float));
+            qnorm.ensure((size_t)nPad * sizeof(float));
+            probe.ensure((size_t)nb * nprobe * sizeof(int));
+            launch_pack_rows(src, nb, dim, qbuf.as<float>(), nPad, dpad, s);
+            const float* probeQ = src;
+            if (metric == Metric::Cosine) {
+                // normalised queries (reference src/IvfIndex.mm:773-780) for the
+                // probe (row-major, dim columns) and the fine scan
+                launch_normalize_rows(qbuf.as<float>(), nb, dpad, s);
+                qrm.ensure((size_t)nb * dim * sizeof(float));
+                launch_pack_rows(src, nb, dim, qrm.as<float>(), nb, dim, s);
+                launch_normalize_rows(qrm.as<float>(), nb, dim, s);
+                probeQ = qrm.as<float>();
+            }
+            coarse->searchDevice(probeQ, nb, nprobe, probe.as<int32_t>(), nullptr, s);
+            const void* qs = qbuf.p;
+            if (storage != kF32) {
+                qh.ensure((size_t)nPad * dpad * esize);
+                launch_round_rows(qbuf.as<float>(), nPad * dpad, storage, qh.p, s);
+                qs = qh.p;
+            }
+            if (metric == Metric::L2) launch_row_norms(qs, nb, dpad, storage, qnorm.as<float>(), s);
+            searchBatch(nb, k, nprobe, ids ? ids + b0 * k : nullptr, vals ? vals + b0 * k : nullptr, s);
+        }
+        HIPC(hipStreamSynchronize(s));
+        return k;
+    }
+};
+
+IvfIndex::IvfIndex(int dim, Metric metric, int nlist, Storage storage) : d_(new Impl) {
+    if (dim <= 0 || nlist <= 0) throw BadArg("IVF index: dim and nlist must be >= 1");
+    if (storage != kF32 && storage != kF16 && storage != kBF16) throw BadArg("unknown storage type");
+    d_->dim = dim;
+    d_->dpad = (int)roundUp(dim, kBK);
+    d_->metric = metric;
+    d_->storage = storage;
+    d_->esize = elem_bytes(storage);
+    d_->nlistReq = nlist;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        (void)hipGetLastError();
+        MFLAT_LOG_INFO("no HIP device - IVF index unavailable");
+        return;
+    }
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        MFLAT_LOG_ERROR("device %d is %s; this build targets gfx950 only", dev, prop.gcnArchName);
+        return;
+    }
+    if (hipStreamCreateWithFlags(&d_->stream, hipStreamNonBlocking) != hipSuccess) {
+        MFLAT_LOG_ERROR("hipStreamCreate failed");
+        return;
+    }
+    d_->device = dev;
+    d_->devOk = true;
+}
+
+IvfIndex::~IvfIndex() {
+    if (!d_) return;
+    if (d_->device >= 0) (void)hipSetDevice(d_->device);
+    if (d_->stream) (void)hipStreamSynchronize(d_->stream);
+    d_->coarse.reset();
+    d_->wt.release();
+    if (d_->stream) (void)hipStreamDestroy(d_->stream);
+}
+
+bool IvfIndex::ready() const { return d_->built; }
+bool IvfIndex::deviceOk() const { return d_->devOk; }
+int IvfIndex::size() const { return (int)d_->n; }
+int IvfIndex::dim() const { return d_->dim; }
+int IvfIndex::nlist() const { return d_->built ? d_->nlist : d_->nlistReq; }
+Metric IvfIndex::metric() const { return d_->metric; }
+Storage IvfIndex::storage() const { return static_cast<Storage>(d_->storage); }
+
+void IvfIndex::build(const float* rows, int n) { d_->buildFrom(rows, n, hipMemcpyHostToDevice, d_->stream); }
+
+void IvfIndex::buildDevice(const float* rows, int n, hipStream_t s) {
+    d_->buildFrom(rows, n, hipMemcpyDeviceToDevice, s ? s : d_->stream);
+}
+
+int IvfIndex::search(const float* q, int m, int k, int nprobe, int32_t* ids, float* dists) {
+    Impl& I = *d_;
+    if (!I.devOk) throw NotReady("no usable HIP device: IVF search needs a gfx950 GPU");
+    if (!I.built) throw NotReady("IVF index is not built");
+    if (m <= 0) return 0;
+    const int kk = std::min(std::max(k, 1), kMaxK);
+    I.setDevice();
+    hipStream_t s = I.stream;
+    I.qin.ensure((size_t)m * I.dim * sizeof(float));
+    I.outIds.ensure((size_t)m * kk * sizeof(int32_t));
+    I.outVals.ensure((size_t)m * kk * sizeof(float));
+    HIPC(hipMemcpyAsync(I.qin.p, q, (size_t)m * I.dim * sizeof(float), hipMemcpyHostToDevice, s));
+    const int used = I.searchDev(I.qin.as<float>(), m, k, nprobe, ids ? I.outIds.as<int32_t>() : nullptr,
+                                 dists ? I.outVals.as<float>() : nullptr, s);
+    if (ids) HIPC(hipMemcpyAsync(ids, I.outIds.p, (size_t)m * used * sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    if (dists) HIPC(hipMemcpyAsync(dists, I.outVals.p, (size_t)m * used * sizeof(float), hipMemcpyDeviceToHost, s));
+    HIPC(hipStreamSynchronize(s));
+    return used;
+}
+
+int IvfIndex::searchDevice(const float* q, int m, int k, int nprobe, int32_t* ids, float* dists, hipStream_t s) {
+    return d_->searchDev(q, m, k, nprobe, ids, dists, s ? s : d_->stream);
+}
+
+void IvfIndex::probe(const float* q, int m, int nprobe, int32_t* cells) {
+    Impl& I = *d_;
+    if (!I.devOk) throw NotReady("no usable HIP device: IVF probe needs a gfx950 GPU");
+    if (!I.built) throw NotReady("IVF index is not built");
+    if (m <= 0) return;
+    if (nprobe < 1) nprobe = 1;
+    if (nprobe > I.nlist) nprobe = I.nlist;
+    if (nprobe > kMaxProbe) throw BadArg("IVF probe: nprobe above 1024 is not supported");
+    I.setDevice();
+    hipStream_t s = I.stream;
+    I.qin.ensure((size_t)m * I.dim * sizeof(float));
+    I.probe.ensure((size_t)m * nprobe * sizeof(int));
+    HIPC(hipMemcpyAsync(I.qin.p, q, (size_t)m * I.dim * sizeof(float), hipMemcpyHostToDevice, s));
+    const float* pq = I.qin.as<float>();
+    if (I.metric == Metric::Cosine) {
+        I.qrm.ensure((size_t)m * I.dim * sizeof(float));
+        launch_pack_rows(pq, m, I.dim, I.qrm.as<float>(), m, I.dim, s);
+        launch_normalize_rows(I.qrm.as<float>(), m, I.dim, s);
+        pq = I.qrm.as<float>();
+    }
+    I.coarse->searchDevice(pq, m, nprobe, I.probe.as<int32_t>(), nullptr, s);
+    HIPC(hipMemcpyAsync(cells, I.probe.p, (size_t)m * nprobe * sizeof(int), hipMemcpyDeviceToHost, s));
+    HIPC(hipStreamSynchronize(s));
+}
+
+const std::vector<float>& IvfIndex::centroids() const { return d_->hCent; }
+const std::vector<int>& IvfIndex::cellStart() const { return d_->hStart; }
+const std::vector<int>& IvfIndex::reorderedIds() const { return d_->hRid; }
+
+}  // namespace mflat_amd

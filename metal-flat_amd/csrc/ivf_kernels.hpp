@@ -1,0 +1,62 @@
+// SPDX-License-Identifier: Apache-2.0
+// ivf_kernels.hpp -- device helpers of the IVF index: the cell-major layout
+// build and the per-search work tables of the fine scan (the scan itself is
+// launch_scan_ivf in kernels.hpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace mflat_amd {
+
+// v[r][c] *= inv[r] for r < n (row-major, dim columns)
+void launch_scale_rows(float* v, int64_t n, int dim, const float* inv, hipStream_t s);
+
+// dst row r = src row idx[r], or zeros where idx[r] < 0 (row-major fp32, r < n)
+void launch_gather_rows_or_zero(const float* src, const int* idx, int64_t n, int dim, float* dst, hipStream_t s);
+
+// dst row r = src row idx[r] for r < n (int32 rows of `width` elements)
+void launch_gather_i32(const int* src, const int* idx, int n, int width, int* dst, hipStream_t s);
+
+// Scan positions: pos[q * np + r] = sum of cellSize[probe[q * np + r']] over
+// r' < r -- where the probe-rank-r cell's first row falls in query q's scan
+// order (cells in probe order, rows in cell order), for q < m.
+void launch_ivf_positions(const int* probe, int m, int np, const int* cellSize, int* pos, hipStream_t s);
+
+// Work table of one fine-scan pass over the entries e = q * np + r of queries
+// q < m and ranks r < ranks (ranks = 1: the nearest cell only; ranks = np: all):
+//   ent        the entries sorted by (cell, e) -- a stable sort by cell
+//   work[w]    (cell, first entry, entries <= 128, 0): each cell's entries in
+//              runs of 128, cells in the order cellOrder gives (decreasing size)
+//   nwork      the number of work items (device int)
+// maxWork() bounds the work items (the grid of the scan launch). Keeps its
+// scratch between calls.
+struct IvfWorkTable {
+    int* ent = nullptr;
+    int4* work = nullptr;
+    int* nwork = nullptr;
+    int maxWork(int m, int ranks, int nlist) const;
+    void build(const int* probe, int m, int np, int ranks, int nlist, const int* cellOrder, hipStream_t s);
+    ~IvfWorkTable();
+    void release();
+
+private:
+    int* keysIn = nullptr;
+    int* keysOut = nullptr;
+    int* valsIn = nullptr;
+    int* counts = nullptr;
+    int* eStart = nullptr;
+    int* tiles = nullptr;
+    int* tEnd = nullptr;
+    void* temp = nullptr;
+    size_t tempBytes = 0;
+    int capE = 0, capWork = 0, capCells = 0;
+};
+
+// In place: ids[q * k + i] (a scan position, or -1) -> the original row id
+// rid[cellStart[probe[q * np + r]] + position - pos[q * np + r]] of the rank r
+// whose cell holds that position (q < m).
+void launch_ivf_finalize(int32_t* ids, int m, int k, const int* pos, const int* probe, int np,
+                         const int* cellStart, const int* rid, hipStream_t s);
+
+}  // namespace mflat_amd

@@ -314,13 +314,15 @@ __global__ void max_norm_kernel(const float* __restrict__ xn, int64_t n, unsigne
 //
 // One group of a lane's 32 x 32 accumulators: rows r0 .. r0 + 3 (register
 // g4*4 + i of each block, row norms xn4) against the lane's query slots b0 and
-// b0 + 1 (acc[b0 + b], per-query state tk/ti/qn/ft/qv). Eight fast tests
-// without branches, then one wave-level branch: a group rarely holds a
+// b0 + 1 (acc[b0 + b], per-query state tk/ti/qn/ft/qv). Rows at or above
+// rowLim are padding; row r reports id r * idStride + idb[slot]. Eight fast
+// tests without branches, then one wave-level branch: a group rarely holds a
 // survivor in any of the 64 lanes. Only survivors take the exact
 // lexicographic test; they go to emit(slot, key, id), or, for k = 1, replace
 // the slot's running best.
 template <int METRIC, int PASS, int NB, class Emit>
 __device__ __forceinline__ void filter_group(const fx16 (&acc)[NB], int g4, int b0, const fx4& xn4, int64_t r0,
+                                             int64_t rowLim, int idStride, const int (&idb)[NB],
                                              const ScanParams& p, float (&tk)[NB], int (&ti)[NB],
                                              const float (&qn)[NB], float (&ft)[NB], const bool (&qv)[NB],
                                              Emit&& emit) {
@@ -337,12 +339,13 @@ __device__ __forceinline__ void filter_group(const fx16 (&acc)[NB], int g4, int 
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int64_t row = r0 + i;
-        const bool rv = row < p.nrows;
-        const int id = (int)(row * p.id_stride);
+        const bool rv = row < rowLim;
+        const int idr = (int)(row * idStride);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             const int bn = b0 + b;
             if (!f[i][b]) continue;
+            const int id = idr + idb[bn];
             const float dot = acc[bn][g4 * 4 + i];
             float key;
             if (METRIC == 0) {
@@ -452,6 +455,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     float tk[2], qn[2], ft[2];
     int ti[2];
     bool qv[2];
+    const int idb[2] = {0, 0};   // ids are row * id_stride
 #pragma unroll
     for (int bn = 0; bn < 2; ++bn) {
         const int q = qb * kBN + wn * 64 + bn * 32 + r32;
@@ -609,7 +613,8 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
                     const int64_t r0 = tileRow0 + rl;
                     fx4 xn4 = {0.0f, 0.0f, 0.0f, 0.0f};
                     if (METRIC == 0) xn4 = xnr[bm][g4];
-                    filter_group<METRIC, PASS, 2>(acc[bm], g4, 0, xn4, r0, p, tk, ti, qn, ft, qv,
+                    filter_group<METRIC, PASS, 2>(acc[bm], g4, 0, xn4, r0, p.nrows, p.id_stride, idb, p, tk,
+                                                  ti, qn, ft, qv,
                                                   [&](int bn, float key, int id) {
                         const int ql = wn * 64 + bn * 32 + r32;
                         const int slot = atomicAdd(&sCnt[ql], 1);
@@ -681,7 +686,14 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
 // the workgroups of up to kQGroup query blocks resident on one XCD read the
 // same split at about the same time and share it through that XCD's L2 (a
 // non-temporal hint here cost 7% at d = 128 fp32 and 16% with fp16 storage).
-template <int S, int METRIC, int PASS, int G>
+// IVF: the fine scan of an inverted-file index. A workgroup owns one work item
+// (a cell and up to kBN of the (query, probe rank) entries that probe it): its
+// query tile is gathered from the entries' query rows, its rows are the cell's
+// (padded to kBM in the database), filter ids are cell-relative rows plus the
+// entry's scan position, and survivors go to the entry's region
+// (query * ivf_nreg + rank). Work items are in decreasing cell size, so the
+// largest run first.
+template <int S, int METRIC, int PASS, int G, bool IVF>
 __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     constexpr int ES = S == kF32 ? 4 : 2;
     constexpr int NK = S == kF32 ? 4 : 2;          // operand pieces per row block per chunk
@@ -701,18 +713,28 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     __shared__ int sRingId[RING ? 4 * kRing : 1];
     __shared__ int sRingQ[RING ? 4 * kRing : 1];
     __shared__ int sRingN[4];
+    __shared__ int sEnt[IVF ? kBN : 1];   // IVF: the tile's entries (-1: empty slot)
+    __shared__ int sQi[IVF ? kBN : 1];    // ... their queries
+    __shared__ int sReg[IVF ? kBN : 1];   // ... their candidate regions
 
-    // Workgroup -> (query block, split): the XCD grouping of scan_filter.
-    const int nwg = gridDim.x;
-    const int bid = blockIdx.x;
-    const int full = (nwg / 8) * 8;
-    const int v = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
-    const int grpSize = p.nqb < kQGroup ? p.nqb : kQGroup;
-    const int grp = v / (grpSize * p.nsplit);
-    const int r = v - grp * grpSize * p.nsplit;
-    const int inGrp = p.nqb - grp * grpSize < grpSize ? p.nqb - grp * grpSize : grpSize;
-    const int split = r / inGrp;
-    const int qb = grp * grpSize + (r - split * inGrp);
+    int qb = 0, split = 0;
+    int4 wk = make_int4(0, 0, 0, 0);   // IVF work item: (cell, first entry, entries, 0)
+    if constexpr (IVF) {
+        if ((int)blockIdx.x >= *p.ivf_nwork) return;
+        wk = p.ivf_work[blockIdx.x];
+    } else {
+        // Workgroup -> (query block, split): the XCD grouping of scan_filter.
+        const int nwg = gridDim.x;
+        const int bid = blockIdx.x;
+        const int full = (nwg / 8) * 8;
+        const int v = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
+        const int grpSize = p.nqb < kQGroup ? p.nqb : kQGroup;
+        const int grp = v / (grpSize * p.nsplit);
+        const int r = v - grp * grpSize * p.nsplit;
+        const int inGrp = p.nqb - grp * grpSize < grpSize ? p.nqb - grp * grpSize : grpSize;
+        split = r / inGrp;
+        qb = grp * grpSize + (r - split * inGrp);
+    }
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -721,13 +743,30 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     const int h = lane >> 5;
     const int ldqB = (p.dpad + 16 / ES) * ES;   // LDS query row stride (bytes): 16 B of padding
 
+    if constexpr (IVF) {
+        if (tid < kBN) {
+            const int e = tid < wk.z ? p.ivf_ent[wk.y + tid] : -1;
+            const int q = e >= 0 ? e / p.ivf_nprobe : -1;
+            sEnt[tid] = e;
+            sQi[tid] = q;
+            sReg[tid] = e >= 0 ? q * p.ivf_nreg + (e - q * p.ivf_nprobe) : -1;
+        }
+        __syncthreads();
+    }
     {
         const int rowP = p.dpad * ES / 16;
         const fx4* qg = (const fx4*)p.Q + (int64_t)qb * kBN * rowP;
         for (int i = tid; i < kBN * rowP; i += 256) {
             const int row = i / rowP;
             const int c = i - row * rowP;
-            *(fx4*)((char*)sQr + row * ldqB + c * 16) = qg[(int64_t)row * rowP + c];
+            fx4 v;
+            if constexpr (IVF) {
+                const int q = sQi[row];
+                v = q >= 0 ? ((const fx4*)p.Q)[(int64_t)q * rowP + c] : fx4{0.0f, 0.0f, 0.0f, 0.0f};
+            } else {
+                v = qg[(int64_t)row * rowP + c];
+            }
+            *(fx4*)((char*)sQr + row * ldqB + c * 16) = v;
         }
     }
     if (tid < kBN) {
@@ -740,10 +779,18 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     float tk[4], qn[4], ft[4];
     int ti[4];
     bool qv[4];
+    int idb[4] = {0, 0, 0, 0};   // IVF: scan position of the cell's first row, per slot
 #pragma unroll
     for (int bn = 0; bn < 4; ++bn) {
-        const int q = qb * kBN + bn * 32 + r32;
-        qv[bn] = q < p.nq;
+        int q;
+        if constexpr (IVF) {
+            q = sQi[bn * 32 + r32];
+            qv[bn] = q >= 0;
+            if (qv[bn]) idb[bn] = p.ivf_pos[sEnt[bn * 32 + r32]];
+        } else {
+            q = qb * kBN + bn * 32 + r32;
+            qv[bn] = q < p.nq;
+        }
         if (PASS == kPassArgmin) {
             tk[bn] = INFINITY;
             ti[bn] = -1;
@@ -761,11 +808,29 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     }
     __syncthreads();
 
-    const int64_t rows_pad = (p.nrows + kBM - 1) / kBM * kBM;
-    const int64_t rowBeg = (int64_t)split * p.rows_per_split;
-    int64_t rowEnd = rowBeg + p.rows_per_split;
-    if (rowEnd > rows_pad) rowEnd = rows_pad;
-    const int nsl = rowEnd > rowBeg ? (int)((rowEnd - rowBeg) / 64) : 0;
+    // Rows: [rowBeg, rowBeg + 64 nsl) of the database; filter rows count from
+    // rowOrg (IVF: the cell's first row), rows at or above rowLim are padding.
+    int64_t rowBeg, rowOrg, rowLim;
+    int nsl;
+    if constexpr (IVF) {
+        rowBeg = p.ivf_cell_pad[wk.x];
+        rowOrg = 0;
+        rowLim = p.ivf_cell_size[wk.x];
+        nsl = (int)((rowLim + 63) / 64);
+    } else {
+        const int64_t rows_pad = (p.nrows + kBM - 1) / kBM * kBM;
+        rowBeg = (int64_t)split * p.rows_per_split;
+        int64_t rowEnd = rowBeg + p.rows_per_split;
+        if (rowEnd > rows_pad) rowEnd = rows_pad;
+        nsl = rowEnd > rowBeg ? (int)((rowEnd - rowBeg) / 64) : 0;
+        rowOrg = rowBeg;
+        rowLim = p.nrows;
+    }
+    const int idStride = IVF ? 1 : p.id_stride;
+    auto region = [&](int ql) -> int64_t {
+        if constexpr (IVF) return sReg[ql];
+        return ((int64_t)qb * kBN + ql) * p.nsplit + split;
+    };
     const int nchunk = p.dpad / 32;
     const int64_t blkB = (int64_t)32 * p.dpad * ES;
     const char* xw = (const char*)p.X + rowBeg * p.dpad * ES +
@@ -821,12 +886,13 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
 #pragma unroll
             for (int g4 = 0; g4 < 4; ++g4) {
                 const int rl = bm * 32 + g4 * 8 + h * 4;
-                const int64_t r0 = rowBeg + (int64_t)sl * 64 + rl;
+                const int64_t r0 = rowOrg + (int64_t)sl * 64 + rl;
                 fx4 xn4 = {0.0f, 0.0f, 0.0f, 0.0f};
                 if (METRIC == 0) xn4 = *(const fx4*)(sXn + wave * 64 + rl);
 #pragma unroll
                 for (int bp = 0; bp < 2; ++bp)
-                    filter_group<METRIC, PASS, 4>(acc[bm], g4, 2 * bp, xn4, r0, p, tk, ti, qn, ft, qv,
+                    filter_group<METRIC, PASS, 4>(acc[bm], g4, 2 * bp, xn4, r0, rowLim, idStride, idb, p, tk,
+                                                  ti, qn, ft, qv,
                                                   [&](int bn, float key, int id) {
                         const int ql = bn * 32 + r32;
                         const int pos = RING ? atomicAdd(&sRingN[wave], 1) : kRing;
@@ -836,11 +902,8 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
                             sRingQ[wave * kRing + pos] = ql;
                         } else {   // ring full (or not used): store directly
                             const int slot = atomicAdd(&sCnt[ql], 1);
-                            if (slot < p.cap) {
-                                const int64_t q = (int64_t)qb * kBN + ql;
-                                p.cand[(q * p.nsplit + split) * p.cap + slot] =
-                                    make_uint2(__float_as_uint(key), (unsigned)id);
-                            }
+                            if (slot < p.cap)
+                                p.cand[region(ql) * p.cap + slot] = make_uint2(__float_as_uint(key), (unsigned)id);
                         }
                     });
             }
@@ -862,11 +925,9 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
             for (int e = lane; e < n; e += 64) {
                 const int ql = sRingQ[wave * kRing + e];
                 const int slot = atomicAdd(&sCnt[ql], 1);
-                if (slot < p.cap) {
-                    const int64_t q = (int64_t)qb * kBN + ql;
-                    p.cand[(q * p.nsplit + split) * p.cap + slot] =
+                if (slot < p.cap)
+                    p.cand[region(ql) * p.cap + slot] =
                         make_uint2(sRingKey[wave * kRing + e], (unsigned)sRingId[wave * kRing + e]);
-                }
             }
             __builtin_amdgcn_wave_barrier();
             if (lane == 0) sRingN[wave] = 0;
@@ -952,7 +1013,9 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
         return;
     }
     __syncthreads();
-    if (tid < kBN) {
+    if constexpr (IVF) {
+        if (tid < wk.z) p.cnt[sReg[tid]] = sCnt[tid];
+    } else if (tid < kBN) {
         const int q = qb * kBN + tid;
         if (q < p.nq) p.cnt[(int64_t)q * p.nsplit + split] = sCnt[tid];
     }
@@ -1702,11 +1765,11 @@ static void allow_resident_lds(const void* f) {
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kResidentMaxLds) != hipSuccess)
         throw std::runtime_error("scan_resident: cannot raise the dynamic LDS limit");
 }
-template <int S, int M, int P, int G>
+template <int S, int M, int P, int G, bool IVF = false>
 static void launch_resident_p(const ScanParams& p, int g, size_t lds, hipStream_t s) {
-    static const bool ok = (allow_resident_lds((const void*)scan_resident_kernel<S, M, P, G>), true);
+    static const bool ok = (allow_resident_lds((const void*)scan_resident_kernel<S, M, P, G, IVF>), true);
     (void)ok;
-    scan_resident_kernel<S, M, P, G><<<g, 256, lds, s>>>(p);
+    scan_resident_kernel<S, M, P, G, IVF><<<g, 256, lds, s>>>(p);
 }
 template <int S, int M, int G>
 static void launch_resident_g(const ScanParams& p, int pass, int g, size_t lds, hipStream_t s) {
@@ -1729,6 +1792,26 @@ template <int S>
 static void launch_resident_s(const ScanParams& p, int metric, int pass, int g, size_t lds, hipStream_t s) {
     if (metric == 0) launch_resident<S, 0>(p, pass, g, lds, s);
     else launch_resident<S, 1>(p, pass, g, lds, s);
+}
+// IVF fine scan: kPassSample (no bound, the bound pass) or kPassFull, with
+// the G variants of the flat scan (the same key function for a given dpad).
+template <int S, int M, int G>
+static void launch_ivf_g(const ScanParams& p, int pass, int g, size_t lds, hipStream_t s) {
+    if (pass == kPassSample) launch_resident_p<S, M, kPassSample, G, true>(p, g, lds, s);
+    else launch_resident_p<S, M, kPassFull, G, true>(p, g, lds, s);
+}
+template <int S, int M>
+static void launch_ivf(const ScanParams& p, int pass, int g, size_t lds, hipStream_t s) {
+    if constexpr (S != kF32) {
+        if (p.dpad == 96) return launch_ivf_g<S, M, 3>(p, pass, g, lds, s);
+        if (p.dpad == 128) return launch_ivf_g<S, M, 4>(p, pass, g, lds, s);
+    }
+    launch_ivf_g<S, M, 0>(p, pass, g, lds, s);
+}
+template <int S>
+static void launch_ivf_s(const ScanParams& p, int metric, int pass, int g, size_t lds, hipStream_t s) {
+    if (metric == 0) launch_ivf<S, 0>(p, pass, g, lds, s);
+    else launch_ivf<S, 1>(p, pass, g, lds, s);
 }
 
 static size_t resident_lds_bytes(int dpad, int storage) {
@@ -1804,6 +1887,23 @@ void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, 
     else launch_tiled_s<kBF16>(p, metric, pass, g, s);
     prof_end(tok, s);
     check_launch("scan_filter");
+}
+
+void launch_scan_ivf(const ScanParams& p, int metric, int pass, int storage, int grid, hipStream_t s) {
+    if (storage != kF32 && storage != kF16 && storage != kBF16) throw std::runtime_error("scan_ivf: unknown storage type");
+    if (grid <= 0) return;
+    if (pass != kPassSample && pass != kPassFull) throw std::runtime_error("scan_ivf: bad pass");
+    if (!resident_scan_fits(p.dpad, storage) || p.dpad % kBK != 0 || p.cap < 1 || p.ivf_nprobe < 1 ||
+        p.ivf_nreg < 1)
+        throw std::runtime_error("scan_ivf: bad parameters");
+    void* tok;
+    prof_begin(pass == kPassSample ? kFamScanSample : kFamScan, s, &tok);
+    const size_t lds = resident_lds_bytes(p.dpad, storage);
+    if (storage == kF32) launch_ivf_s<kF32>(p, metric, pass, grid, lds, s);
+    else if (storage == kF16) launch_ivf_s<kF16>(p, metric, pass, grid, lds, s);
+    else launch_ivf_s<kBF16>(p, metric, pass, grid, lds, s);
+    prof_end(tok, s);
+    check_launch("scan_ivf");
 }
 
 void launch_argmin_finalize(const unsigned long long* best, int nq, int metric, int32_t* ids, float* vals,

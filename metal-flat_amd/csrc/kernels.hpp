@@ -99,6 +99,15 @@ struct ScanParams {
     int* cnt;                // per (query, split) candidate counts (may exceed cap)
     int cap;                 // entries per (query, split) region
     unsigned long long* best;  // kPassArgmin: per-query packed best, pre-filled with all ones
+    // IVF fine scan (launch_scan_ivf): one workgroup per work item
+    const int4* ivf_work;      // (cell, first entry, entries <= kBN, 0); items >= *ivf_nwork are idle
+    const int* ivf_nwork;      // device: valid work items
+    const int* ivf_ent;        // entries grouped by cell: e = query * ivf_nprobe + probe rank
+    const int* ivf_pos;        // per entry: scan position of its cell's first row for its query
+    const int64_t* ivf_cell_pad;   // first database row of each cell (a multiple of kBM)
+    const int* ivf_cell_size;  // rows of each cell
+    int ivf_nprobe;
+    int ivf_nreg;              // candidate regions per query (1 or ivf_nprobe): query * nreg + rank
 };
 
 struct SelectParams {
@@ -167,6 +176,10 @@ bool small_scan_fits(int nq, int dpad, int storage);
 bool resident_scan_fits(int dpad, int storage);
 void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, hipStream_t s,
                         bool allowSmall = true);
+// IVF fine scan (scan_resident over the work items of ScanParams::ivf_*; the
+// query tile must fit, resident_scan_fits): pass kPassSample or kPassFull,
+// grid = an upper bound of the work items.
+void launch_scan_ivf(const ScanParams& p, int metric, int pass, int storage, int grid, hipStream_t s);
 void launch_select(const SelectParams& p, hipStream_t s);
 void launch_argmin_finalize(const unsigned long long* best, int nq, int metric, int32_t* ids, float* vals,
                             hipStream_t s);

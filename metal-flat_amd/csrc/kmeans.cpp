@@ -51,8 +51,8 @@ uint32_t bounded(std::mt19937& rng, uint32_t range) {   // uniform in [0, range)
 
 }  // namespace
 
-int kmeansTrain(const float* points, int n, int dim, int nlistReq, int iters, int maxPointsPerCentroid,
-                float* centroids, int32_t* assign, int32_t* cellStart, int32_t* order) {
+int kmeansTrainDevice(const float* dData, int n, int dim, int nlistReq, int iters, int maxPointsPerCentroid,
+                      float* dCentOut, int32_t* dAssignOut, int32_t* dOrderOut, int32_t* cellStart, hipStream_t s) {
     if (n < 1 || dim < 1 || nlistReq < 1 || iters < 0 || maxPointsPerCentroid < 0)
         throw BadArg("kmeans: n, dim, nlist must be >= 1 and iters, max_points_per_centroid >= 0");
     const int nlist = std::min(nlistReq, n);
@@ -68,29 +68,30 @@ int kmeansTrain(const float* points, int n, int dim, int nlistReq, int iters, in
     int trainN = n;
     if (maxPointsPerCentroid > 0 && (int64_t)maxPointsPerCentroid * nlist < n) trainN = maxPointsPerCentroid * nlist;
 
-    Stream st;
-    const hipStream_t s = st.s;
     const size_t rowB = (size_t)dim * sizeof(float);
-    DevMem dData((size_t)n * rowB), dCent((size_t)nlist * rowB), dPerm((size_t)n * sizeof(int));
-    HIPC(hipMemcpyAsync(dData.p, points, (size_t)n * rowB, hipMemcpyHostToDevice, s));
+    DevMem dPerm((size_t)n * sizeof(int));
     HIPC(hipMemcpyAsync(dPerm.p, perm.data(), (size_t)n * sizeof(int), hipMemcpyHostToDevice, s));
-    launch_gather_points(dData.as<float>(), dPerm.as<int>(), nlist, dim, dCent.as<float>(), s);
-    const float* dTrain = dData.as<float>();
+    float* dCent = dCentOut;
+    launch_gather_points(dData, dPerm.as<int>(), nlist, dim, dCent, s);
+    const float* dTrain = dData;
     DevMem dTrainBuf(trainN < n ? (size_t)trainN * rowB : 0);
     if (trainN < n) {
-        launch_gather_points(dData.as<float>(), dPerm.as<int>(), trainN, dim, dTrainBuf.as<float>(), s);
+        launch_gather_points(dData, dPerm.as<int>(), trainN, dim, dTrainBuf.as<float>(), s);
         dTrain = dTrainBuf.as<float>();
     }
 
-    DevMem dAssign((size_t)n * sizeof(int)), dOrder((size_t)n * sizeof(int)), dCounts((size_t)nlist * sizeof(int));
+    DevMem dAssignBuf(dAssignOut ? 0 : (size_t)n * sizeof(int)), dOrderBuf(dOrderOut ? 0 : (size_t)n * sizeof(int));
+    int* dAssign = dAssignOut ? dAssignOut : dAssignBuf.as<int>();
+    int* dOrder = dOrderOut ? dOrderOut : dOrderBuf.as<int>();
+    DevMem dCounts((size_t)nlist * sizeof(int));
     DevMem dStart((size_t)(nlist + 1) * sizeof(int)), dReseed((size_t)nlist * sizeof(int));
     CellGrouping grouping;
     std::vector<int> counts((size_t)nlist), start((size_t)nlist + 1), reseed((size_t)nlist);
     auto assignAll = [&](const float* pts, int m) {
         assigner.reset();
-        assigner.addDevice(dCent.as<float>(), nlist, s);
-        assigner.searchDevice(pts, m, 1, dAssign.as<int32_t>(), nullptr, s);
-        grouping.group(dAssign.as<int>(), m, nlist, dOrder.as<int>(), dCounts.as<int>(), s);
+        assigner.addDevice(dCent, nlist, s);
+        assigner.searchDevice(pts, m, 1, dAssign, nullptr, s);
+        grouping.group(dAssign, m, nlist, dOrder, dCounts.as<int>(), s);
         HIPC(hipMemcpyAsync(counts.data(), dCounts.p, (size_t)nlist * sizeof(int), hipMemcpyDeviceToHost, s));
         HIPC(hipStreamSynchronize(s));
         start[0] = 0;
@@ -105,17 +106,38 @@ int kmeansTrain(const float* points, int n, int dim, int nlistReq, int iters, in
             reseed[(size_t)c] = counts[(size_t)c] == 0 ? (int)(rng() % (uint32_t)trainN) : -1;
         HIPC(hipMemcpyAsync(dStart.p, start.data(), start.size() * sizeof(int), hipMemcpyHostToDevice, s));
         HIPC(hipMemcpyAsync(dReseed.p, reseed.data(), reseed.size() * sizeof(int), hipMemcpyHostToDevice, s));
-        launch_update_centroids(dTrain, dim, dOrder.as<int>(), dStart.as<int>(), dReseed.as<int>(), nlist,
-                                dCent.as<float>(), s);
+        launch_update_centroids(dTrain, dim, dOrder, dStart.as<int>(), dReseed.as<int>(), nlist, dCent, s);
     }
     // final assignment of every point (reference src/Internal.h:357-359) and its CSR
     // (src/CoarseQuantizer.mm:135-145)
-    assignAll(dData.as<float>(), n);
+    assignAll(dData, n);
+    HIPC(hipStreamSynchronize(s));
+    if (cellStart) std::copy(start.begin(), start.end(), cellStart);
+    return nlist;
+}
+
+int kmeansTrain(const float* points, int n, int dim, int nlistReq, int iters, int maxPointsPerCentroid,
+                float* centroids, int32_t* assign, int32_t* cellStart, int32_t* order) {
+    if (n < 1 || dim < 1 || nlistReq < 1 || iters < 0 || maxPointsPerCentroid < 0)
+        throw BadArg("kmeans: n, dim, nlist must be >= 1 and iters, max_points_per_centroid >= 0");
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        (void)hipGetLastError();
+        throw NotReady("no usable HIP device: k-means needs a gfx950 GPU");
+    }
+    const int nlist = std::min(nlistReq, n);
+    Stream st;
+    const hipStream_t s = st.s;
+    const size_t rowB = (size_t)dim * sizeof(float);
+    DevMem dData((size_t)n * rowB), dCent((size_t)nlist * rowB);
+    DevMem dAssign(assign ? (size_t)n * sizeof(int) : 0), dOrder(order ? (size_t)n * sizeof(int) : 0);
+    HIPC(hipMemcpyAsync(dData.p, points, (size_t)n * rowB, hipMemcpyHostToDevice, s));
+    kmeansTrainDevice(dData.as<float>(), n, dim, nlistReq, iters, maxPointsPerCentroid, dCent.as<float>(),
+                      assign ? dAssign.as<int32_t>() : nullptr, order ? dOrder.as<int32_t>() : nullptr, cellStart, s);
     HIPC(hipMemcpyAsync(centroids, dCent.p, (size_t)nlist * rowB, hipMemcpyDeviceToHost, s));
     if (assign) HIPC(hipMemcpyAsync(assign, dAssign.p, (size_t)n * sizeof(int), hipMemcpyDeviceToHost, s));
     if (order) HIPC(hipMemcpyAsync(order, dOrder.p, (size_t)n * sizeof(int), hipMemcpyDeviceToHost, s));
     HIPC(hipStreamSynchronize(s));
-    if (cellStart) std::copy(start.begin(), start.end(), cellStart);
     return nlist;
 }
 

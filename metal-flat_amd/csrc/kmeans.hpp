@@ -2,6 +2,8 @@
 // kmeans.hpp -- k-means training of an IVF coarse quantizer on one MI355X.
 #pragma once
 
+#include <hip/hip_runtime.h>
+
 #include <cstdint>
 
 namespace mflat_amd {
@@ -30,5 +32,12 @@ namespace mflat_amd {
 // usable device, BadArg for bad sizes.
 int kmeansTrain(const float* points, int n, int dim, int nlistReq, int iters, int maxPointsPerCentroid,
                 float* centroids, int32_t* assign, int32_t* cellStart, int32_t* order);
+
+// The same on device memory, asynchronous on s except for the per-iteration
+// cell counts: points n x dim, centroids nlist x dim, assign / order n
+// (nullable) are device pointers, cellStart (nlist + 1, nullable) is host
+// memory. Returns nlist.
+int kmeansTrainDevice(const float* points, int n, int dim, int nlistReq, int iters, int maxPointsPerCentroid,
+                      float* centroids, int32_t* assign, int32_t* order, int32_t* cellStart, hipStream_t s);
 
 }  // namespace mflat_amd

@@ -14,6 +14,7 @@
 
 #include "../../include/mflat.h"
 #include "flat_index.hpp"
+#include "ivf_index.hpp"
 #include "kmeans.hpp"
 #include "log.hpp"
 
@@ -72,6 +73,12 @@ struct mflat_flat_index {
     FlatIndex idx;
     std::mutex mu;
     mflat_flat_index(int d, Metric m, mflat_amd::Storage st) : idx(d, m, st) {}
+};
+
+struct mflat_ivf_index {
+    mflat_amd::IvfIndex idx;
+    std::mutex mu;
+    mflat_ivf_index(int d, Metric m, int nl, mflat_amd::Storage st) : idx(d, m, nl, st) {}
 };
 
 extern "C" {
@@ -229,6 +236,110 @@ MFLAT_API mflat_status_t mflat_kmeans_train(const float* pts, int n, int dim, in
     return guarded([&] {
         const int used = mflat_amd::kmeansTrain(pts, n, dim, nlist, iters, mpc, oc, oa, ocs, oo);
         if (onl) *onl = used;
+        return MFLAT_OK;
+    });
+}
+
+MFLAT_API mflat_ivf_index_t* mflat_ivf_create_ex(int dim, mflat_metric_t metric, int nlist, mflat_storage_t storage,
+                                                 mflat_status_t* st) {
+    if (dim <= 0 || nlist <= 0 || (storage != MFLAT_STORAGE_F32 && storage != MFLAT_STORAGE_F16 &&
+                                   storage != MFLAT_STORAGE_BF16)) {
+        if (st) *st = MFLAT_ERR_BAD_ARG;
+        return nullptr;
+    }
+    try {
+        auto* h = new mflat_ivf_index(dim, conv(metric), nlist, static_cast<mflat_amd::Storage>(storage));
+        if (st) *st = MFLAT_OK;
+        return h;
+    } catch (const std::bad_alloc&) {
+        if (st) *st = MFLAT_ERR_ALLOC;
+        return nullptr;
+    } catch (...) {
+        if (st) *st = MFLAT_ERR_INTERNAL;
+        return nullptr;
+    }
+}
+
+MFLAT_API mflat_ivf_index_t* mflat_ivf_create(int dim, mflat_metric_t metric, int nlist, mflat_status_t* st) {
+    return mflat_ivf_create_ex(dim, metric, nlist, MFLAT_STORAGE_F32, st);
+}
+
+MFLAT_API void mflat_ivf_free(mflat_ivf_index_t* h) { delete h; }
+MFLAT_API int mflat_ivf_ready(const mflat_ivf_index_t* h) { return (h && h->idx.ready()) ? 1 : 0; }
+MFLAT_API int mflat_ivf_size(const mflat_ivf_index_t* h) { return h ? h->idx.size() : 0; }
+MFLAT_API int mflat_ivf_dim(const mflat_ivf_index_t* h) { return h ? h->idx.dim() : 0; }
+MFLAT_API int mflat_ivf_nlist(const mflat_ivf_index_t* h) { return h ? h->idx.nlist() : 0; }
+MFLAT_API mflat_storage_t mflat_ivf_storage(const mflat_ivf_index_t* h) {
+    return h ? static_cast<mflat_storage_t>(h->idx.storage()) : MFLAT_STORAGE_F32;
+}
+
+MFLAT_API mflat_status_t mflat_ivf_build(mflat_ivf_index_t* h, const float* v, int n) {
+    if (!h || !v) return MFLAT_ERR_NULL_ARG;
+    if (n <= 0) return MFLAT_ERR_BAD_ARG;
+    return guarded([&] {
+        std::lock_guard<std::mutex> lk(h->mu);
+        h->idx.build(v, n);
+        return MFLAT_OK;
+    });
+}
+
+MFLAT_API mflat_status_t mflat_ivf_search(mflat_ivf_index_t* h, const float* q, int m, int k, int nprobe,
+                                          int32_t* oi, float* od, int* ok) {
+    if (!h || !q) return MFLAT_ERR_NULL_ARG;
+    if (m < 0 || k < 1 || nprobe < 1) return MFLAT_ERR_BAD_ARG;
+    if (!h->idx.ready()) return MFLAT_ERR_NOT_READY;
+    if (m == 0) {
+        if (ok) *ok = 0;
+        return MFLAT_OK;
+    }
+    return guarded([&] {
+        std::lock_guard<std::mutex> lk(h->mu);
+        const int used = h->idx.search(q, m, k, nprobe, oi, od);
+        if (ok) *ok = used;
+        return MFLAT_OK;
+    });
+}
+
+MFLAT_API mflat_status_t mflat_ivf_search_device(mflat_ivf_index_t* h, const float* q, int m, int k, int nprobe,
+                                                 int32_t* oi, float* od, int* ok, void* stream) {
+    if (!h || !q) return MFLAT_ERR_NULL_ARG;
+    if (m < 0 || k < 1 || nprobe < 1) return MFLAT_ERR_BAD_ARG;
+    if (!h->idx.ready()) return MFLAT_ERR_NOT_READY;
+    if (m == 0) {
+        if (ok) *ok = 0;
+        return MFLAT_OK;
+    }
+    return guarded([&] {
+        std::lock_guard<std::mutex> lk(h->mu);
+        const int used = h->idx.searchDevice(q, m, k, nprobe, oi, od, static_cast<hipStream_t>(stream));
+        if (ok) *ok = used;
+        return MFLAT_OK;
+    });
+}
+
+MFLAT_API mflat_status_t mflat_ivf_probe(mflat_ivf_index_t* h, const float* q, int m, int nprobe, int32_t* cells) {
+    if (!h || !q || !cells) return MFLAT_ERR_NULL_ARG;
+    if (m < 0 || nprobe < 1) return MFLAT_ERR_BAD_ARG;
+    if (!h->idx.ready()) return MFLAT_ERR_NOT_READY;
+    return guarded([&] {
+        std::lock_guard<std::mutex> lk(h->mu);
+        h->idx.probe(q, m, nprobe, cells);
+        return MFLAT_OK;
+    });
+}
+
+MFLAT_API mflat_status_t mflat_ivf_coarse(const mflat_ivf_index_t* h, float* oc, int32_t* ocs, int32_t* orid) {
+    if (!h) return MFLAT_ERR_NULL_ARG;
+    if (!h->idx.ready()) return MFLAT_ERR_NOT_READY;
+    auto* hh = const_cast<mflat_ivf_index_t*>(h);
+    return guarded([&] {
+        std::lock_guard<std::mutex> lk(hh->mu);
+        const auto& c = h->idx.centroids();
+        const auto& cs = h->idx.cellStart();
+        const auto& r = h->idx.reorderedIds();
+        if (oc) std::memcpy(oc, c.data(), c.size() * sizeof(float));
+        if (ocs) std::memcpy(ocs, cs.data(), cs.size() * sizeof(int32_t));
+        if (orid) std::memcpy(orid, r.data(), r.size() * sizeof(int32_t));
         return MFLAT_OK;
     });
 }

@@ -61,6 +61,20 @@ SIGNATURES = {
     "mflat_flat_add_device": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
     "mflat_kmeans_train": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
                                    c_void_p, c_void_p, POINTER(c_int)]),
+    "mflat_ivf_create": (c_void_p, [c_int, c_int, c_int, POINTER(c_int)]),
+    "mflat_ivf_create_ex": (c_void_p, [c_int, c_int, c_int, c_int, POINTER(c_int)]),
+    "mflat_ivf_free": (None, [c_void_p]),
+    "mflat_ivf_ready": (c_int, [c_void_p]),
+    "mflat_ivf_size": (c_int, [c_void_p]),
+    "mflat_ivf_dim": (c_int, [c_void_p]),
+    "mflat_ivf_nlist": (c_int, [c_void_p]),
+    "mflat_ivf_storage": (c_int, [c_void_p]),
+    "mflat_ivf_build": (c_int, [c_void_p, c_void_p, c_int]),
+    "mflat_ivf_search": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, POINTER(c_int)]),
+    "mflat_ivf_search_device": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p,
+                                        POINTER(c_int), c_void_p]),
+    "mflat_ivf_probe": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "mflat_ivf_coarse": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p]),
     "mflat_profile_enable": (None, [c_int]),
     "mflat_profile_reset": (None, []),
     "mflat_profile_read": (c_int, [c_char_p, POINTER(c_double), POINTER(c_longlong)]),
@@ -199,6 +213,101 @@ class FlatIndex:
             out_dist.data_ptr() if out_dist is not None else None,
             ctypes.byref(used), _stream_ptr(stream)), "mflat_flat_search_device")
         return used.value
+
+
+class IvfIndex:
+    """Python view of one mflat_ivf_index_t (reference IvfIndex.h:29-62)."""
+
+    def __init__(self, dim: int, metric: int = MFLAT_METRIC_L2, nlist: int = 64,
+                 storage: int = MFLAT_STORAGE_F32):
+        lib = load()
+        st = c_int(-1)
+        if storage == MFLAT_STORAGE_F32:
+            self._h = lib.mflat_ivf_create(int(dim), int(metric), int(nlist), ctypes.byref(st))
+        else:
+            self._h = lib.mflat_ivf_create_ex(int(dim), int(metric), int(nlist), int(storage), ctypes.byref(st))
+        if not self._h:
+            raise MflatError(st.value, "mflat_ivf_create")
+        self.dim = int(dim)
+        self.metric = int(metric)
+        self.storage = int(storage)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            load().mflat_ivf_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def handle(self):
+        return self._h
+
+    def ready(self) -> bool:
+        return load().mflat_ivf_ready(self._h) == 1
+
+    def size(self) -> int:
+        return load().mflat_ivf_size(self._h)
+
+    def nlist(self) -> int:
+        return load().mflat_ivf_nlist(self._h)
+
+    def build(self, vectors) -> None:
+        v = _f32(vectors).reshape(-1, self.dim)
+        _check(load().mflat_ivf_build(self._h, v.ctypes.data, v.shape[0]), "mflat_ivf_build")
+
+    def search(self, queries, k: int, nprobe: int):
+        """Returns (ids int32 [m, k_used], distances float32 [m, k_used], k_used)."""
+        q = _f32(queries).reshape(-1, self.dim)
+        m = q.shape[0]
+        kk = max(1, min(int(k), load().mflat_max_k()))
+        ids = np.full((max(m, 1), kk), -7, dtype=np.int32)
+        dist = np.full((max(m, 1), kk), np.nan, dtype=np.float32)
+        used = c_int(-1)
+        _check(load().mflat_ivf_search(self._h, q.ctypes.data, m, int(k), int(nprobe), ids.ctypes.data,
+                                        dist.ctypes.data, ctypes.byref(used)), "mflat_ivf_search")
+        ku = used.value
+        return (ids.reshape(-1)[: m * ku].reshape(m, ku).copy(),
+                dist.reshape(-1)[: m * ku].reshape(m, ku).copy(), ku)
+
+    def search_device(self, q, k: int, nprobe: int, out_ids, out_dist, stream=None) -> int:
+        used = c_int(-1)
+        _check(load().mflat_ivf_search_device(
+            self._h, q.data_ptr(), q.shape[0], int(k), int(nprobe),
+            out_ids.data_ptr() if out_ids is not None else None,
+            out_dist.data_ptr() if out_dist is not None else None,
+            ctypes.byref(used), _stream_ptr(stream)), "mflat_ivf_search_device")
+        return used.value
+
+    def probe(self, queries, nprobe: int) -> np.ndarray:
+        """The m x nprobe nearest cells (nprobe clamped to [1, nlist]), nearest first."""
+        q = _f32(queries).reshape(-1, self.dim)
+        m = q.shape[0]
+        npb = max(1, min(int(nprobe), self.nlist()))
+        cells = np.full((max(m, 1), npb), -7, dtype=np.int32)
+        _check(load().mflat_ivf_probe(self._h, q.ctypes.data, m, int(nprobe), cells.ctypes.data), "mflat_ivf_probe")
+        return cells[:m].copy()
+
+    def coarse(self):
+        """(centroids [nlist, dim] float32, cell_start [nlist + 1] int32,
+        reordered_ids [size] int32) of a built index."""
+        nl, n = self.nlist(), self.size()
+        cent = np.empty((nl, self.dim), np.float32)
+        start = np.empty(nl + 1, np.int32)
+        rid = np.empty(max(n, 1), np.int32)
+        _check(load().mflat_ivf_coarse(self._h, cent.ctypes.data, start.ctypes.data, rid.ctypes.data),
+               "mflat_ivf_coarse")
+        return cent, start, rid[:n]
 
 
 def kmeans_train(points, nlist: int, iters: int, max_points_per_centroid: int = 256):

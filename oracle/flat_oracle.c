@@ -26,6 +26,11 @@
  *                        double sums over the points in ascending index order,
  *                        centroid = float(sum / count); an empty cell copies
  *                        the row its reseed entry names
+ *   orc_ivf_search       src/IvfIndex.mm:518-560 (searchCpu, with the caller's
+ *                        probed cells as its probedRows): per query, a running
+ *                        top-k over the rows of its cells in probe order (rows
+ *                        lo..hi of the cell-ordered payload), strict '>'
+ *                        insertion, ids through reorderedIds, cells < 0 skipped
  *
  * Build with -ffp-contract=off so no multiply-add is fused: the sums are the
  * plain sequential fp32 sums the reference's C++ source spells out.
@@ -247,4 +252,81 @@ void orc_kmeans_update(const float* pts, int64_t n, int dim, const int32_t* assi
     }
     free(sums);
     free(counts);
+}
+
+/* IVF fine scan (searchCpu): rdb = the rows in cell order (row j of cell c is
+   payload row cellStart[c] + j, i.e. reorderedDb), rid = reorderedIds, probed =
+   m x nprobe cells nearest first. metric 0 L2, otherwise dot (Cosine callers
+   pass normalised rows and queries). threads as orc_cpu_search. */
+typedef struct {
+    const float* rdb; const int32_t* rid; const int32_t* cs; int dim; int metric;
+    const float* q; const int32_t* probed; int nprobe; int k;
+    int32_t* ids; float* vals; int64_t lo, hi; int status;
+} orc_ivf_job_t;
+
+static void* orc_ivf_worker(void* arg) {
+    orc_ivf_job_t* j = (orc_ivf_job_t*)arg;
+    float* bs = (float*)malloc(sizeof(float) * (size_t)j->k);
+    int32_t* bi = (int32_t*)malloc(sizeof(int32_t) * (size_t)j->k);
+    if (!bs || !bi) { free(bs); free(bi); j->status = -1; return NULL; }
+    for (int64_t qi = j->lo; qi < j->hi; ++qi) {
+        const float* q = j->q + qi * j->dim;
+        for (int i = 0; i < j->k; ++i) { bs[i] = -INFINITY; bi[i] = -1; }
+        for (int pp = 0; pp < j->nprobe; ++pp) {
+            const int32_t c = j->probed[qi * j->nprobe + pp];
+            if (c < 0) continue;
+            for (int64_t r = j->cs[c]; r < j->cs[c + 1]; ++r) {
+                const float s = orc_score(j->metric, q, j->rdb + r * j->dim, j->dim);
+                if (s > bs[0]) {
+                    int pos = 0;
+                    while (pos + 1 < j->k && s > bs[pos + 1]) {
+                        bs[pos] = bs[pos + 1];
+                        bi[pos] = bi[pos + 1];
+                        ++pos;
+                    }
+                    bs[pos] = s;
+                    bi[pos] = j->rid[r];
+                }
+            }
+        }
+        for (int i = 0; i < j->k; ++i) {
+            const int src = j->k - 1 - i;
+            j->ids[qi * j->k + i] = bi[src];
+            j->vals[qi * j->k + i] = orc_score_to_value(j->metric, bs[src]);
+        }
+    }
+    free(bs); free(bi);
+    j->status = 0;
+    return NULL;
+}
+
+int orc_ivf_search(const float* rdb, const int32_t* rid, const int32_t* cell_start, int dim, int metric,
+                   const float* q, int64_t m, const int32_t* probed, int nprobe, int k,
+                   int32_t* out_ids, float* out_vals, int threads) {
+    if (k < 1 || m < 0 || dim <= 0 || nprobe < 1) return -2;
+    const int sm = (metric == ORC_L2) ? ORC_L2 : ORC_IP;
+    if (threads <= 1 || m < 2) {
+        orc_ivf_job_t j = {rdb, rid, cell_start, dim, sm, q, probed, nprobe, k, out_ids, out_vals, 0, m, 0};
+        orc_ivf_worker(&j);
+        return j.status;
+    }
+    if (threads > 256) threads = 256;
+    pthread_t tid[256];
+    orc_ivf_job_t jobs[256];
+    const int64_t chunk = (m + threads - 1) / threads;
+    int started = 0, rc = 0;
+    for (int t = 0; t < threads; ++t) {
+        const int64_t lo = (int64_t)t * chunk;
+        const int64_t hi = lo + chunk < m ? lo + chunk : m;
+        if (lo >= hi) break;
+        orc_ivf_job_t jj = {rdb, rid, cell_start, dim, sm, q, probed, nprobe, k, out_ids, out_vals, lo, hi, 0};
+        jobs[t] = jj;
+        if (pthread_create(&tid[t], NULL, orc_ivf_worker, &jobs[t]) != 0) { rc = -1; break; }
+        ++started;
+    }
+    for (int t = 0; t < started; ++t) {
+        pthread_join(tid[t], NULL);
+        if (jobs[t].status != 0) rc = -1;
+    }
+    return rc;
 }

@@ -44,6 +44,9 @@ def lib():
         o.orc_argmin_l2.argtypes = [c_void_p, c_int64, c_void_p, c_int64, c_int, c_void_p, c_void_p]
         o.orc_kmeans_update.restype = None
         o.orc_kmeans_update.argtypes = [c_void_p, c_int64, c_int, c_void_p, c_int, c_void_p, c_void_p]
+        o.orc_ivf_search.restype = c_int
+        o.orc_ivf_search.argtypes = [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int64, c_void_p,
+                                     c_int, c_int, c_void_p, c_void_p, c_int]
         o.orc_brute_lex.restype = c_int
         o.orc_brute_lex.argtypes = [c_void_p, c_int64, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p]
         _o = o
@@ -250,3 +253,73 @@ def kmeans_train(points, nlist, iters, max_points_per_centroid=256):
     start = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
     order = np.argsort(a, kind="stable").astype(np.int32)
     return cent, a.astype(np.int32), start, order
+
+
+# ---- IVF (the inverted-file index's checker) ----------------------------------
+# Restates the reference's IvfIndex build and two-stage search: the coarse layer
+# of CoarseQuantizer::train (src/CoarseQuantizer.mm:104-159), its CSR
+# (:134-143), the CPU probe (probeCellsCpu, :190-197) and searchCpu
+# (src/IvfIndex.mm:518-560) over the probed cells.
+
+IVF_TRAIN_ITERS = 12            # src/IvfIndex.mm:493
+IVF_POINTS_PER_CENTROID = 256   # src/CoarseQuantizer.mm:116-117
+
+
+def ivf_csr(assign, nlist):
+    """Cell histogram -> prefix sum -> stable slot permutation
+    (src/CoarseQuantizer.mm:134-143): (cell_start [nlist + 1], reordered_ids [n])."""
+    assign = np.asarray(assign, np.int64)
+    start = np.zeros(nlist + 1, np.int64)
+    for a in assign:
+        start[a + 1] += 1
+    start = np.cumsum(start)
+    cursor = start[:-1].copy()
+    rid = np.empty(assign.size, np.int32)
+    for i, a in enumerate(assign):
+        rid[cursor[a]] = i
+        cursor[a] += 1
+    return start.astype(np.int32), rid
+
+
+def ivf_build(db, nlist, metric=0):
+    """(centroids, cell_start, reordered_ids) of IvfIndex::build on the
+    library's k-means (kmeans_train above): Cosine rows are normalised first."""
+    db = normalize_rows(db) if metric == 2 else _f32(db)
+    cent, assign, _, _ = kmeans_train(db, nlist, IVF_TRAIN_ITERS, IVF_POINTS_PER_CENTROID)
+    start, rid = ivf_csr(assign, cent.shape[0])
+    return cent, start, rid
+
+
+def ivf_probe(cent, q, nprobe, metric=0):
+    """probeCellsCpu: the nprobe cells of smallest (sqL2(q, centroid), cell),
+    nearest first (src/CoarseQuantizer.mm:190-197) -- cpuSearch over the
+    centroids under L2 keeps the same order (strict '>' keeps the lower cell on
+    ties). Cosine queries are normalised first (src/IvfIndex.mm:773-780)."""
+    q = normalize_rows(q) if metric == 2 else _f32(q)
+    nprobe = max(1, min(int(nprobe), cent.shape[0]))
+    ids, _ = flat_search(cent, q, nprobe, 0)
+    return ids
+
+
+def ivf_search(db, cell_start, rid, q, k, probed, metric=0, threads=1):
+    """searchCpu over the given probed cells: (ids [m, k], values [m, k]).
+    db: the caller's rows (row-major, original order); Cosine rows and
+    queries are normalised and ranked by the dot product."""
+    db = _f32(db)
+    q = _f32(q)
+    if metric == 2:
+        db = normalize_rows(db)
+        q = normalize_rows(q)
+        metric = 1
+    rid = np.ascontiguousarray(rid, np.int32)
+    rdb = np.ascontiguousarray(db[rid]) if db.size else db
+    start = np.ascontiguousarray(cell_start, np.int32)
+    probed = np.ascontiguousarray(probed, np.int32)
+    m, d = q.shape
+    ids = np.empty((m, k), np.int32)
+    vals = np.empty((m, k), np.float32)
+    rc = lib().orc_ivf_search(rdb.ctypes.data, rid.ctypes.data, start.ctypes.data, d, metric, q.ctypes.data, m,
+                              probed.ctypes.data, probed.shape[1], k, ids.ctypes.data, vals.ctypes.data, threads)
+    if rc != 0:
+        raise RuntimeError(f"orc_ivf_search rc={rc}")
+    return ids, vals

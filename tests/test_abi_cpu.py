@@ -176,3 +176,45 @@ def test_kmeans_arguments():
     if not idx.ready():
         assert rc == mflat.MFLAT_ERR_NOT_READY
     idx.close()
+
+
+def test_ivf_arguments():
+    """reference c/mflat.cpp:131-159: create / build / search checks, in that order."""
+    lib = mflat.load()
+    st = ctypes.c_int(-1)
+    assert not lib.mflat_ivf_create(0, 0, 4, ctypes.byref(st)) and st.value == mflat.MFLAT_ERR_BAD_ARG
+    assert not lib.mflat_ivf_create(8, 0, 0, ctypes.byref(st)) and st.value == mflat.MFLAT_ERR_BAD_ARG
+    assert not lib.mflat_ivf_create_ex(8, 0, 4, 9, ctypes.byref(st)) and st.value == mflat.MFLAT_ERR_BAD_ARG
+    lib.mflat_ivf_free(None)
+    for f in (lib.mflat_ivf_ready, lib.mflat_ivf_size, lib.mflat_ivf_dim, lib.mflat_ivf_nlist):
+        assert f(None) == 0
+    h = lib.mflat_ivf_create(8, 42, 5, ctypes.byref(st))   # unknown metric maps to L2
+    assert h and st.value == mflat.MFLAT_OK
+    assert lib.mflat_ivf_ready(h) == 0 and lib.mflat_ivf_size(h) == 0
+    assert lib.mflat_ivf_dim(h) == 8 and lib.mflat_ivf_nlist(h) == 5
+    assert lib.mflat_ivf_storage(h) == mflat.MFLAT_STORAGE_F32
+    x = np.zeros((3, 8), np.float32)
+    used = ctypes.c_int(-1)
+    assert lib.mflat_ivf_build(None, x.ctypes.data, 3) == mflat.MFLAT_ERR_NULL_ARG
+    assert lib.mflat_ivf_build(h, None, 3) == mflat.MFLAT_ERR_NULL_ARG
+    assert lib.mflat_ivf_build(h, x.ctypes.data, 0) == mflat.MFLAT_ERR_BAD_ARG
+    s = lib.mflat_ivf_search
+    assert s(None, x.ctypes.data, 1, 1, 1, None, None, None) == mflat.MFLAT_ERR_NULL_ARG
+    assert s(h, None, 1, 1, 1, None, None, None) == mflat.MFLAT_ERR_NULL_ARG
+    for m, k, npb in ((-1, 1, 1), (1, 0, 1), (1, 1, 0)):
+        assert s(h, x.ctypes.data, m, k, npb, None, None, None) == mflat.MFLAT_ERR_BAD_ARG
+    # not built: NOT_READY (even for m == 0, as the reference checks ready first)
+    assert s(h, x.ctypes.data, 0, 1, 1, None, None, ctypes.byref(used)) == mflat.MFLAT_ERR_NOT_READY
+    assert lib.mflat_ivf_probe(h, x.ctypes.data, 1, 1, x.ctypes.data) == mflat.MFLAT_ERR_NOT_READY
+    assert lib.mflat_ivf_coarse(h, None, None, None) == mflat.MFLAT_ERR_NOT_READY
+    assert lib.mflat_ivf_coarse(None, None, None, None) == mflat.MFLAT_ERR_NULL_ARG
+    probe = mflat.FlatIndex(4)
+    if not probe.ready():
+        # no device: build fails loudly, nothing falls back to the CPU
+        assert lib.mflat_ivf_build(h, x.ctypes.data, 3) == mflat.MFLAT_ERR_NOT_READY
+        assert lib.mflat_ivf_ready(h) == 0
+    probe.close()
+    lib.mflat_ivf_free(h)
+    hx = lib.mflat_ivf_create_ex(8, 1, 3, mflat.MFLAT_STORAGE_BF16, ctypes.byref(st))
+    assert hx and lib.mflat_ivf_storage(hx) == mflat.MFLAT_STORAGE_BF16
+    lib.mflat_ivf_free(hx)
