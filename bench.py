@@ -156,6 +156,119 @@ def kmeans_bench(iters):
                       "total_s": {"iters_0": round(t[0], 3), f"iters_{iters}": round(t[1], 3)}}), flush=True)
 
 
+def ivf_bench(args):
+    """IVF search (mflat_ivf_*) on C2's database and queries: nlist and nprobe by
+    the reference bench's rule (bench/bench.mm:96-101: nlist = max(64, sqrt(N)),
+    nprobe = max(1, nlist / 16)) unless given, k = C2's 100. A step is one search
+    of the whole query batch (device pointers, inputs resident in HBM); the build
+    (k-means + cell-major layout) is timed once, apart. roofline: the fine-scan
+    launches (scan_filter family: the bounded pass over every probed cell and its
+    retries) against the fp32 MFMA peak, with algorithmic FLOP = 2 d x the rows of
+    every query's probed cells. cpu_baseline: the oracle's searchCpu restatement
+    over the same probed cells on a bounded query prefix."""
+    import numpy as np
+    import datagen
+    import hipmem
+    import mflat
+    import oracle
+
+    mflat.load()
+    x, q = datagen.gmm()
+    if args.nq:
+        q = q[: args.nq]
+    nb, d = x.shape
+    nq = q.shape[0]
+    k = 100
+    nlist = args.nlist or max(64, int(np.sqrt(nb)))
+    nprobe = args.nprobe or max(1, nlist // 16)
+    storage = mflat.STORAGE_NAMES[args.storage]
+    log(f"[bench] ivf: nb={nb} d={d} nq={nq} k={k} nlist={nlist} nprobe={nprobe} storage={args.storage}")
+    idx = mflat.IvfIndex(d, mflat.MFLAT_METRIC_L2, nlist, storage)
+    t0 = time.perf_counter()
+    idx.build(x)
+    build_s = time.perf_counter() - t0
+    log(f"[bench] ivf build {build_s:.2f}s")
+    _, start, rid = idx.coarse()
+    probed = idx.probe(q, nprobe)
+    sizes = np.diff(start.astype(np.int64))
+    rows = int(sizes[probed].sum())
+    flop = 2.0 * d * rows
+
+    qd = hipmem.DeviceArray.from_numpy(q)
+    ids = hipmem.DeviceArray((nq, k), np.int32)
+    dist = hipmem.DeviceArray((nq, k), np.float32)
+    for i in range(args.warmup):
+        idx.search_device(qd, k, nprobe, ids, dist)
+    hipmem.synchronize()
+    mflat.profile_reset()
+    mflat.profile_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        idx.search_device(qd, k, nprobe, ids, dist)
+    hipmem.synchronize()
+    elapsed = time.perf_counter() - t0
+    mflat.profile_enable(False)
+    kern = {}
+    for fam in ("scan_filter", "scan_sample", "select", "norms", "prep"):
+        ms, n = mflat.profile_read(fam)
+        if n:
+            kern[fam] = {"total_ms": round(ms, 4), "launches": n, "mean_ms": round(ms / n, 4)}
+    gi = ids.numpy()
+    log(f"[bench] ivf {args.steps} steps in {elapsed:.3f}s")
+
+    peak = PEAK_FP32_MFMA_TFLOPS if storage == mflat.MFLAT_STORAGE_F32 else PEAK_F16_MFMA_TFLOPS
+    ach = flop * args.steps / (kern["scan_filter"]["total_ms"] / 1000.0) / 1e12
+    flat = mflat.FlatIndex(d, mflat.MFLAT_METRIC_L2)
+    flat.add(x)
+    fi, _, _ = flat.search(q, k)
+    flat.close()
+    recall = float(np.mean([len(set(gi[r].tolist()) & set(fi[r].tolist())) / k for r in range(nq)]))
+    out = {
+        "metric": f"QPS, IVF L2 d={d} nb={nb} nlist={nlist} nprobe={nprobe} k={k} (1 GPU)",
+        "value": round(nq * args.steps / elapsed, 2),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1000.0 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"f32": "fp32", "f16": "fp16 storage, fp32 accumulate",
+                  "bf16": "bf16 storage, fp32 accumulate"}[args.storage],
+        "data": "synthetic",
+        "config": {"workload": f"IVF over C2's database and queries (GMM 1024 centres, sigma 0.3, seed 1), "
+                               f"nlist={nlist}, nprobe={nprobe}, k={k}", "nb": nb, "d": d, "nq": nq, "k": k,
+                   "nlist": nlist, "nprobe": nprobe, "storage": args.storage, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(ach / peak, 4), "traffic": None},
+        "kernels": kern,
+        "probed_rows_per_query": round(rows / nq, 1),
+        "recall_vs_exact_flat": round(recall, 5),
+        "build_s": round(build_s, 3),
+    }
+    if not args.no_cpu_baseline:
+        payload = oracle.ivf_payload(x, rid)   # the reference keeps reorderedDb resident
+        for threads, key in ((1, "cpu_baseline"), (host_threads(), "cpu_baseline_all_cores")):
+            log(f"[bench] ivf cpu baseline ({threads} threads) ...")
+            t0 = time.perf_counter()
+            oracle.ivf_search(None, start, rid, q[:threads], k, probed[:threads], 0, threads=threads,
+                              payload=payload)
+            one = max(time.perf_counter() - t0, 1e-6) / threads
+            n = int(max(1, min(nq, 12.0 / one)))
+            t0 = time.perf_counter()
+            oi, _ = oracle.ivf_search(None, start, rid, q[:n], k, probed[:n], 0, threads=threads,
+                                      payload=payload)
+            dt = time.perf_counter() - t0
+            agree = float(np.mean([len(set(oi[r].tolist()) & set(gi[r].tolist())) / k for r in range(n)]))
+            out[key] = {"value": n / dt, "unit": "queries/s", "cores": threads, "kind": "port",
+                        "sample": f"first {n} of the {nq} queries over the same probed cells (searchCpu "
+                                  f"restatement), {dt:.1f} s on {threads} host thread(s); GPU/oracle id "
+                                  f"agreement on the sample {agree:.5f}"}
+    idx.close()
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -169,6 +282,10 @@ def main():
     ap.add_argument("--kmeans", type=int, default=0, metavar="ITERS",
                     help="time the device k-means loop (mflat_kmeans_train) on C5's points and centroid "
                          "count instead: one JSON line with ms per training iteration")
+    ap.add_argument("--ivf", action="store_true",
+                    help="time IVF search (mflat_ivf_*) on C2's database and queries instead")
+    ap.add_argument("--nlist", type=int, default=0, help="--ivf: cells (default max(64, sqrt(nb)))")
+    ap.add_argument("--nprobe", type=int, default=0, help="--ivf: probed cells (default nlist / 16)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 3 device-to-device copies of MIB MiB (counter calibration)")
     args = ap.parse_args()
@@ -195,6 +312,10 @@ def main():
               "(the database would shard by rows with an all-gather merge of per-GPU top-k; "
               "not built). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+
+    if args.ivf:
+        ivf_bench(args)
+        return
 
     import numpy as np
     import hipmem

@@ -20,7 +20,7 @@
 //                retry admits at least k fewer rows). Exactness never depends on
 //                the estimate, only the amount of work does.
 //
-// Small databases (nb <= 2*R0) skip the levels: one unbounded pass.
+// Small databases (nb <= max(2*R0, kSelLds)) skip the levels: one unbounded pass.
 #include "flat_index.hpp"
 
 #include <algorithm>
@@ -202,7 +202,10 @@ struct FlatIndex::Impl {
         if (mb <= kSmallMaxQ) r = std::min<int64_t>(r, kSelLds);
         r = std::max<int64_t>(r, std::max<int64_t>(4LL * k, 256));
         r = roundUp(r, kBM);
-        if (nb <= 2 * r) {
+        // A database whose every row fits one select block's LDS (e.g. an IVF
+        // coarse quantizer's centroids) takes one unbounded pass: cheaper than
+        // a sample level and its select.
+        if (nb <= std::max<int64_t>(2 * r, kSelLds)) {
             pl.direct = true;
             splitPlan(nb, (int)mb, dpad, storage, pl.rps1, pl.nsplit1);
             pl.cap1 = (int)pl.rps1;

@@ -233,10 +233,25 @@ struct IvfIndex::Impl {
         p.Q = Q; p.qnorm = qn; p.nq = nq; p.nqb = (nq + kBN - 1) / kBN; p.dpad = dpad;
         p.tau_key = tk; p.tau_id = ti;
         p.cand = cand.as<uint2>(); p.cnt = cnt.as<int>(); p.cap = cap;
-        p.ivf_work = wt.work; p.ivf_nwork = wt.nwork; p.ivf_ent = wt.ent; p.ivf_pos = posb;
+        p.ivf_ent = wt.ent; p.ivf_pos = posb;
         p.ivf_cell_pad = dCellPad.as<int64_t>(); p.ivf_cell_size = dCellSize.as<int>();
         p.ivf_nprobe = nprobe; p.ivf_nreg = nreg;
-        launch_scan_ivf(p, kernMetric(), pass, storage, wt.maxWork(nq, ranks, nlist), s);
+        p.ivf_work = wt.work; p.ivf_nwork = wt.nwork;
+        launch_scan_ivf(p, kernMetric(), pass, storage, kBN, wt.maxWork(nq, ranks, nlist), s);
+        p.ivf_work = wt.workN; p.ivf_nwork = wt.nwork + 1;
+        launch_scan_ivf(p, kernMetric(), pass, storage, kIvfNarrow, wt.maxWorkNarrow(nq, ranks, nlist, narrowMax()),
+                        s);
+    }
+
+    // Tile widths of the work tables: MFLAT_IVF_TILES = 128 / 32 (diagnostics)
+    // makes every work item wide / narrow; both compute the same keys, so the
+    // results never depend on it.
+    static int narrowMax() {
+        if (const char* e = std::getenv("MFLAT_IVF_TILES")) {
+            if (std::atoi(e) == 128) return 0;
+            if (std::atoi(e) == 32) return -1;
+        }
+        return kBN - kIvfNarrow;
     }
 
     SelectParams selectParams(int nq, int nsplit, int cap, int k) const {
@@ -261,7 +276,7 @@ struct IvfIndex::Impl {
             const int v = std::atoi(e);
             if (v >= 1) return v;
         }
-        return nprobe == 1 ? capR() : pow2ceil(std::max(2 * k, 128));
+        return nprobe == 1 ? capR() : pow2ceil(std::max(4 * k, 256));
     }
 
     // Search mb staged queries (qbuf / qh, norms in qnorm, probes in probe).
@@ -277,7 +292,7 @@ struct IvfIndex::Impl {
         if (nprobe > 1) {
             // A: the nearest cell of every query, no bound -> guaranteed bound
             const int ca = capA(k);
-            wt.build(probe.as<int>(), mb, nprobe, 1, nlist, dCellOrder.as<int>(), s);
+            wt.build(probe.as<int>(), mb, nprobe, 1, nlist, dCellOrder.as<int>(), narrowMax(), s);
             scanPass(kPassSample, mb, 1, nprobe, 1, ca, Q, qn, tauAk.as<float>(), tauAi.as<int>(), pos.as<int>(), s);
             SelectParams sp = selectParams(mb, 1, ca, k);
             sp.tau_k_key = tauAk.as<float>(); sp.tau_k_id = tauAi.as<int>();
@@ -290,7 +305,7 @@ struct IvfIndex::Impl {
             posOut.ensure((size_t)mb * k * sizeof(int32_t));
             posIds = posOut.as<int32_t>();
         }
-        wt.build(probe.as<int>(), mb, nprobe, nprobe, nlist, dCellOrder.as<int>(), s);
+        wt.build(probe.as<int>(), mb, nprobe, nprobe, nlist, dCellOrder.as<int>(), narrowMax(), s);
         scanPass(kPassFull, mb, nprobe, nprobe, nprobe, cb, Q, qn, tauAk.as<float>(), tauAi.as<int>(), pos.as<int>(),
                  s);
         {
@@ -328,7 +343,7 @@ struct IvfIndex::Impl {
                 launch_gather_i32(tauKi.as<int>(), cIdx.as<int>(), nf, 1, cTi.as<int>(), s);
                 launch_gather_i32(probe.as<int>(), cIdx.as<int>(), nf, nprobe, cProbe.as<int>(), s);
                 launch_gather_i32(pos.as<int>(), cIdx.as<int>(), nf, nprobe, cPos.as<int>(), s);
-                wt.build(cProbe.as<int>(), nf, nprobe, nprobe, nlist, dCellOrder.as<int>(), s);
+                wt.build(cProbe.as<int>(), nf, nprobe, nprobe, nlist, dCellOrder.as<int>(), narrowMax(), s);
                 scanPass(kPassFull, nf, nprobe, nprobe, nprobe, cr, cQ.p, cQn.as<float>(), cTk.as<float>(),
                          cTi.as<int>(), cPos.as<int>(), s);
                 SelectParams sp = selectParams(nf, nprobe, cr, k);

@@ -76,38 +76,85 @@ __global__ void ivf_positions_kernel(const int* __restrict__ probe, int m, int n
 // entries i < m * ranks of the pass: e = (i / ranks) * np + i % ranks. An
 // entry without a cell (probe -1) sorts after every cell and is never scanned.
 __global__ void ivf_entries_kernel(const int* __restrict__ probe, int m, int np, int ranks, int nlist,
-                                   int* __restrict__ keys, int* __restrict__ vals, int* __restrict__ counts) {
+                                   int* __restrict__ keys, int* __restrict__ vals) {
     const int64_t n = (int64_t)m * ranks;
     const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (i >= n) return;
     const int q = (int)(i / ranks);
     const int e = q * np + (int)(i - (int64_t)q * ranks);
     const int c = probe[e];
-    const bool ok = c >= 0 && c < nlist;
-    keys[i] = ok ? c : nlist;
+    keys[i] = c >= 0 && c < nlist ? c : nlist;
     vals[i] = e;
-    if (ok) atomicAdd(&counts[c], 1);
 }
 
-// tiles[i] = work items of cell cellOrder[i]
-__global__ void ivf_tiles_kernel(const int* __restrict__ cellOrder, const int* __restrict__ counts, int nlist,
-                                 int* __restrict__ tiles) {
+// Each cell's run [eStart[c], eEnd[c]) in the sorted keys (both pre-zeroed:
+// cells without entries keep an empty run) -- no atomics, whose contention on
+// the few hot cells of a batch costs more than the sort.
+__global__ void ivf_runs_kernel(const int* __restrict__ keys, int n, int nlist, int* __restrict__ eStart,
+                                int* __restrict__ eEnd) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < nlist) tiles[i] = (counts[cellOrder[i]] + kBN - 1) / kBN;
+    if (i >= n) return;
+    const int c = keys[i];
+    if (c >= nlist) return;
+    if (i == 0 || keys[i - 1] != c) eStart[c] = i;
+    if (i == n - 1 || keys[i + 1] != c) eEnd[c] = i + 1;
 }
 
-__global__ void ivf_work_kernel(const int* __restrict__ cellOrder, const int* __restrict__ counts,
-                                const int* __restrict__ eStart, const int* __restrict__ tEnd, int nlist,
-                                int4* __restrict__ work, int* __restrict__ nwork) {
+// A cell's n entries: wide tiles of kBN, then the rest in narrow tiles of
+// kIvfNarrow -- unless more than narrowMax remain, which take one more wide
+// tile (a tile's cost is its rows times its width; narrowMax = kBN - kIvfNarrow:
+// up to three narrow tiles are cheaper than a wide one). narrowMax = 0: wide
+// only; narrowMax < 0: narrow only.
+__device__ __forceinline__ void ivf_split(int n, int narrowMax, int& wide, int& narrow) {
+    if (narrowMax < 0) {
+        wide = 0;
+        narrow = (n + kIvfNarrow - 1) / kIvfNarrow;
+        return;
+    }
+    wide = n / kBN;
+    const int rem = n - wide * kBN;
+    if (rem > narrowMax) {
+        ++wide;
+        narrow = 0;
+    } else {
+        narrow = (rem + kIvfNarrow - 1) / kIvfNarrow;
+    }
+}
+
+// tiles of cell cellOrder[i]: wide in tilesW[i], narrow in tilesN[i]
+__global__ void ivf_tiles_kernel(const int* __restrict__ cellOrder, const int* __restrict__ eStart,
+                                 const int* __restrict__ eEnd, int nlist, int narrowMax, int* __restrict__ tilesW,
+                                 int* __restrict__ tilesN) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nlist) return;
     const int c = cellOrder[i];
-    const int cnt = counts[c];
-    const int nt = (cnt + kBN - 1) / kBN;
-    const int t0 = tEnd[i] - nt;
-    for (int t = 0; t < nt; ++t)
-        work[t0 + t] = make_int4(c, eStart[c] + t * kBN, min(kBN, cnt - t * kBN), 0);
-    if (i == nlist - 1) *nwork = tEnd[i];
+    int w, nn;
+    ivf_split(eEnd[c] - eStart[c], narrowMax, w, nn);
+    tilesW[i] = w;
+    tilesN[i] = nn;
+}
+
+__global__ void ivf_work_kernel(const int* __restrict__ cellOrder, const int* __restrict__ eEnd,
+                                const int* __restrict__ eStart, const int* __restrict__ tEndW,
+                                const int* __restrict__ tEndN, int nlist, int narrowMax, int4* __restrict__ work,
+                                int4* __restrict__ workN, int* __restrict__ nwork) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nlist) return;
+    const int c = cellOrder[i];
+    const int e0 = eStart[c];
+    const int cnt = eEnd[c] - e0;
+    int nw, nn;
+    ivf_split(cnt, narrowMax, nw, nn);
+    const int t0 = tEndW[i] - nw;
+    for (int t = 0; t < nw; ++t) work[t0 + t] = make_int4(c, e0 + t * kBN, min(kBN, cnt - t * kBN), 0);
+    const int n0 = tEndN[i] - nn;
+    const int base = nw * kBN;
+    for (int t = 0; t < nn; ++t)
+        workN[n0 + t] = make_int4(c, e0 + base + t * kIvfNarrow, min(kIvfNarrow, cnt - base - t * kIvfNarrow), 0);
+    if (i == nlist - 1) {
+        nwork[0] = tEndW[i];
+        nwork[1] = tEndN[i];
+    }
 }
 
 __global__ void ivf_finalize_kernel(int32_t* __restrict__ ids, int m, int k, const int* __restrict__ pos,
@@ -174,25 +221,36 @@ int IvfWorkTable::maxWork(int m, int ranks, int nlist) const {
     return (int)w;
 }
 
+int IvfWorkTable::maxWorkNarrow(int m, int ranks, int nlist, int narrowMax) const {
+    const int64_t e = (int64_t)m * ranks;
+    int64_t w = (e + kIvfNarrow - 1) / kIvfNarrow + nlist;
+    if (narrowMax >= 0)   // at most ceil(min(narrowMax, kBN - 1) / kIvfNarrow) per cell
+        w = std::min<int64_t>(w, (int64_t)nlist * ((std::min(narrowMax, kBN - 1) + kIvfNarrow - 1) / kIvfNarrow));
+    if (w > 0x7FFFFFFF) throw std::runtime_error("ivf: too many work items");
+    return (int)w;
+}
+
 IvfWorkTable::~IvfWorkTable() { release(); }
 
 void IvfWorkTable::release() {
-    for (void** p : {(void**)&ent, (void**)&work, (void**)&nwork, (void**)&keysIn, (void**)&keysOut,
-                     (void**)&valsIn, (void**)&counts, (void**)&eStart, (void**)&tiles, (void**)&tEnd, &temp}) {
+    for (void** p : {(void**)&ent, (void**)&work, (void**)&workN, (void**)&nwork, (void**)&keysIn, (void**)&keysOut,
+                     (void**)&valsIn, (void**)&eEnd, (void**)&eStart, (void**)&tiles, (void**)&tEnd,
+                     (void**)&tilesN, (void**)&tEndN, &temp}) {
         if (*p) (void)hipFree(*p);
         *p = nullptr;
     }
     tempBytes = 0;
-    capE = capWork = capCells = 0;
+    capE = capWork = capWorkN = capCells = 0;
 }
 
 void IvfWorkTable::build(const int* probe, int m, int np, int ranks, int nlist, const int* cellOrder,
-                         hipStream_t s) {
+                         int narrowMax, hipStream_t s) {
     const int64_t ne64 = (int64_t)m * ranks;
     if (m <= 0 || ranks < 1 || ranks > np || nlist < 1) throw std::runtime_error("ivf work table: bad sizes");
     if (ne64 > 0x7FFFFFFF) throw std::runtime_error("ivf work table: too many entries");
     const int ne = (int)ne64;
     const int mw = maxWork(m, ranks, nlist);
+    const int mn = maxWorkNarrow(m, ranks, nlist, narrowMax);
     if (ne > capE) {
         for (int** p : {&ent, &keysIn, &keysOut, &valsIn}) {
             if (*p) (void)hipFree(*p);
@@ -207,26 +265,31 @@ void IvfWorkTable::build(const int* probe, int m, int np, int ranks, int nlist, 
         check(hipMalloc((void**)&work, (size_t)mw * sizeof(int4)), "hipMalloc(work)");
         capWork = mw;
     }
+    if (mn > capWorkN) {
+        if (workN) (void)hipFree(workN);
+        workN = nullptr;
+        check(hipMalloc((void**)&workN, (size_t)mn * sizeof(int4)), "hipMalloc(work)");
+        capWorkN = mn;
+    }
     if (nlist > capCells) {
-        for (int** p : {&counts, &eStart, &tiles, &tEnd}) {
+        for (int** p : {&eEnd, &eStart, &tiles, &tEnd, &tilesN, &tEndN}) {
             if (*p) (void)hipFree(*p);
             *p = nullptr;
         }
-        for (int** p : {&counts, &eStart, &tiles, &tEnd})
+        for (int** p : {&eEnd, &eStart, &tiles, &tEnd, &tilesN, &tEndN})
             check(hipMalloc((void**)p, (size_t)nlist * sizeof(int)), "hipMalloc(cells)");
         capCells = nlist;
     }
-    if (!nwork) check(hipMalloc((void**)&nwork, sizeof(int)), "hipMalloc(nwork)");
+    if (!nwork) check(hipMalloc((void**)&nwork, 2 * sizeof(int)), "hipMalloc(nwork)");
 
     int bits = 1;
     while ((1 << bits) <= nlist) ++bits;   // keys 0 .. nlist
-    size_t needSort = 0, needEx = 0, needIn = 0;
+    size_t needSort = 0, needIn = 0;
     check(hipcub::DeviceRadixSort::SortPairs(nullptr, needSort, (const int*)keysIn, keysOut, (const int*)valsIn,
                                              ent, ne, 0, bits, s),
           "SortPairs (size)");
-    check(hipcub::DeviceScan::ExclusiveSum(nullptr, needEx, (const int*)counts, eStart, nlist, s), "ExclusiveSum (size)");
     check(hipcub::DeviceScan::InclusiveSum(nullptr, needIn, (const int*)tiles, tEnd, nlist, s), "InclusiveSum (size)");
-    const size_t need = std::max({needSort, needEx, needIn, (size_t)16});
+    const size_t need = std::max({needSort, needIn, (size_t)16});
     if (need > tempBytes) {
         if (temp) (void)hipFree(temp);
         temp = nullptr;
@@ -236,20 +299,24 @@ void IvfWorkTable::build(const int* probe, int m, int np, int ranks, int nlist, 
 
     void* tok;
     prof_begin(kFamPrep, s, &tok);
-    check(hipMemsetAsync(counts, 0, (size_t)nlist * sizeof(int), s), "hipMemsetAsync(counts)");
-    ivf_entries_kernel<<<(int)((ne + 255) / 256), 256, 0, s>>>(probe, m, np, ranks, nlist, keysIn, valsIn, counts);
+    check(hipMemsetAsync(eEnd, 0, (size_t)nlist * sizeof(int), s), "hipMemsetAsync(eEnd)");
+    check(hipMemsetAsync(eStart, 0, (size_t)nlist * sizeof(int), s), "hipMemsetAsync(eStart)");
+    ivf_entries_kernel<<<(int)((ne + 255) / 256), 256, 0, s>>>(probe, m, np, ranks, nlist, keysIn, valsIn);
     check(hipGetLastError(), "ivf_entries");
     size_t t = tempBytes;
     check(hipcub::DeviceRadixSort::SortPairs(temp, t, (const int*)keysIn, keysOut, (const int*)valsIn, ent, ne, 0,
                                              bits, s),
           "SortPairs");
-    t = tempBytes;
-    check(hipcub::DeviceScan::ExclusiveSum(temp, t, (const int*)counts, eStart, nlist, s), "ExclusiveSum");
-    ivf_tiles_kernel<<<(nlist + 255) / 256, 256, 0, s>>>(cellOrder, counts, nlist, tiles);
+    ivf_runs_kernel<<<(ne + 255) / 256, 256, 0, s>>>(keysOut, ne, nlist, eStart, eEnd);
+    check(hipGetLastError(), "ivf_runs");
+    ivf_tiles_kernel<<<(nlist + 255) / 256, 256, 0, s>>>(cellOrder, eStart, eEnd, nlist, narrowMax, tiles, tilesN);
     check(hipGetLastError(), "ivf_tiles");
     t = tempBytes;
     check(hipcub::DeviceScan::InclusiveSum(temp, t, (const int*)tiles, tEnd, nlist, s), "InclusiveSum");
-    ivf_work_kernel<<<(nlist + 255) / 256, 256, 0, s>>>(cellOrder, counts, eStart, tEnd, nlist, work, nwork);
+    t = tempBytes;
+    check(hipcub::DeviceScan::InclusiveSum(temp, t, (const int*)tilesN, tEndN, nlist, s), "InclusiveSum");
+    ivf_work_kernel<<<(nlist + 255) / 256, 256, 0, s>>>(cellOrder, eEnd, eStart, tEnd, tEndN, nlist, narrowMax, work,
+                                                         workN, nwork);
     check(hipGetLastError(), "ivf_work");
     prof_end(tok, s);
 }

@@ -23,20 +23,30 @@ void launch_gather_i32(const int* src, const int* idx, int n, int width, int* ds
 // order (cells in probe order, rows in cell order), for q < m.
 void launch_ivf_positions(const int* probe, int m, int np, const int* cellSize, int* pos, hipStream_t s);
 
+constexpr int kIvfNarrow = 32;   // entries per narrow work item (one 32-query block)
+
 // Work table of one fine-scan pass over the entries e = q * np + r of queries
 // q < m and ranks r < ranks (ranks = 1: the nearest cell only; ranks = np: all):
 //   ent        the entries sorted by (cell, e) -- a stable sort by cell
-//   work[w]    (cell, first entry, entries <= 128, 0): each cell's entries in
-//              runs of 128, cells in the order cellOrder gives (decreasing size)
-//   nwork      the number of work items (device int)
-// maxWork() bounds the work items (the grid of the scan launch). Keeps its
-// scratch between calls.
+//   work[w]    wide items (cell, first entry, entries <= 128, 0): each cell's
+//              entries in runs of 128, cells in the order cellOrder gives
+//              (decreasing size)
+//   workN[w]   narrow items (entries <= 32): the last n mod 128 entries of a
+//              cell when at most narrowMax of them remain (else they take one
+//              more wide item); narrowMax = 96 balances the two tile costs,
+//              0 makes every item wide, < 0 every item narrow
+//   nwork      device ints: wide, narrow item counts
+// maxWork() / maxWorkNarrow() bound them (the grids of the scan launches).
+// Keeps its scratch between calls.
 struct IvfWorkTable {
     int* ent = nullptr;
     int4* work = nullptr;
+    int4* workN = nullptr;
     int* nwork = nullptr;
     int maxWork(int m, int ranks, int nlist) const;
-    void build(const int* probe, int m, int np, int ranks, int nlist, const int* cellOrder, hipStream_t s);
+    int maxWorkNarrow(int m, int ranks, int nlist, int narrowMax) const;
+    void build(const int* probe, int m, int np, int ranks, int nlist, const int* cellOrder, int narrowMax,
+               hipStream_t s);
     ~IvfWorkTable();
     void release();
 
@@ -44,13 +54,15 @@ private:
     int* keysIn = nullptr;
     int* keysOut = nullptr;
     int* valsIn = nullptr;
-    int* counts = nullptr;
+    int* eEnd = nullptr;
     int* eStart = nullptr;
     int* tiles = nullptr;
     int* tEnd = nullptr;
+    int* tilesN = nullptr;
+    int* tEndN = nullptr;
     void* temp = nullptr;
     size_t tempBytes = 0;
-    int capE = 0, capWork = 0, capCells = 0;
+    int capE = 0, capWork = 0, capWorkN = 0, capCells = 0;
 };
 
 // In place: ids[q * k + i] (a scan position, or -1) -> the original row id

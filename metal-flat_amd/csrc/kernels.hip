@@ -313,28 +313,29 @@ __global__ void max_norm_kernel(const float* __restrict__ xn, int64_t n, unsigne
 // ---------------------------------------------------------------------------
 //
 // One group of a lane's 32 x 32 accumulators: rows r0 .. r0 + 3 (register
-// g4*4 + i of each block, row norms xn4) against the lane's query slots b0 and
-// b0 + 1 (acc[b0 + b], per-query state tk/ti/qn/ft/qv). Rows at or above
-// rowLim are padding; row r reports id r * idStride + idb[slot]. Eight fast
+// g4*4 + i of each block, row norms xn4) against the lane's query slots b0 ..
+// b0 + NS - 1 (acc[b0 + b], per-query state tk/ti/qn/ft/qv). Rows at or above
+// rowLim are padding; row r reports id r * idStride + idb[slot]. 4 NS fast
 // tests without branches, then one wave-level branch: a group rarely holds a
 // survivor in any of the 64 lanes. Only survivors take the exact
 // lexicographic test; they go to emit(slot, key, id), or, for k = 1, replace
 // the slot's running best.
-template <int METRIC, int PASS, int NB, class Emit>
+template <int METRIC, int PASS, int NB, int NS, class Emit>
 __device__ __forceinline__ void filter_group(const fx16 (&acc)[NB], int g4, int b0, const fx4& xn4, int64_t r0,
                                              int64_t rowLim, int idStride, const int (&idb)[NB],
                                              const ScanParams& p, float (&tk)[NB], int (&ti)[NB],
                                              const float (&qn)[NB], float (&ft)[NB], const bool (&qv)[NB],
                                              Emit&& emit) {
-    bool f[4][2];
+    bool f[4][NS];
+    bool any = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
+        for (int b = 0; b < NS; ++b) {
             const float dot = acc[b0 + b][g4 * 4 + i];
             f[i][b] = METRIC == 0 ? fmaf(-2.0f, dot, xn4[i]) <= ft[b0 + b] : dot >= ft[b0 + b];
+            any |= f[i][b];
         }
-    const bool any = f[0][0] | f[0][1] | f[1][0] | f[1][1] | f[2][0] | f[2][1] | f[3][0] | f[3][1];
     if (!any) return;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -342,7 +343,7 @@ __device__ __forceinline__ void filter_group(const fx16 (&acc)[NB], int g4, int 
         const bool rv = row < rowLim;
         const int idr = (int)(row * idStride);
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
+        for (int b = 0; b < NS; ++b) {
             const int bn = b0 + b;
             if (!f[i][b]) continue;
             const int id = idr + idb[bn];
@@ -613,7 +614,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
                     const int64_t r0 = tileRow0 + rl;
                     fx4 xn4 = {0.0f, 0.0f, 0.0f, 0.0f};
                     if (METRIC == 0) xn4 = xnr[bm][g4];
-                    filter_group<METRIC, PASS, 2>(acc[bm], g4, 0, xn4, r0, p.nrows, p.id_stride, idb, p, tk,
+                    filter_group<METRIC, PASS, 2, 2>(acc[bm], g4, 0, xn4, r0, p.nrows, p.id_stride, idb, p, tk,
                                                   ti, qn, ft, qv,
                                                   [&](int bn, float key, int id) {
                         const int ql = wn * 64 + bn * 32 + r32;
@@ -693,16 +694,17 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
 // entry's scan position, and survivors go to the entry's region
 // (query * ivf_nreg + rank). Work items are in decreasing cell size, so the
 // largest run first.
-template <int S, int METRIC, int PASS, int G, bool IVF>
+template <int S, int METRIC, int PASS, int G, bool IVF, int NB>
 __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
+    constexpr int TQ = 32 * NB;                    // queries per tile (NB blocks of 32)
     constexpr int ES = S == kF32 ? 4 : 2;
     constexpr int NK = S == kF32 ? 4 : 2;          // operand pieces per row block per chunk
     constexpr int KSTEP = S == kF32 ? 256 : 512;   // byte step between a lane's pieces in a chunk
     constexpr int CB = 32 * 32 * ES;               // bytes per 32 x 32 chunk
-    extern __shared__ __attribute__((aligned(16))) float sQr[];   // [kBN][dpad + 16 / ES] elements
+    extern __shared__ __attribute__((aligned(16))) float sQr[];   // [TQ][dpad + 16 / ES] elements
     __shared__ __attribute__((aligned(16))) float sXn[4 * 64];    // per wave: its slice's row norms
-    __shared__ int sCnt[kBN];
-    __shared__ unsigned long long sBest[kBN];
+    __shared__ int sCnt[TQ];
+    __shared__ unsigned long long sBest[TQ];
     // Per-wave survivor ring (fp32 full and retry passes): (key, id, query)
     // staged in LDS and written to the candidate regions half a ring at a
     // time, so the next slices' prefetch waits rarely wait on survivor stores
@@ -713,9 +715,9 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     __shared__ int sRingId[RING ? 4 * kRing : 1];
     __shared__ int sRingQ[RING ? 4 * kRing : 1];
     __shared__ int sRingN[4];
-    __shared__ int sEnt[IVF ? kBN : 1];   // IVF: the tile's entries (-1: empty slot)
-    __shared__ int sQi[IVF ? kBN : 1];    // ... their queries
-    __shared__ int sReg[IVF ? kBN : 1];   // ... their candidate regions
+    __shared__ int sEnt[IVF ? TQ : 1];   // IVF: the tile's entries (-1: empty slot)
+    __shared__ int sQi[IVF ? TQ : 1];    // ... their queries
+    __shared__ int sReg[IVF ? TQ : 1];   // ... their candidate regions
 
     int qb = 0, split = 0;
     int4 wk = make_int4(0, 0, 0, 0);   // IVF work item: (cell, first entry, entries, 0)
@@ -744,7 +746,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     const int ldqB = (p.dpad + 16 / ES) * ES;   // LDS query row stride (bytes): 16 B of padding
 
     if constexpr (IVF) {
-        if (tid < kBN) {
+        if (tid < TQ) {
             const int e = tid < wk.z ? p.ivf_ent[wk.y + tid] : -1;
             const int q = e >= 0 ? e / p.ivf_nprobe : -1;
             sEnt[tid] = e;
@@ -756,7 +758,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     {
         const int rowP = p.dpad * ES / 16;
         const fx4* qg = (const fx4*)p.Q + (int64_t)qb * kBN * rowP;
-        for (int i = tid; i < kBN * rowP; i += 256) {
+        for (int i = tid; i < TQ * rowP; i += 256) {
             const int row = i / rowP;
             const int c = i - row * rowP;
             fx4 v;
@@ -769,19 +771,19 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
             *(fx4*)((char*)sQr + row * ldqB + c * 16) = v;
         }
     }
-    if (tid < kBN) {
+    if (tid < TQ) {
         sCnt[tid] = 0;
         sBest[tid] = ~0ull;
     }
     if (tid < 4) sRingN[tid] = 0;
 
-    // Per-lane query state for its 4 query blocks; bounds as in scan_filter.
-    float tk[4], qn[4], ft[4];
-    int ti[4];
-    bool qv[4];
-    int idb[4] = {0, 0, 0, 0};   // IVF: scan position of the cell's first row, per slot
+    // Per-lane query state for its NB query blocks; bounds as in scan_filter.
+    float tk[NB], qn[NB], ft[NB];
+    int ti[NB];
+    bool qv[NB];
+    int idb[NB] = {};   // IVF: scan position of the cell's first row, per slot
 #pragma unroll
-    for (int bn = 0; bn < 4; ++bn) {
+    for (int bn = 0; bn < NB; ++bn) {
         int q;
         if constexpr (IVF) {
             q = sQi[bn * 32 + r32];
@@ -843,7 +845,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
         return *(const fx4*)(qlds + bn * 32 * ldqB + t * 32 * ES + k * 32);
     };
 
-    fx16 acc[2][4];
+    fx16 acc[2][NB];
     // One chunk of MFMAs from operand pieces a[bm][k]; a slice's first chunk
     // starts every accumulator from an inline zero.
     auto mma = [&](const fx4 (&a)[2][NK], int t, auto zeroTag) {
@@ -852,23 +854,23 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
                         0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int k = 0; k < NK; ++k) {
-            fx4 b[4];
+            fx4 b[NB];
 #pragma unroll
-            for (int bn = 0; bn < 4; ++bn) b[bn] = ldb(bn, t, k);
+            for (int bn = 0; bn < NB; ++bn) b[bn] = ldb(bn, t, k);
             if constexpr (S == kF32) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
 #pragma unroll
                     for (int bm = 0; bm < 2; ++bm)
 #pragma unroll
-                        for (int bn = 0; bn < 4; ++bn)
+                        for (int bn = 0; bn < NB; ++bn)
                             acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(
                                 a[bm][k][j], b[bn][j], (ZERO && k == 0 && j == 0) ? z : acc[bm][bn], 0, 0, 0);
             } else {
 #pragma unroll
                 for (int bm = 0; bm < 2; ++bm)
 #pragma unroll
-                    for (int bn = 0; bn < 4; ++bn)
+                    for (int bn = 0; bn < NB; ++bn)
                         acc[bm][bn] = mfma32x32x16<S>(a[bm][k], b[bn], (ZERO && k == 0) ? z : acc[bm][bn]);
             }
         }
@@ -890,9 +892,9 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
                 fx4 xn4 = {0.0f, 0.0f, 0.0f, 0.0f};
                 if (METRIC == 0) xn4 = *(const fx4*)(sXn + wave * 64 + rl);
 #pragma unroll
-                for (int bp = 0; bp < 2; ++bp)
-                    filter_group<METRIC, PASS, 4>(acc[bm], g4, 2 * bp, xn4, r0, rowLim, idStride, idb, p, tk,
-                                                  ti, qn, ft, qv,
+                for (int bp = 0; bp < (NB + 1) / 2; ++bp)
+                    filter_group<METRIC, PASS, NB, NB == 1 ? 1 : 2>(acc[bm], g4, 2 * bp, xn4, r0, rowLim, idStride,
+                                                                     idb, p, tk, ti, qn, ft, qv,
                                                   [&](int bn, float key, int id) {
                         const int ql = bn * 32 + r32;
                         const int pos = RING ? atomicAdd(&sRingN[wave], 1) : kRing;
@@ -1001,12 +1003,12 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     flush(1);
     if (PASS == kPassArgmin) {
 #pragma unroll
-        for (int bn = 0; bn < 4; ++bn)
+        for (int bn = 0; bn < NB; ++bn)
             if (ti[bn] >= 0)
                 atomicMin(&sBest[bn * 32 + r32],
                           ((unsigned long long)key_to_ord(__float_as_uint(tk[bn])) << 32) | (unsigned)ti[bn]);
         __syncthreads();
-        if (tid < kBN) {
+        if (tid < TQ) {
             const int q = qb * kBN + tid;
             if (q < p.nq && sBest[tid] != ~0ull) atomicMin(&p.best[q], sBest[tid]);
         }
@@ -1015,7 +1017,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     __syncthreads();
     if constexpr (IVF) {
         if (tid < wk.z) p.cnt[sReg[tid]] = sCnt[tid];
-    } else if (tid < kBN) {
+    } else if (tid < TQ) {
         const int q = qb * kBN + tid;
         if (q < p.nq) p.cnt[(int64_t)q * p.nsplit + split] = sCnt[tid];
     }
@@ -1765,11 +1767,11 @@ static void allow_resident_lds(const void* f) {
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kResidentMaxLds) != hipSuccess)
         throw std::runtime_error("scan_resident: cannot raise the dynamic LDS limit");
 }
-template <int S, int M, int P, int G, bool IVF = false>
+template <int S, int M, int P, int G, bool IVF = false, int NB = 4>
 static void launch_resident_p(const ScanParams& p, int g, size_t lds, hipStream_t s) {
-    static const bool ok = (allow_resident_lds((const void*)scan_resident_kernel<S, M, P, G, IVF>), true);
+    static const bool ok = (allow_resident_lds((const void*)scan_resident_kernel<S, M, P, G, IVF, NB>), true);
     (void)ok;
-    scan_resident_kernel<S, M, P, G, IVF><<<g, 256, lds, s>>>(p);
+    scan_resident_kernel<S, M, P, G, IVF, NB><<<g, 256, lds, s>>>(p);
 }
 template <int S, int M, int G>
 static void launch_resident_g(const ScanParams& p, int pass, int g, size_t lds, hipStream_t s) {
@@ -1794,29 +1796,35 @@ static void launch_resident_s(const ScanParams& p, int metric, int pass, int g, 
     else launch_resident<S, 1>(p, pass, g, lds, s);
 }
 // IVF fine scan: kPassSample (no bound, the bound pass) or kPassFull, with
-// the G variants of the flat scan (the same key function for a given dpad).
-template <int S, int M, int G>
+// the G variants of the flat scan (the same key function for a given dpad);
+// tiles of 128 (NB = 4) or 32 (NB = 1) queries, bit-identical keys.
+template <int S, int M, int G, int NB>
 static void launch_ivf_g(const ScanParams& p, int pass, int g, size_t lds, hipStream_t s) {
-    if (pass == kPassSample) launch_resident_p<S, M, kPassSample, G, true>(p, g, lds, s);
-    else launch_resident_p<S, M, kPassFull, G, true>(p, g, lds, s);
+    if (pass == kPassSample) launch_resident_p<S, M, kPassSample, G, true, NB>(p, g, lds, s);
+    else launch_resident_p<S, M, kPassFull, G, true, NB>(p, g, lds, s);
 }
-template <int S, int M>
+template <int S, int M, int NB>
 static void launch_ivf(const ScanParams& p, int pass, int g, size_t lds, hipStream_t s) {
     if constexpr (S != kF32) {
-        if (p.dpad == 96) return launch_ivf_g<S, M, 3>(p, pass, g, lds, s);
-        if (p.dpad == 128) return launch_ivf_g<S, M, 4>(p, pass, g, lds, s);
+        if (p.dpad == 96) return launch_ivf_g<S, M, 3, NB>(p, pass, g, lds, s);
+        if (p.dpad == 128) return launch_ivf_g<S, M, 4, NB>(p, pass, g, lds, s);
     }
-    launch_ivf_g<S, M, 0>(p, pass, g, lds, s);
+    launch_ivf_g<S, M, 0, NB>(p, pass, g, lds, s);
 }
 template <int S>
-static void launch_ivf_s(const ScanParams& p, int metric, int pass, int g, size_t lds, hipStream_t s) {
-    if (metric == 0) launch_ivf<S, 0>(p, pass, g, lds, s);
-    else launch_ivf<S, 1>(p, pass, g, lds, s);
+static void launch_ivf_s(const ScanParams& p, int metric, int pass, int nb, int g, size_t lds, hipStream_t s) {
+    if (nb == 4) {
+        if (metric == 0) launch_ivf<S, 0, 4>(p, pass, g, lds, s);
+        else launch_ivf<S, 1, 4>(p, pass, g, lds, s);
+    } else {
+        if (metric == 0) launch_ivf<S, 0, 1>(p, pass, g, lds, s);
+        else launch_ivf<S, 1, 1>(p, pass, g, lds, s);
+    }
 }
 
-static size_t resident_lds_bytes(int dpad, int storage) {
+static size_t resident_lds_bytes(int dpad, int storage, int tileQueries = kBN) {
     const int es = elem_bytes(storage);
-    return (size_t)kBN * (dpad + 16 / es) * es;
+    return (size_t)tileQueries * (dpad + 16 / es) * es;
 }
 
 bool resident_scan_fits(int dpad, int storage) {
@@ -1889,19 +1897,22 @@ void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, 
     check_launch("scan_filter");
 }
 
-void launch_scan_ivf(const ScanParams& p, int metric, int pass, int storage, int grid, hipStream_t s) {
+void launch_scan_ivf(const ScanParams& p, int metric, int pass, int storage, int tileQueries, int grid,
+                     hipStream_t s) {
     if (storage != kF32 && storage != kF16 && storage != kBF16) throw std::runtime_error("scan_ivf: unknown storage type");
     if (grid <= 0) return;
     if (pass != kPassSample && pass != kPassFull) throw std::runtime_error("scan_ivf: bad pass");
+    if (tileQueries != 128 && tileQueries != 32) throw std::runtime_error("scan_ivf: tiles hold 128 or 32 queries");
     if (!resident_scan_fits(p.dpad, storage) || p.dpad % kBK != 0 || p.cap < 1 || p.ivf_nprobe < 1 ||
         p.ivf_nreg < 1)
         throw std::runtime_error("scan_ivf: bad parameters");
     void* tok;
     prof_begin(pass == kPassSample ? kFamScanSample : kFamScan, s, &tok);
-    const size_t lds = resident_lds_bytes(p.dpad, storage);
-    if (storage == kF32) launch_ivf_s<kF32>(p, metric, pass, grid, lds, s);
-    else if (storage == kF16) launch_ivf_s<kF16>(p, metric, pass, grid, lds, s);
-    else launch_ivf_s<kBF16>(p, metric, pass, grid, lds, s);
+    const size_t lds = resident_lds_bytes(p.dpad, storage, tileQueries);
+    const int nb = tileQueries / 32;
+    if (storage == kF32) launch_ivf_s<kF32>(p, metric, pass, nb, grid, lds, s);
+    else if (storage == kF16) launch_ivf_s<kF16>(p, metric, pass, nb, grid, lds, s);
+    else launch_ivf_s<kBF16>(p, metric, pass, nb, grid, lds, s);
     prof_end(tok, s);
     check_launch("scan_ivf");
 }

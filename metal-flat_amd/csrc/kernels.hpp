@@ -177,9 +177,11 @@ bool resident_scan_fits(int dpad, int storage);
 void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, hipStream_t s,
                         bool allowSmall = true);
 // IVF fine scan (scan_resident over the work items of ScanParams::ivf_*; the
-// query tile must fit, resident_scan_fits): pass kPassSample or kPassFull,
-// grid = an upper bound of the work items.
-void launch_scan_ivf(const ScanParams& p, int metric, int pass, int storage, int grid, hipStream_t s);
+// 128-query tile must fit, resident_scan_fits): pass kPassSample or kPassFull,
+// work items of up to tileQueries (128 or 32) entries, grid = an upper bound of
+// the work items. Both tile widths compute bit-identical keys.
+void launch_scan_ivf(const ScanParams& p, int metric, int pass, int storage, int tileQueries, int grid,
+                     hipStream_t s);
 void launch_select(const SelectParams& p, hipStream_t s);
 void launch_argmin_finalize(const unsigned long long* best, int nq, int metric, int32_t* ids, float* vals,
                             hipStream_t s);

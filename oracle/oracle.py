@@ -301,18 +301,23 @@ def ivf_probe(cent, q, nprobe, metric=0):
     return ids
 
 
-def ivf_search(db, cell_start, rid, q, k, probed, metric=0, threads=1):
+def ivf_payload(db, rid, metric=0):
+    """The rows in cell order (the reference's reorderedDb), Cosine-normalised."""
+    db = normalize_rows(db) if metric == 2 else _f32(db)
+    return np.ascontiguousarray(db[np.asarray(rid, np.int64)]) if db.size else db
+
+
+def ivf_search(db, cell_start, rid, q, k, probed, metric=0, threads=1, payload=None):
     """searchCpu over the given probed cells: (ids [m, k], values [m, k]).
     db: the caller's rows (row-major, original order); Cosine rows and
-    queries are normalised and ranked by the dot product."""
-    db = _f32(db)
+    queries are normalised and ranked by the dot product. payload: a
+    precomputed ivf_payload(db, rid, metric) (db is then unused)."""
     q = _f32(q)
+    rid = np.ascontiguousarray(rid, np.int32)
+    rdb = ivf_payload(db, rid, metric) if payload is None else payload
     if metric == 2:
-        db = normalize_rows(db)
         q = normalize_rows(q)
         metric = 1
-    rid = np.ascontiguousarray(rid, np.int32)
-    rdb = np.ascontiguousarray(db[rid]) if db.size else db
     start = np.ascontiguousarray(cell_start, np.int32)
     probed = np.ascontiguousarray(probed, np.int32)
     m, d = q.shape

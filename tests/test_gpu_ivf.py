@@ -203,3 +203,18 @@ def test_rebuild_replaces_index(gpu_ok):
         idx.build(x2)
         assert idx.size() == 2_500
         check(idx, x2, q, 12, 4, L2, exact=True)
+
+
+def test_tile_widths_compute_identical_keys(gpu_ok, monkeypatch):
+    """Work items of 128 and of 32 queries run the same per-pair MFMA sequence:
+    all-wide, all-narrow and mixed tables give bit-identical results (the bound
+    pass and the full pass may use different widths for the same row)."""
+    x, q = datagen.gmm(nb=50_000, nq=900, d=128, ncenters=128, seed=26)
+    with build(x, 96) as idx:
+        ref = idx.search(q, 100, 10)
+        for tiles in ("128", "32"):
+            monkeypatch.setenv("MFLAT_IVF_TILES", tiles)
+            got = idx.search(q, 100, 10)
+            parity.exact(got[0], got[1], ref[0], ref[1])
+        monkeypatch.delenv("MFLAT_IVF_TILES")
+        check(idx, x, q, 100, 10, L2)
