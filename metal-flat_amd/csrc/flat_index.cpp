@@ -406,6 +406,7 @@ struct FlatIndex::Impl {
                  tauSk.as<float>(), tauSi.as<int>(), pl.cap1, s);
             SelectParams sp = selectParams(mb, pl.nsplit1, pl.cap1, k, 1);
             sp.out_ids = oIds; sp.out_vals = oVals;
+            sp.expect = (int)std::min<int64_t>(nb, INT_MAX);   // every row is stored
             launch_select(sp, s);
             return;
         }
@@ -422,6 +423,7 @@ struct FlatIndex::Impl {
              tauSk.as<float>(), tauSi.as<int>(), pl.cap0, s, kPassSample);
         {
             SelectParams sp = selectParams(mb, pl.nsplit0, pl.cap0, k, pl.j);
+            sp.expect = (int)pl.R0;   // the sample is stored whole
             sp.j2 = pl.j2;
             sp.tau_j_key = tauSk.as<float>(); sp.tau_j_id = tauSi.as<int>();
             sp.tau_j2_key = tauS2k.as<float>(); sp.tau_j2_id = tauS2i.as<int>();

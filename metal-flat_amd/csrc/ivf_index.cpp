@@ -11,15 +11,18 @@
 //   probe    the coarse FlatIndex's top-nprobe over the centroids (nearest
 //            first, ties to the lower cell id: the reference's FlatIndex probe
 //            and its partial_sort over (distance, cell), CoarseQuantizer.mm:170-188)
-//   A bound  each query's nearest cell alone, no bound; the k-th best (key,
+//   A bound  each query's nearest cells, up to the first that brings its scan
+//            to k rows (at most kBoundRanks), no bound; the k-th best (key,
 //            scan position) of what it stored is a GUARANTEED bound -- the k-th
 //            best over a subset of the probed rows is never better than the
 //            k-th best over all of them (skipped for nprobe = 1)
-//   B scan   all probed cells with that bound; select the k best of the
-//            stored survivors. Exact unless a candidate region overflowed.
-//   retry    overflowed queries rerun B with the k-th best of what they
-//            stored as the bound, into regions that hold a whole cell each
-//            (no overflow is possible), so one retry is final.
+//   B scan   all probed cells with that bound, into one region per (query,
+//            cell) plus a spill region per query for what overflows them;
+//            select the k best of the stored survivors. Exact unless the spill
+//            overflowed too.
+//   retry    those queries rerun B with the k-th best of what they stored as
+//            the bound, into regions that hold a whole cell each (no overflow
+//            is possible), so one retry is final.
 //   finalize scan positions -> original row ids.
 // The ranking key and the bound test are the flat index's (kernels.hpp), so a
 // row's key is the same in every pass of a search.
@@ -54,7 +57,8 @@ void hipCheck(hipError_t e, const char* what) {
 constexpr int kTrainIters = 12;            // reference src/IvfIndex.mm:493
 constexpr int kPointsPerCentroid = 256;    // reference src/CoarseQuantizer.mm:116-117
 constexpr size_t kCandBudget = size_t(3) << 30;   // candidate regions per batch
-constexpr int kCapAMax = 4096;             // bound pass: entries stored per query
+constexpr int kBoundRanks = 4;             // bound pass: most cells per query
+constexpr int64_t kHostTableMax = 1 << 17;  // retries of at most this many entries build their table on the host
 
 int64_t roundUp(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
@@ -109,13 +113,14 @@ struct IvfIndex::Impl {
     float xnMax = 0.0f;
     DevBuf dCellSize, dCellPad, dCellStart, dRid, dCellOrder;
     std::vector<float> hCent;
-    std::vector<int> hStart, hRid;
+    std::vector<int> hStart, hRid, hCellOrder;
 
     // per-search workspace
     DevBuf qin, outIds, outVals, qbuf, qh, qnorm, qrm, probe, pos, posOut, cand, cnt;
     DevBuf tauAk, tauAi, tauKk, tauKi, status;
     DevBuf cQ, cQn, cTk, cTi, cIdx, cProbe, cPos;
     IvfWorkTable wt;
+    std::vector<int> hProbe;
 
     int kernMetric() const { return metric == Metric::L2 ? 0 : 1; }
     float emptyValue() const { return metric == Metric::L2 ? INFINITY : -INFINITY; }
@@ -215,12 +220,14 @@ struct IvfIndex::Impl {
         start.resize((size_t)nl + 1);
         hStart.swap(start);
         hRid.swap(rid);
+        hCellOrder.swap(cellOrder);
         built = true;
     }
 
     // One fine-scan pass over the work table wt (built for nq queries).
     void scanPass(int pass, int nq, int ranks, int nprobe, int nreg, int cap, const void* Q, const float* qn,
-                  const float* tk, const int* ti, const int* posb, hipStream_t s) {
+                  const float* tk, const int* ti, const int* posb, hipStream_t s, bool spill = false,
+                  int rowCap = 0) {
         cand.ensure((size_t)nq * nreg * cap * sizeof(uint2));
         cnt.ensure((size_t)nq * nreg * sizeof(int));
         // every region a work item covers gets its count from it; the others
@@ -235,7 +242,7 @@ struct IvfIndex::Impl {
         p.cand = cand.as<uint2>(); p.cnt = cnt.as<int>(); p.cap = cap;
         p.ivf_ent = wt.ent; p.ivf_pos = posb;
         p.ivf_cell_pad = dCellPad.as<int64_t>(); p.ivf_cell_size = dCellSize.as<int>();
-        p.ivf_nprobe = nprobe; p.ivf_nreg = nreg;
+        p.ivf_nprobe = nprobe; p.ivf_nreg = nreg; p.ivf_spill = spill ? 1 : 0; p.ivf_row_cap = rowCap;
         p.ivf_work = wt.work; p.ivf_nwork = wt.nwork;
         launch_scan_ivf(p, kernMetric(), pass, storage, kBN, wt.maxWork(nq, ranks, nlist), s);
         p.ivf_work = wt.workN; p.ivf_nwork = wt.nwork + 1;
@@ -267,7 +274,14 @@ struct IvfIndex::Impl {
     // Region capacities. capA: bound pass, per query; capB: full pass, per
     // (query, probe rank) -- a whole cell when nprobe = 1 (no bound, every row
     // stored); capR: retries, a whole cell.
-    int capA(int k) const { return (int)std::max<int64_t>(k, std::min<int64_t>(roundUp(std::max(maxCell, 1), 64), kCapAMax)); }
+    // Bound pass rows per cell: >= k (so a cell of at least k rows yields a
+    // bound by itself), and few enough that the pass stays a small fraction
+    // of the full one; the full pass then admits ~k * size / sampleRows rows of
+    // the nearest cell.
+    static int sampleRows(int k) { return std::max(4 * k, 1024); }
+    int capA(int k) const {
+        return (int)roundUp(std::max(1, std::min(maxCell, sampleRows(k))), 64);
+    }
     int capR() const { return (int)roundUp(std::max(maxCell, 1), 64); }
     // MFLAT_IVF_CAP_B (diagnostics) overrides capB to exercise the retries;
     // the results never depend on it, only the work done.
@@ -290,12 +304,19 @@ struct IvfIndex::Impl {
         status.ensure((size_t)mb * 4);
         launch_fill_tau_none(tauAk.as<float>(), tauAi.as<int>(), mb, s);
         if (nprobe > 1) {
-            // A: the nearest cell of every query, no bound -> guaranteed bound
+            // A: the first sampleRows(k) rows (ascending id within a cell: a
+            // uniform sample) of each query's nearest cells, no bound, up to the
+            // first cell that brings its scan to k rows (at most kBoundRanks)
+            // -> a guaranteed bound: the k-th best of what was stored
+            const int sr = sampleRows(k);
             const int ca = capA(k);
-            wt.build(probe.as<int>(), mb, nprobe, 1, nlist, dCellOrder.as<int>(), narrowMax(), s);
-            scanPass(kPassSample, mb, 1, nprobe, 1, ca, Q, qn, tauAk.as<float>(), tauAi.as<int>(), pos.as<int>(), s);
-            SelectParams sp = selectParams(mb, 1, ca, k);
+            const int ra = std::min(nprobe, kBoundRanks);
+            wt.build(probe.as<int>(), mb, nprobe, ra, nlist, dCellOrder.as<int>(), narrowMax(), s, pos.as<int>(), k);
+            scanPass(kPassSample, mb, ra, nprobe, ra, ca, Q, qn, tauAk.as<float>(), tauAi.as<int>(), pos.as<int>(), s,
+                     false, sr);
+            SelectParams sp = selectParams(mb, ra, ca, k);
             sp.tau_k_key = tauAk.as<float>(); sp.tau_k_id = tauAi.as<int>();
+            sp.expect = std::min(sr, std::max(maxCell, 1));
             launch_select(sp, s);
         }
         // B: every probed cell under the bound
@@ -305,14 +326,18 @@ struct IvfIndex::Impl {
             posOut.ensure((size_t)mb * k * sizeof(int32_t));
             posIds = posOut.as<int32_t>();
         }
+        // regions: one per (query, probe rank), plus a spill region per query
         wt.build(probe.as<int>(), mb, nprobe, nprobe, nlist, dCellOrder.as<int>(), narrowMax(), s);
-        scanPass(kPassFull, mb, nprobe, nprobe, nprobe, cb, Q, qn, tauAk.as<float>(), tauAi.as<int>(), pos.as<int>(),
-                 s);
+        scanPass(kPassFull, mb, nprobe, nprobe, nprobe + 1, cb, Q, qn, tauAk.as<float>(), tauAi.as<int>(),
+                 pos.as<int>(), s, true);
         {
-            SelectParams sp = selectParams(mb, nprobe, cb, k);
+            SelectParams sp = selectParams(mb, nprobe + 1, cb, k);
             sp.out_ids = posIds; sp.out_vals = oVals;
             sp.tau_k_key = tauKk.as<float>(); sp.tau_k_id = tauKi.as<int>();
             sp.status = status.as<int>();
+            // the bound is the k-th of the nearest cell: survivors ~ a few k
+            // (all rows when nprobe = 1)
+            sp.expect = nprobe > 1 ? 4 * k : std::min(cb, maxCell);
             launch_select(sp, s);
         }
         std::vector<int> st((size_t)mb);
@@ -343,10 +368,19 @@ struct IvfIndex::Impl {
                 launch_gather_i32(tauKi.as<int>(), cIdx.as<int>(), nf, 1, cTi.as<int>(), s);
                 launch_gather_i32(probe.as<int>(), cIdx.as<int>(), nf, nprobe, cProbe.as<int>(), s);
                 launch_gather_i32(pos.as<int>(), cIdx.as<int>(), nf, nprobe, cPos.as<int>(), s);
-                wt.build(cProbe.as<int>(), nf, nprobe, nprobe, nlist, dCellOrder.as<int>(), narrowMax(), s);
+                if ((int64_t)nf * nprobe <= kHostTableMax) {   // few entries: the table on the host
+                    hProbe.resize((size_t)nf * nprobe);
+                    HIPC(hipMemcpyAsync(hProbe.data(), cProbe.p, hProbe.size() * sizeof(int), hipMemcpyDeviceToHost,
+                                        s));
+                    HIPC(hipStreamSynchronize(s));
+                    wt.buildHost(hProbe.data(), nf, nprobe, nlist, hCellOrder.data(), narrowMax(), s);
+                } else {
+                    wt.build(cProbe.as<int>(), nf, nprobe, nprobe, nlist, dCellOrder.as<int>(), narrowMax(), s);
+                }
                 scanPass(kPassFull, nf, nprobe, nprobe, nprobe, cr, cQ.p, cQn.as<float>(), cTk.as<float>(),
                          cTi.as<int>(), cPos.as<int>(), s);
                 SelectParams sp = selectParams(nf, nprobe, cr, k);
+                sp.expect = 4 * k;
                 sp.qmap = cIdx.as<int>();
                 sp.out_ids = posIds; sp.out_vals = oVals;
                 launch_select(sp, s);
@@ -378,7 +412,8 @@ struct IvfIndex::Impl {
             throw BadArg("IVF search: the fine scan holds a 128-query tile in LDS (fp32 dim <= 128, fp16/bf16 dim <= 256)");
         setDevice();
         // batch the queries so the candidate regions stay bounded
-        const size_t perQuery = std::max<size_t>(nprobe > 1 ? (size_t)capA(k) : 0, (size_t)nprobe * capB(k, nprobe)) *
+        const size_t perQuery = std::max<size_t>(nprobe > 1 ? (size_t)std::min(nprobe, kBoundRanks) * capA(k) : 0,
+                                                 (size_t)(nprobe + 1) * capB(k, nprobe)) *
                                 sizeof(uint2);
         int64_t mb = std::max<int64_t>(1, (int64_t)(kCandBudget / perQuery));
         if (mb >= kBN) mb = mb / kBN * kBN;

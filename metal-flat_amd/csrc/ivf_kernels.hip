@@ -74,16 +74,19 @@ __global__ void ivf_positions_kernel(const int* __restrict__ probe, int m, int n
 }
 
 // entries i < m * ranks of the pass: e = (i / ranks) * np + i % ranks. An
-// entry without a cell (probe -1) sorts after every cell and is never scanned.
+// entry without a cell (probe -1), or (pos non-null) whose cell starts at scan
+// position posLimit or later, sorts after every cell and is never scanned.
 __global__ void ivf_entries_kernel(const int* __restrict__ probe, int m, int np, int ranks, int nlist,
-                                   int* __restrict__ keys, int* __restrict__ vals) {
+                                   const int* __restrict__ pos, int posLimit, int* __restrict__ keys,
+                                   int* __restrict__ vals) {
     const int64_t n = (int64_t)m * ranks;
     const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (i >= n) return;
     const int q = (int)(i / ranks);
     const int e = q * np + (int)(i - (int64_t)q * ranks);
     const int c = probe[e];
-    keys[i] = c >= 0 && c < nlist ? c : nlist;
+    const bool ok = c >= 0 && c < nlist && (pos == nullptr || pos[e] < posLimit);
+    keys[i] = ok ? c : nlist;
     vals[i] = e;
 }
 
@@ -243,14 +246,7 @@ void IvfWorkTable::release() {
     capE = capWork = capWorkN = capCells = 0;
 }
 
-void IvfWorkTable::build(const int* probe, int m, int np, int ranks, int nlist, const int* cellOrder,
-                         int narrowMax, hipStream_t s) {
-    const int64_t ne64 = (int64_t)m * ranks;
-    if (m <= 0 || ranks < 1 || ranks > np || nlist < 1) throw std::runtime_error("ivf work table: bad sizes");
-    if (ne64 > 0x7FFFFFFF) throw std::runtime_error("ivf work table: too many entries");
-    const int ne = (int)ne64;
-    const int mw = maxWork(m, ranks, nlist);
-    const int mn = maxWorkNarrow(m, ranks, nlist, narrowMax);
+void IvfWorkTable::reserve(int ne, int mw, int mn, int nlist) {
     if (ne > capE) {
         for (int** p : {&ent, &keysIn, &keysOut, &valsIn}) {
             if (*p) (void)hipFree(*p);
@@ -281,6 +277,19 @@ void IvfWorkTable::build(const int* probe, int m, int np, int ranks, int nlist, 
         capCells = nlist;
     }
     if (!nwork) check(hipMalloc((void**)&nwork, 2 * sizeof(int)), "hipMalloc(nwork)");
+}
+
+void IvfWorkTable::build(const int* probe, int m, int np, int ranks, int nlist, const int* cellOrder,
+                         int narrowMax, hipStream_t s, const int* pos, int posLimit) {
+    const int64_t ne64 = (int64_t)m * ranks;
+    if (m <= 0 || ranks < 1 || ranks > np || nlist < 1) throw std::runtime_error("ivf work table: bad sizes");
+    if (ne64 > 0x7FFFFFFF) throw std::runtime_error("ivf work table: too many entries");
+    const int ne = (int)ne64;
+    const int mw = maxWork(m, ranks, nlist);
+    const int mn = maxWorkNarrow(m, ranks, nlist, narrowMax);
+    reserve(ne, mw, mn, nlist);
+
+
 
     int bits = 1;
     while ((1 << bits) <= nlist) ++bits;   // keys 0 .. nlist
@@ -301,7 +310,8 @@ void IvfWorkTable::build(const int* probe, int m, int np, int ranks, int nlist, 
     prof_begin(kFamPrep, s, &tok);
     check(hipMemsetAsync(eEnd, 0, (size_t)nlist * sizeof(int), s), "hipMemsetAsync(eEnd)");
     check(hipMemsetAsync(eStart, 0, (size_t)nlist * sizeof(int), s), "hipMemsetAsync(eStart)");
-    ivf_entries_kernel<<<(int)((ne + 255) / 256), 256, 0, s>>>(probe, m, np, ranks, nlist, keysIn, valsIn);
+    ivf_entries_kernel<<<(int)((ne + 255) / 256), 256, 0, s>>>(probe, m, np, ranks, nlist, pos, posLimit, keysIn,
+                                                                valsIn);
     check(hipGetLastError(), "ivf_entries");
     size_t t = tempBytes;
     check(hipcub::DeviceRadixSort::SortPairs(temp, t, (const int*)keysIn, keysOut, (const int*)valsIn, ent, ne, 0,
@@ -319,6 +329,58 @@ void IvfWorkTable::build(const int* probe, int m, int np, int ranks, int nlist, 
                                                          workN, nwork);
     check(hipGetLastError(), "ivf_work");
     prof_end(tok, s);
+}
+
+void IvfWorkTable::buildHost(const int* probe, int m, int np, int nlist, const int* cellOrder, int narrowMax,
+                             hipStream_t s) {
+    const int64_t ne64 = (int64_t)m * np;
+    if (m <= 0 || np < 1 || nlist < 1 || ne64 > 0x7FFFFFFF) throw std::runtime_error("ivf work table: bad sizes");
+    const int ne = (int)ne64;
+    const int mw = maxWork(m, np, nlist);
+    const int mn = maxWorkNarrow(m, np, nlist, narrowMax);
+    reserve(ne, mw, mn, nlist);
+    // counting sort of the entries by cell, ascending entry within a cell
+    hCnt.assign((size_t)nlist + 1, 0);
+    for (int e = 0; e < ne; ++e)
+        if (probe[e] >= 0 && probe[e] < nlist) ++hCnt[(size_t)probe[e] + 1];
+    hStart.assign((size_t)nlist + 1, 0);
+    for (int c = 0; c < nlist; ++c) hStart[(size_t)c + 1] = hStart[(size_t)c] + hCnt[(size_t)c + 1];
+    hEnt.assign((size_t)std::max(ne, 1), 0);
+    std::vector<int> cur(hStart.begin(), hStart.end() - 1);
+    for (int e = 0; e < ne; ++e)
+        if (probe[e] >= 0 && probe[e] < nlist) hEnt[(size_t)cur[(size_t)probe[e]]++] = e;
+    hWork.clear();
+    hWorkN.clear();
+    for (int i = 0; i < nlist; ++i) {
+        const int c = cellOrder[i];
+        const int e0 = hStart[(size_t)c], cnt = hCnt[(size_t)c + 1];
+        int wide, narrow;
+        if (narrowMax < 0) {
+            wide = 0;
+            narrow = (cnt + kIvfNarrow - 1) / kIvfNarrow;
+        } else {
+            wide = cnt / kBN;
+            const int rem = cnt - wide * kBN;
+            if (rem > narrowMax) { ++wide; narrow = 0; }
+            else narrow = (rem + kIvfNarrow - 1) / kIvfNarrow;
+        }
+        for (int t = 0; t < wide; ++t) hWork.push_back(make_int4(c, e0 + t * kBN, std::min(kBN, cnt - t * kBN), 0));
+        const int base = wide * kBN;
+        for (int t = 0; t < narrow; ++t)
+            hWorkN.push_back(make_int4(c, e0 + base + t * kIvfNarrow, std::min(kIvfNarrow, cnt - base - t * kIvfNarrow), 0));
+    }
+    if ((int)hWork.size() > mw || (int)hWorkN.size() > mn) throw std::runtime_error("ivf work table: bound exceeded");
+    const int counts[2] = {(int)hWork.size(), (int)hWorkN.size()};
+    check(hipMemcpyAsync(ent, hEnt.data(), (size_t)ne * sizeof(int), hipMemcpyHostToDevice, s), "hipMemcpyAsync(ent)");
+    if (counts[0])
+        check(hipMemcpyAsync(work, hWork.data(), hWork.size() * sizeof(int4), hipMemcpyHostToDevice, s),
+              "hipMemcpyAsync(work)");
+    if (counts[1])
+        check(hipMemcpyAsync(workN, hWorkN.data(), hWorkN.size() * sizeof(int4), hipMemcpyHostToDevice, s),
+              "hipMemcpyAsync(work)");
+    check(hipMemcpyAsync(nwork, counts, sizeof counts, hipMemcpyHostToDevice, s), "hipMemcpyAsync(nwork)");
+    // the host vectors are the copies' sources: wait before they can change
+    check(hipStreamSynchronize(s), "hipStreamSynchronize");
 }
 
 }  // namespace mflat_amd

@@ -6,6 +6,7 @@
 
 #include <hip/hip_runtime.h>
 #include <cstdint>
+#include <vector>
 
 namespace mflat_amd {
 
@@ -45,8 +46,14 @@ struct IvfWorkTable {
     int* nwork = nullptr;
     int maxWork(int m, int ranks, int nlist) const;
     int maxWorkNarrow(int m, int ranks, int nlist, int narrowMax) const;
+    // pos (nullable): scan positions (launch_ivf_positions); entries whose
+    // cell starts at posLimit or later are left out.
     void build(const int* probe, int m, int np, int ranks, int nlist, const int* cellOrder, int narrowMax,
-               hipStream_t s);
+               hipStream_t s, const int* pos = nullptr, int posLimit = 0);
+    // The same table built on the host from host probes (m x np, all ranks)
+    // and a host cell order, then uploaded: for the few queries of a retry,
+    // where the device sort's fixed cost dominates.
+    void buildHost(const int* probe, int m, int np, int nlist, const int* cellOrder, int narrowMax, hipStream_t s);
     ~IvfWorkTable();
     void release();
 
@@ -62,6 +69,9 @@ private:
     int* tEndN = nullptr;
     void* temp = nullptr;
     size_t tempBytes = 0;
+    std::vector<int> hEnt, hCnt, hStart;
+    std::vector<int4> hWork, hWorkN;
+    void reserve(int ne, int mw, int mn, int nlist);
     int capE = 0, capWork = 0, capWorkN = 0, capCells = 0;
 };
 

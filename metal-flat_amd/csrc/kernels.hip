@@ -818,6 +818,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
         rowBeg = p.ivf_cell_pad[wk.x];
         rowOrg = 0;
         rowLim = p.ivf_cell_size[wk.x];
+        if (p.ivf_row_cap > 0 && rowLim > p.ivf_row_cap) rowLim = p.ivf_row_cap;   // a cell's first rows only
         nsl = (int)((rowLim + 63) / 64);
     } else {
         const int64_t rows_pad = (p.nrows + kBM - 1) / kBM * kBM;
@@ -832,6 +833,21 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     auto region = [&](int ql) -> int64_t {
         if constexpr (IVF) return sReg[ql];
         return ((int64_t)qb * kBN + ql) * p.nsplit + split;
+    };
+    // Survivor of slot ql at its region's slot `slot`. IVF with a spill region
+    // (region nprobe of each query, filled by global atomics on its count): the
+    // survivors beyond a region's capacity go there, so one crowded cell does
+    // not force a retry; the spill's count past cap still flags the overflow.
+    auto store = [&](int ql, int slot, uint2 v) {
+        if (slot < p.cap) {
+            p.cand[region(ql) * p.cap + slot] = v;
+        } else if constexpr (IVF) {
+            if (p.ivf_spill) {
+                const int64_t sr = (int64_t)sQi[ql] * p.ivf_nreg + p.ivf_nprobe;
+                const int sp = atomicAdd(&p.cnt[sr], 1);
+                if (sp < p.cap) p.cand[sr * p.cap + sp] = v;
+            }
+        }
     };
     const int nchunk = p.dpad / 32;
     const int64_t blkB = (int64_t)32 * p.dpad * ES;
@@ -903,9 +919,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
                             sRingId[wave * kRing + pos] = id;
                             sRingQ[wave * kRing + pos] = ql;
                         } else {   // ring full (or not used): store directly
-                            const int slot = atomicAdd(&sCnt[ql], 1);
-                            if (slot < p.cap)
-                                p.cand[region(ql) * p.cap + slot] = make_uint2(__float_as_uint(key), (unsigned)id);
+                            store(ql, atomicAdd(&sCnt[ql], 1), make_uint2(__float_as_uint(key), (unsigned)id));
                         }
                     });
             }
@@ -926,10 +940,8 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
             if (n < atLeast) return;
             for (int e = lane; e < n; e += 64) {
                 const int ql = sRingQ[wave * kRing + e];
-                const int slot = atomicAdd(&sCnt[ql], 1);
-                if (slot < p.cap)
-                    p.cand[region(ql) * p.cap + slot] =
-                        make_uint2(sRingKey[wave * kRing + e], (unsigned)sRingId[wave * kRing + e]);
+                store(ql, atomicAdd(&sCnt[ql], 1),
+                      make_uint2(sRingKey[wave * kRing + e], (unsigned)sRingId[wave * kRing + e]));
             }
             __builtin_amdgcn_wave_barrier();
             if (lane == 0) sRingN[wave] = 0;
@@ -1016,7 +1028,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     }
     __syncthreads();
     if constexpr (IVF) {
-        if (tid < wk.z) p.cnt[sReg[tid]] = sCnt[tid];
+        if (tid < wk.z) p.cnt[sReg[tid]] = p.ivf_spill && sCnt[tid] > p.cap ? p.cap : sCnt[tid];
     } else if (tid < TQ) {
         const int q = qb * kBN + tid;
         if (q < p.nq) p.cnt[(int64_t)q * p.nsplit + split] = sCnt[tid];
@@ -1250,8 +1262,9 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
 // One workgroup (256 threads) per query. The (key, id) composites are distinct
 // (an id appears at most once per query), so the k-th smallest composite T is
 // unique and the winners are exactly the composites <= T.
+template <int NBUF>
 __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
-    __shared__ uint64_t sBuf[kSelLds];
+    __shared__ uint64_t sBuf[NBUF];
     __shared__ uint64_t sTop[kTopMax];
     extern __shared__ int sOff[];   // nsplit + 1 entries (dynamic)
     __shared__ unsigned sHist[256];
@@ -1303,7 +1316,7 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
     if (tid == 0) sOff[0] = 0;
     const bool ovf = __syncthreads_or(ovfLocal);
     const int c = sWave[0] + sWave[1] + sWave[2] + sWave[3];
-    const bool inLds = c <= kSelLds;
+    const bool inLds = c <= NBUF;
 
     // flat index -> candidate (binary search over the split offsets)
     auto fetch = [&](int e) -> uint64_t {
@@ -1944,15 +1957,22 @@ void launch_select(const SelectParams& p, hipStream_t s) {
     // the split offsets (dynamic LDS) reach (kMaxSplit + 1) ints, above the
     // default dynamic-LDS limit of a launch
     static const bool attr = [] {
-        if (hipFuncSetAttribute((const void*)select_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)((kMaxSplit + 1) * sizeof(int))) != hipSuccess)
-            throw std::runtime_error("select: cannot raise the dynamic LDS limit");
+        for (const void* f : {(const void*)select_kernel<kSelLds>, (const void*)select_kernel<kSelLdsSmall>})
+            if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)((kMaxSplit + 1) * sizeof(int))) != hipSuccess)
+                throw std::runtime_error("select: cannot raise the dynamic LDS limit");
         return true;
     }();
     (void)attr;
     void* tok;
     prof_begin(kFamSelect, s, &tok);
-    select_kernel<<<p.nq, 256, (size_t)(p.nsplit + 1) * sizeof(int), s>>>(p);
+    // A query's candidates are staged in LDS when they fit (else read from
+    // global memory on every pass): the small buffer runs ~2.5x more blocks per
+    // CU, for searches that expect few candidates per query.
+    if (p.expect > 0 && p.expect <= kSelLdsSmall)
+        select_kernel<kSelLdsSmall><<<p.nq, 256, (size_t)(p.nsplit + 1) * sizeof(int), s>>>(p);
+    else
+        select_kernel<kSelLds><<<p.nq, 256, (size_t)(p.nsplit + 1) * sizeof(int), s>>>(p);
     prof_end(tok, s);
     check_launch("select");
 }

@@ -43,6 +43,7 @@ constexpr int kBM = 128;   // database rows per scan tile
 constexpr int kBN = 128;   // queries per scan tile
 constexpr int kBK = 32;    // dpad granularity; fp32 columns per LDS-staged chunk
 constexpr int kSelLds = 4096;   // candidates a select block holds in LDS
+constexpr int kSelLdsSmall = 1024;   // ... in its small-buffer variant (SelectParams::expect)
 constexpr int kTopMax = 1024;   // largest k (== MFLAT_MAX_K)
 constexpr int kMaxSplit = 16384;  // most database splits one select block indexes
 constexpr int kSmallMaxQ = 64;                 // scan_small serves batches up to this size
@@ -107,7 +108,9 @@ struct ScanParams {
     const int64_t* ivf_cell_pad;   // first database row of each cell (a multiple of kBM)
     const int* ivf_cell_size;  // rows of each cell
     int ivf_nprobe;
-    int ivf_nreg;              // candidate regions per query (1 or ivf_nprobe): query * nreg + rank
+    int ivf_nreg;              // candidate regions per query: query * nreg + rank (1, nprobe or nprobe + 1)
+    int ivf_spill;             // 1: region nprobe of each query takes what overflows the others (nreg = nprobe + 1)
+    int ivf_row_cap;           // > 0: scan only the first ivf_row_cap rows of each cell
 };
 
 struct SelectParams {
@@ -131,6 +134,8 @@ struct SelectParams {
     float* tau_k_key;        // nullable: k-th smallest (key, id), or "no bound"
     int* tau_k_id;
     int* status;             // nullable: bit0 = a region overflowed, bit1 = fewer than k stored
+    int expect;              // expected stored candidates per query (0: unknown); <= kSelLdsSmall picks the
+                             // small-buffer variant
 };
 
 // Launchers (kernels.hip). All are asynchronous on `s` and bracket the launch
