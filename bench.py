@@ -55,6 +55,8 @@ MEASURED_TRAFFIC_BYTES = {
     ("C4", 1, "f16"): 1.960e9,
     ("C4", 64, "f16"): 1.972e9,
     ("C5", 2_000_000, "f32"): 34.27e9,
+    # IVF fine scan (both launches of a search), C2's data, nlist 1000, nprobe 62
+    ("IVF", 1000, 62, "f32"): 4.66e9,
 }
 
 WORKLOADS = {
@@ -162,9 +164,9 @@ def ivf_bench(args):
     nprobe = max(1, nlist / 16)) unless given, k = C2's 100. A step is one search
     of the whole query batch (device pointers, inputs resident in HBM); the build
     (k-means + cell-major layout) is timed once, apart. roofline: the fine-scan
-    launches (scan_filter family: the bounded pass over every probed cell and its
-    retries) against the fp32 MFMA peak, with algorithmic FLOP = 2 d x the rows of
-    every query's probed cells. cpu_baseline: the oracle's searchCpu restatement
+    launches (ivf_scan family: the bounded pass over every probed cell, in
+    128- and 32-query work items, and its retries) against the fp32 MFMA peak,
+    with algorithmic FLOP = 2 d x the rows of every query's probed cells. cpu_baseline: the oracle's searchCpu restatement
     over the same probed cells on a bounded query prefix."""
     import numpy as np
     import datagen
@@ -209,7 +211,7 @@ def ivf_bench(args):
     elapsed = time.perf_counter() - t0
     mflat.profile_enable(False)
     kern = {}
-    for fam in ("scan_filter", "scan_sample", "select", "norms", "prep"):
+    for fam in ("ivf_scan", "ivf_bound", "scan_filter", "scan_sample", "select", "norms", "prep"):
         ms, n = mflat.profile_read(fam)
         if n:
             kern[fam] = {"total_ms": round(ms, 4), "launches": n, "mean_ms": round(ms / n, 4)}
@@ -217,7 +219,7 @@ def ivf_bench(args):
     log(f"[bench] ivf {args.steps} steps in {elapsed:.3f}s")
 
     peak = PEAK_FP32_MFMA_TFLOPS if storage == mflat.MFLAT_STORAGE_F32 else PEAK_F16_MFMA_TFLOPS
-    ach = flop * args.steps / (kern["scan_filter"]["total_ms"] / 1000.0) / 1e12
+    ach = flop * args.steps / (kern["ivf_scan"]["total_ms"] / 1000.0) / 1e12
     flat = mflat.FlatIndex(d, mflat.MFLAT_METRIC_L2)
     flat.add(x)
     fi, _, _ = flat.search(q, k)
@@ -241,7 +243,8 @@ def ivf_bench(args):
                                f"nlist={nlist}, nprobe={nprobe}, k={k}", "nb": nb, "d": d, "nq": nq, "k": k,
                    "nlist": nlist, "nprobe": nprobe, "storage": args.storage, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(ach / peak, 4), "traffic": None},
+                     "frac": round(ach / peak, 4),
+                     "traffic": MEASURED_TRAFFIC_BYTES.get(("IVF", nlist, nprobe, args.storage)) if nq == 10_000 else None},
         "kernels": kern,
         "probed_rows_per_query": round(rows / nq, 1),
         "recall_vs_exact_flat": round(recall, 5),

@@ -241,7 +241,10 @@ MFLAT_API mflat_status_t mflat_ivf_coarse(const mflat_ivf_index_t*, float* out_c
    over the row sample that sets the thresholds), "scan_retry" (the same
    kernel re-run for the few queries whose threshold must be refined),
    "select" (per-query top-k select / merge), "argmin" (fused k = 1),
-   "norms", "prep". Returns 0 and fills the outputs, or -1 for an unknown name. */
+   "norms", "prep", "ivf_scan" (IVF fine scan over every probed cell under
+   the bound, and its retries), "ivf_bound" (the IVF bound pass over a row
+   sample of each query's nearest cells). Returns 0 and fills the outputs, or
+   -1 for an unknown name. */
 MFLAT_API void mflat_profile_enable(int on);
 MFLAT_API void mflat_profile_reset(void);
 MFLAT_API int  mflat_profile_read(const char* name, double* total_ms, long long* launches);

@@ -1920,7 +1920,7 @@ void launch_scan_ivf(const ScanParams& p, int metric, int pass, int storage, int
         p.ivf_nreg < 1)
         throw std::runtime_error("scan_ivf: bad parameters");
     void* tok;
-    prof_begin(pass == kPassSample ? kFamScanSample : kFamScan, s, &tok);
+    prof_begin(pass == kPassSample ? kFamIvfBound : kFamIvfScan, s, &tok);
     const size_t lds = resident_lds_bytes(p.dpad, storage, tileQueries);
     const int nb = tileQueries / 32;
     if (storage == kF32) launch_ivf_s<kF32>(p, metric, pass, nb, grid, lds, s);

@@ -58,7 +58,7 @@ inline int elem_bytes(int storage) { return storage == kF32 ? 4 : 2; }
 
 enum KernelFamily {
     kFamScan = 0, kFamScanSample = 1, kFamScanRetry = 2, kFamSelect = 3, kFamArgmin = 4,
-    kFamNorms = 5, kFamPrep = 6, kFamCount = 7
+    kFamNorms = 5, kFamPrep = 6, kFamIvfScan = 7, kFamIvfBound = 8, kFamCount = 9
 };
 // kPassArgmin: k = 1; each query's best (key, id) goes to ScanParams::best
 // (packed ordered key << 32 | id, combined with 64-bit atomicMin) instead of

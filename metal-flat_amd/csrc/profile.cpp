@@ -73,7 +73,8 @@ void prof_reset() {
 }
 
 int prof_read(const char* name, double* ms, long long* n) {
-    static const char* kNames[kFamCount] = {"scan_filter", "scan_sample", "scan_retry", "select", "argmin", "norms", "prep"};
+    static const char* kNames[kFamCount] = {"scan_filter", "scan_sample", "scan_retry", "select", "argmin",
+                                            "norms",       "prep",        "ivf_scan",   "ivf_bound"};
     int fam = -1;
     for (int i = 0; i < kFamCount; ++i)
         if (name && std::strcmp(name, kNames[i]) == 0) fam = i;

@@ -152,7 +152,8 @@ def test_no_device_is_not_ready():
 
 def test_profile_names():
     mflat.profile_reset()
-    for name in ("scan_filter", "scan_sample", "scan_retry", "select", "argmin", "norms", "prep"):
+    for name in ("scan_filter", "scan_sample", "scan_retry", "select", "argmin", "norms", "prep", "ivf_scan",
+                 "ivf_bound"):
         ms, n = mflat.profile_read(name)
         assert ms == 0.0 and n == 0
     with pytest.raises(KeyError):
