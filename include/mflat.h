@@ -23,8 +23,12 @@
  *    with the same argument checks and result layout; IVF search serves
  *    k <= MFLAT_MAX_K and nprobe <= MFLAT_MAX_K on the device (the reference
  *    serves k > 64 on its CPU path, src/IvfIndex.mm:762-764), and the fine
- *    scan needs dim <= 128 (fp32) or <= 256 (fp16 / bf16 storage). The IVF-PQ
- *    entry points (c/include/mflat.h:107-129) are not part of this library.
+ *    scan needs dim <= 128 (fp32) or <= 256 (fp16 / bf16 storage).
+ *  - The IVF-PQ entry points (reference c/include/mflat.h:107-129) are here with
+ *    the reference C ABI's behaviour: residual PQ, no OPQ (the reference's C
+ *    ABI reaches neither of its setResidual / setOpq switches); k up to
+ *    MFLAT_MAX_K (reference 64), rerank shortlists up to MFLAT_MAX_K rows, and
+ *    m_sub <= 128.
  *  - Additive entry points (reduced-precision storage, device-pointer
  *    search/add, kernel timing) follow the flat block; they have no
  *    counterpart in the reference.
@@ -140,6 +144,43 @@ MFLAT_API mflat_status_t mflat_ivf_build(mflat_ivf_index_t*, const float* vector
 MFLAT_API mflat_status_t mflat_ivf_search(mflat_ivf_index_t*, const float* queries,
         int m, int k, int nprobe, int32_t* out_ids, float* out_distances, int* out_k_used);
 
+/* ---------------- IvfPqIndex (compressed) ---------------------------------- */
+/* reference c/include/mflat.h:107-129, c/mflat.cpp:161-198, src/IvfPqIndex.mm.
+   build() trains the coarse cells as mflat_ivf_build, then product-quantizes
+   every row's residual to its cell centroid: m_sub sub-vectors of dim / m_sub
+   columns, each replaced by the byte id of its nearest of 256 sub-centroids
+   (k-means per sub-space, 12 iterations over all rows). search() ranks the
+   rows of each query's nprobe nearest cells by the asymmetric distance
+   ||q - c||^2 + sum_m (||p_m||^2 - 2 q_m . p_m + 2 c_m . p_m) (p_m the row's
+   sub-centroids), ties in scan order, and reports that value (an
+   approximate squared distance, for L2 and Cosine alike). With rerank > k on
+   an index built after mflat_ivfpq_set_rerank(h, 1), the top-rerank of that
+   ranking is re-ranked by exact distance (values: squared L2, or the dot for
+   Cosine), ties in shortlist order. Metric must be L2 or Cosine. */
+typedef struct mflat_ivfpq_index mflat_ivfpq_index_t;  /* opaque */
+
+/* reference c/mflat.cpp:162-170: dim, nlist, m_sub <= 0, dim % m_sub != 0 or
+   INNER_PRODUCT -> NULL + BAD_ARG (also m_sub > 128 here) */
+MFLAT_API mflat_ivfpq_index_t*
+mflat_ivfpq_create(int dim, mflat_metric_t metric, int nlist, int m_sub, mflat_status_t* out_status);
+MFLAT_API void mflat_ivfpq_free(mflat_ivfpq_index_t*);
+/* keep the full rows for exact reranking; takes effect at the next build */
+MFLAT_API void mflat_ivfpq_set_rerank(mflat_ivfpq_index_t*, int enable);
+
+MFLAT_API int mflat_ivfpq_ready(const mflat_ivfpq_index_t*);  /* 1 after build() */
+MFLAT_API int mflat_ivfpq_size (const mflat_ivfpq_index_t*);
+MFLAT_API int mflat_ivfpq_dim  (const mflat_ivfpq_index_t*);
+MFLAT_API int mflat_ivfpq_nlist(const mflat_ivfpq_index_t*);
+MFLAT_API int mflat_ivfpq_subquantizers(const mflat_ivfpq_index_t*);  /* bytes per code */
+
+/* reference c/mflat.cpp:182-188 */
+MFLAT_API mflat_status_t mflat_ivfpq_build(mflat_ivfpq_index_t*, const float* vectors, int n);
+/* reference c/mflat.cpp:189-198: rerank < 0 -> BAD_ARG besides the IVF checks;
+   rerank 0 or 1 (or <= k) = off. */
+MFLAT_API mflat_status_t mflat_ivfpq_search(mflat_ivfpq_index_t*, const float* queries,
+        int m, int k, int nprobe, int rerank,
+        int32_t* out_ids, float* out_distances, int* out_k_used);
+
 /* ---------------- Additive: reduced-precision storage --------------------- */
 /* No counterpart in the reference (its FlatIndex stores fp32 only,
    src/FlatIndex.mm:236-245). The index holds its database, and each search
@@ -231,6 +272,20 @@ MFLAT_API mflat_status_t mflat_ivf_probe(mflat_ivf_index_t*, const float* querie
         int32_t* out_cells);
 MFLAT_API mflat_status_t mflat_ivf_coarse(const mflat_ivf_index_t*, float* out_centroids,
         int32_t* out_cell_start, int32_t* out_reordered_ids);
+
+/* ---------------- Additive: IVF-PQ extensions ----------------------------- */
+/* No C counterpart in the reference. mflat_ivfpq_search_device: as
+   mflat_ivfpq_search on device pointers. mflat_ivfpq_probe: the coarse stage
+   alone (as mflat_ivf_probe). mflat_ivfpq_coarse: after build, the coarse
+   layer (as mflat_ivf_coarse) and the codebook: out_pq_centroids m_sub x 256 x
+   (dim / m_sub) floats, out_codes size() x m_sub bytes in cell order (the row
+   slot of out_reordered_ids); each nullable. */
+MFLAT_API mflat_status_t mflat_ivfpq_search_device(mflat_ivfpq_index_t*, const float* d_queries, int m, int k,
+        int nprobe, int rerank, int32_t* d_out_ids, float* d_out_distances, int* out_k_used, void* stream);
+MFLAT_API mflat_status_t mflat_ivfpq_probe(mflat_ivfpq_index_t*, const float* queries, int m, int nprobe,
+        int32_t* out_cells);
+MFLAT_API mflat_status_t mflat_ivfpq_coarse(const mflat_ivfpq_index_t*, float* out_centroids,
+        int32_t* out_cell_start, int32_t* out_reordered_ids, float* out_pq_centroids, uint8_t* out_codes);
 
 /* ---------------- Additive: kernel timing -------------------------------- */
 /* No counterpart in the reference. When enabled, every launch of the library's

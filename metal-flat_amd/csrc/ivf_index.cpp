@@ -43,6 +43,7 @@
 #include "kernels.hpp"
 #include "kmeans.hpp"
 #include "log.hpp"
+#include "pq_kernels.hpp"
 
 namespace mflat_amd {
 namespace {
@@ -58,6 +59,7 @@ constexpr int kTrainIters = 12;            // reference src/IvfIndex.mm:493
 constexpr int kPointsPerCentroid = 256;    // reference src/CoarseQuantizer.mm:116-117
 constexpr size_t kCandBudget = size_t(3) << 30;   // candidate regions per batch
 constexpr int kBoundRanks = 4;             // bound pass: most cells per query
+constexpr int kMaxSubquantizers = 128;     // PQ: M x 256 floats of one query's table fit LDS
 constexpr int64_t kHostTableMax = 1 << 17;  // retries of at most this many entries build their table on the host
 
 int64_t roundUp(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
@@ -108,6 +110,14 @@ struct IvfIndex::Impl {
     int device = -1;
     hipStream_t stream = nullptr;
 
+    // IVF-PQ (pqM > 0): residual product quantization instead of stored rows
+    int pqM = 0, dsub = 0;
+    bool rerankReq = false;    // keep the full rows for exact reranking (set before build)
+    bool fullStored = false;   // ... latched at build
+    DevBuf dCodes, dPqc, dNorms, dT, dCentD, dFull;
+    std::vector<float> hPqc;
+    bool pq() const { return pqM > 0; }
+
     std::unique_ptr<FlatIndex> coarse;
     DevBuf X, xn, maxBits;
     float xnMax = 0.0f;
@@ -119,6 +129,7 @@ struct IvfIndex::Impl {
     DevBuf qin, outIds, outVals, qbuf, qh, qnorm, qrm, probe, pos, posOut, cand, cnt;
     DevBuf tauAk, tauAi, tauKk, tauKi, status;
     DevBuf cQ, cQn, cTk, cTi, cIdx, cProbe, cPos;
+    DevBuf lut, base, cLut, cBase, shortIds, rrCand, rrCnt, rrSel;
     IvfWorkTable wt;
     std::vector<int> hProbe;
 
@@ -179,22 +190,24 @@ struct IvfIndex::Impl {
                          [&](int a, int b) { return size[(size_t)a] > size[(size_t)b]; });
 
         DevBuf slot, tmp;
-        slot.ensure((size_t)P * sizeof(int));
-        tmp.ensure((size_t)P * rowB);
-        HIPC(hipMemcpyAsync(slot.p, slotSrc.data(), (size_t)P * sizeof(int), hipMemcpyHostToDevice, s));
-        launch_gather_rows_or_zero(data.as<float>(), slot.as<int>(), P, dim, tmp.as<float>(), s);
+        float xm = 0.0f;
         X.release();
         xn.release();
-        X.ensure((size_t)P * dpad * esize);
-        xn.ensure((size_t)P * sizeof(float));
-        HIPC(hipMemsetAsync(X.p, 0, (size_t)P * dpad * esize, s));
-        launch_store_rows_blk(tmp.as<float>(), P, dim, nullptr, X.p, 0, dpad, storage, s);
-        launch_row_norms_blk(X.p, 0, P, dpad, storage, xn.as<float>(), s);
-        maxBits.ensure(sizeof(unsigned));
-        HIPC(hipMemsetAsync(maxBits.p, 0, sizeof(unsigned), s));
-        launch_max_norm(xn.as<float>(), P, maxBits.as<unsigned>(), s);
-        float xm = 0.0f;
-        HIPC(hipMemcpyAsync(&xm, maxBits.p, sizeof(float), hipMemcpyDeviceToHost, s));
+        if (!pq()) {
+            slot.ensure((size_t)P * sizeof(int));
+            tmp.ensure((size_t)P * rowB);
+            HIPC(hipMemcpyAsync(slot.p, slotSrc.data(), (size_t)P * sizeof(int), hipMemcpyHostToDevice, s));
+            launch_gather_rows_or_zero(data.as<float>(), slot.as<int>(), P, dim, tmp.as<float>(), s);
+            X.ensure((size_t)P * dpad * esize);
+            xn.ensure((size_t)P * sizeof(float));
+            HIPC(hipMemsetAsync(X.p, 0, (size_t)P * dpad * esize, s));
+            launch_store_rows_blk(tmp.as<float>(), P, dim, nullptr, X.p, 0, dpad, storage, s);
+            launch_row_norms_blk(X.p, 0, P, dpad, storage, xn.as<float>(), s);
+            maxBits.ensure(sizeof(unsigned));
+            HIPC(hipMemsetAsync(maxBits.p, 0, sizeof(unsigned), s));
+            launch_max_norm(xn.as<float>(), P, maxBits.as<unsigned>(), s);
+            HIPC(hipMemcpyAsync(&xm, maxBits.p, sizeof(float), hipMemcpyDeviceToHost, s));
+        }
 
         dCellSize.ensure((size_t)nl * sizeof(int));
         dCellPad.ensure((size_t)nl * sizeof(int64_t));
@@ -206,6 +219,8 @@ struct IvfIndex::Impl {
         HIPC(hipMemcpyAsync(dCellStart.p, start.data(), ((size_t)nl + 1) * sizeof(int), hipMemcpyHostToDevice, s));
         HIPC(hipMemcpyAsync(dRid.p, order.p, (size_t)nrows * sizeof(int), hipMemcpyDeviceToDevice, s));
         HIPC(hipMemcpyAsync(dCellOrder.p, cellOrder.data(), (size_t)nl * sizeof(int), hipMemcpyHostToDevice, s));
+
+        if (pq()) buildPq(data.as<float>(), cent.as<float>(), nrows, nl, s);
 
         coarse.reset(new FlatIndex(dim, Metric::L2, kF32));
         coarse->addDevice(cent.as<float>(), nl, s);
@@ -224,15 +239,79 @@ struct IvfIndex::Impl {
         built = true;
     }
 
+    // Residual product quantization of the rows (reference src/IvfPqIndex.mm:
+    // 286-327, src/PqTrainer.h:37-66): per sub-space, k-means of the residuals
+    // x - c (12 iterations, 256 cells, every row trains, seeds wrapping when
+    // fewer rows than cells); the codes are the final assignments, stored in
+    // cell order; the per-cell cross table T and the sub-centroid norms follow.
+    // data: the (Cosine-normalised) rows; the CSR arrays are on the device.
+    void buildPq(const float* data, const float* cent, int nrows, int nl, hipStream_t s) {
+        const size_t rowB = (size_t)dim * sizeof(float);
+        fullStored = rerankReq;
+        dFull.release();
+        if (fullStored) {   // exact rerank rows, original order, before the residual subtraction
+            dFull.ensure((size_t)nrows * rowB);
+            HIPC(hipMemcpyAsync(dFull.p, data, (size_t)nrows * rowB, hipMemcpyDeviceToDevice, s));
+        }
+        DevBuf assign, r, sub, subAssign;
+        assign.ensure((size_t)nrows * sizeof(int));
+        r.ensure((size_t)nrows * rowB);
+        launch_cell_assign(dCellStart.as<int>(), dRid.as<int>(), nl, assign.as<int>(), s);
+        launch_residuals(data, cent, assign.as<int>(), nrows, dim, r.as<float>(), s);
+        dPqc.ensure((size_t)pqM * kPqKsub * dsub * sizeof(float));
+        dNorms.ensure((size_t)pqM * kPqKsub * sizeof(float));
+        dCodes.ensure((size_t)nrows * pqM);
+        sub.ensure((size_t)nrows * dsub * sizeof(float));
+        subAssign.ensure((size_t)nrows * sizeof(int));
+        for (int mm = 0; mm < pqM; ++mm) {
+            launch_subspace(r.as<float>(), nrows, dim, mm * dsub, dsub, sub.as<float>(), s);
+            kmeansTrainDevice(sub.as<float>(), nrows, dsub, kPqKsub, kTrainIters, 0,
+                              dPqc.as<float>() + (size_t)mm * kPqKsub * dsub, subAssign.as<int>(), nullptr, nullptr,
+                              s, true);
+            launch_pq_codes(subAssign.as<int>(), dRid.as<int>(), nrows, pqM, mm, dCodes.as<uint8_t>(), s);
+        }
+        launch_pq_norms(dPqc.as<float>(), pqM, dsub, dNorms.as<float>(), s);
+        dT.ensure((size_t)nl * pqM * kPqKsub * sizeof(float));
+        launch_pq_cell_table(cent, nl, dim, dPqc.as<float>(), pqM, dsub, dT.as<float>(), s);
+        dCentD.ensure((size_t)nl * rowB);
+        HIPC(hipMemcpyAsync(dCentD.p, cent, (size_t)nl * rowB, hipMemcpyDeviceToDevice, s));
+        hPqc.resize((size_t)pqM * kPqKsub * dsub);
+        HIPC(hipMemcpyAsync(hPqc.data(), dPqc.p, hPqc.size() * sizeof(float), hipMemcpyDeviceToHost, s));
+        HIPC(hipStreamSynchronize(s));
+    }
+
     // One fine-scan pass over the work table wt (built for nq queries).
-    void scanPass(int pass, int nq, int ranks, int nprobe, int nreg, int cap, const void* Q, const float* qn,
-                  const float* tk, const int* ti, const int* posb, hipStream_t s, bool spill = false,
-                  int rowCap = 0) {
+    // The queries of a pass: storage-type rows and norms (flat rows), or the
+    // lookup tables and per-entry coarse terms (PQ).
+    struct QueryRefs {
+        const void* Q;
+        const float* qn;
+        const float* lut;
+        const float* base;
+    };
+
+    void scanPass(int pass, int nq, int ranks, int nprobe, int nreg, int cap, const QueryRefs& qr, const float* tk,
+                  const int* ti, const int* posb, hipStream_t s, bool spill = false, int rowCap = 0) {
         cand.ensure((size_t)nq * nreg * cap * sizeof(uint2));
         cnt.ensure((size_t)nq * nreg * sizeof(int));
         // every region a work item covers gets its count from it; the others
         // (entries without a cell) stay empty
         HIPC(hipMemsetAsync(cnt.p, 0, (size_t)nq * nreg * sizeof(int), s));
+        if (pq()) {
+            AdcParams a;
+            std::memset(&a, 0, sizeof a);
+            a.codes = dCodes.as<uint8_t>(); a.cellStart = dCellStart.as<int>();
+            a.lut = qr.lut; a.T = dT.as<float>(); a.base = qr.base;
+            a.work = wt.work; a.nwork = wt.nwork; a.ent = wt.ent; a.pos = posb;
+            a.tau_key = tk; a.tau_id = ti;
+            a.cand = cand.as<uint2>(); a.cnt = cnt.as<int>(); a.cap = cap;
+            a.M = pqM; a.nprobe = nprobe; a.nreg = nreg; a.spill = spill ? 1 : 0; a.rowCap = rowCap;
+            a.tq = adc_tile_queries(pqM);
+            launch_adc_scan(a, pass, wt.maxWork(nq, ranks, nlist), s);
+            return;
+        }
+        const void* Q = qr.Q;
+        const float* qn = qr.qn;
         ScanParams p;
         std::memset(&p, 0, sizeof p);
         p.X = X.p; p.xnorm = xn.as<float>(); p.xnorm_max = xnMax; p.nrows = rowsPad;
@@ -253,20 +332,23 @@ struct IvfIndex::Impl {
     // Tile widths of the work tables: MFLAT_IVF_TILES = 128 / 32 (diagnostics)
     // makes every work item wide / narrow; both compute the same keys, so the
     // results never depend on it.
-    static int narrowMax() {
+    // PQ work items: adc_tile_queries(M) queries, wide only.
+    int narrowMax() const {
+        if (pq()) return 0;
         if (const char* e = std::getenv("MFLAT_IVF_TILES")) {
             if (std::atoi(e) == 128) return 0;
             if (std::atoi(e) == 32) return -1;
         }
         return kBN - kIvfNarrow;
     }
+    int wideWidth() const { return pq() ? adc_tile_queries(pqM) : kBN; }
 
     SelectParams selectParams(int nq, int nsplit, int cap, int k) const {
         SelectParams sp;
         std::memset(&sp, 0, sizeof sp);
         sp.cand = cand.as<uint2>(); sp.cnt = cnt.as<int>();
         sp.nsplit = nsplit; sp.cap = cap; sp.nq = nq; sp.k = k; sp.j = k; sp.j2 = k;
-        sp.metric = kernMetric();
+        sp.metric = pq() ? 0 : kernMetric();   // PQ values are ADC squared distances for every metric
         sp.out_stride = k;
         return sp;
     }
@@ -297,6 +379,8 @@ struct IvfIndex::Impl {
     void searchBatch(int mb, int k, int nprobe, int32_t* oIds, float* oVals, hipStream_t s) {
         const void* Q = storage == kF32 ? qbuf.p : qh.p;
         const float* qn = qnorm.as<float>();
+        const QueryRefs qr{Q, qn, lut.as<float>(), base.as<float>()};
+        wt.wideW = wideWidth();
         pos.ensure((size_t)mb * nprobe * sizeof(int));
         launch_ivf_positions(probe.as<int>(), mb, nprobe, dCellSize.as<int>(), pos.as<int>(), s);
         tauAk.ensure((size_t)mb * 4); tauAi.ensure((size_t)mb * 4);
@@ -312,7 +396,7 @@ struct IvfIndex::Impl {
             const int ca = capA(k);
             const int ra = std::min(nprobe, kBoundRanks);
             wt.build(probe.as<int>(), mb, nprobe, ra, nlist, dCellOrder.as<int>(), narrowMax(), s, pos.as<int>(), k);
-            scanPass(kPassSample, mb, ra, nprobe, ra, ca, Q, qn, tauAk.as<float>(), tauAi.as<int>(), pos.as<int>(), s,
+            scanPass(kPassSample, mb, ra, nprobe, ra, ca, qr, tauAk.as<float>(), tauAi.as<int>(), pos.as<int>(), s,
                      false, sr);
             SelectParams sp = selectParams(mb, ra, ca, k);
             sp.tau_k_key = tauAk.as<float>(); sp.tau_k_id = tauAi.as<int>();
@@ -328,7 +412,7 @@ struct IvfIndex::Impl {
         }
         // regions: one per (query, probe rank), plus a spill region per query
         wt.build(probe.as<int>(), mb, nprobe, nprobe, nlist, dCellOrder.as<int>(), narrowMax(), s);
-        scanPass(kPassFull, mb, nprobe, nprobe, nprobe + 1, cb, Q, qn, tauAk.as<float>(), tauAi.as<int>(),
+        scanPass(kPassFull, mb, nprobe, nprobe, nprobe + 1, cb, qr, tauAk.as<float>(), tauAi.as<int>(),
                  pos.as<int>(), s, true);
         {
             SelectParams sp = selectParams(mb, nprobe + 1, cb, k);
@@ -362,8 +446,19 @@ struct IvfIndex::Impl {
                 cTk.ensure((size_t)nf * 4); cTi.ensure((size_t)nf * 4);
                 cProbe.ensure((size_t)nf * nprobe * 4); cPos.ensure((size_t)nf * nprobe * 4);
                 HIPC(hipMemcpyAsync(cIdx.p, over.data() + o, (size_t)nf * 4, hipMemcpyHostToDevice, s));
-                launch_gather_rows(Q, cIdx.as<int>(), nf, dpad * esize, cQ.p, nfPad, s);
-                launch_gather_f32(qn, cIdx.as<int>(), nf, cQn.as<float>(), s);
+                QueryRefs cr_{cQ.p, cQn.as<float>(), nullptr, nullptr};
+                if (pq()) {   // the compact batch's lookup tables and coarse terms
+                    const int tab = pqM * kPqKsub;
+                    cLut.ensure((size_t)nf * tab * sizeof(float));
+                    cBase.ensure((size_t)nf * nprobe * sizeof(float));
+                    launch_gather_rows(lut.p, cIdx.as<int>(), nf, tab * (int)sizeof(float), cLut.p, nf, s);
+                    launch_gather_i32(base.as<int>(), cIdx.as<int>(), nf, nprobe, cBase.as<int>(), s);
+                    cr_.lut = cLut.as<float>();
+                    cr_.base = cBase.as<float>();
+                } else {
+                    launch_gather_rows(Q, cIdx.as<int>(), nf, dpad * esize, cQ.p, nfPad, s);
+                    launch_gather_f32(qn, cIdx.as<int>(), nf, cQn.as<float>(), s);
+                }
                 launch_gather_f32(tauKk.as<float>(), cIdx.as<int>(), nf, cTk.as<float>(), s);
                 launch_gather_i32(tauKi.as<int>(), cIdx.as<int>(), nf, 1, cTi.as<int>(), s);
                 launch_gather_i32(probe.as<int>(), cIdx.as<int>(), nf, nprobe, cProbe.as<int>(), s);
@@ -377,8 +472,8 @@ struct IvfIndex::Impl {
                 } else {
                     wt.build(cProbe.as<int>(), nf, nprobe, nprobe, nlist, dCellOrder.as<int>(), narrowMax(), s);
                 }
-                scanPass(kPassFull, nf, nprobe, nprobe, nprobe, cr, cQ.p, cQn.as<float>(), cTk.as<float>(),
-                         cTi.as<int>(), cPos.as<int>(), s);
+                scanPass(kPassFull, nf, nprobe, nprobe, nprobe, cr, cr_, cTk.as<float>(), cTi.as<int>(), cPos.as<int>(),
+                         s);
                 SelectParams sp = selectParams(nf, nprobe, cr, k);
                 sp.expect = 4 * k;
                 sp.qmap = cIdx.as<int>();
@@ -392,7 +487,7 @@ struct IvfIndex::Impl {
                                 dRid.as<int>(), s);
     }
 
-    int searchDev(const float* dq, int m, int k, int nprobe, int32_t* ids, float* vals, hipStream_t s) {
+    int searchDev(const float* dq, int m, int k, int nprobe, int rerank, int32_t* ids, float* vals, hipStream_t s) {
         if (!devOk) throw NotReady("no usable HIP device: IVF search needs a gfx950 GPU");
         if (!built) throw NotReady("IVF index is not built");
         if (m <= 0) return 0;
@@ -404,17 +499,23 @@ struct IvfIndex::Impl {
             }
             k = kMaxK;
         }
-        // reference src/IvfIndex.mm:766-767
+        // reference src/IvfIndex.mm:766-767, src/IvfPqIndex.mm:557-559
         if (nprobe < 1) nprobe = 1;
         if (nprobe > nlist) nprobe = nlist;
         if (nprobe > kMaxProbe) throw BadArg("IVF search: nprobe above 1024 is not supported");
-        if (!resident_scan_fits(dpad, storage))
+        if (!pq() && !resident_scan_fits(dpad, storage))
             throw BadArg("IVF search: the fine scan holds a 128-query tile in LDS (fp32 dim <= 128, fp16/bf16 dim <= 256)");
+        // PQ rerank (src/IvfPqIndex.mm:583-585): a PQ shortlist of kRun rows,
+        // re-ranked by exact distance, when rerank > k and the rows were kept
+        const bool doRerank = pq() && rerank > k && fullStored;
+        const int kRun = doRerank ? (int)std::min<int64_t>({(int64_t)rerank, n, (int64_t)kMaxK}) : k;
         setDevice();
         // batch the queries so the candidate regions stay bounded
-        const size_t perQuery = std::max<size_t>(nprobe > 1 ? (size_t)std::min(nprobe, kBoundRanks) * capA(k) : 0,
-                                                 (size_t)(nprobe + 1) * capB(k, nprobe)) *
-                                sizeof(uint2);
+        size_t perQuery = std::max<size_t>(nprobe > 1 ? (size_t)std::min(nprobe, kBoundRanks) * capA(kRun) : 0,
+                                           (size_t)(nprobe + 1) * capB(kRun, nprobe)) *
+                          sizeof(uint2);
+        if (pq()) perQuery += (size_t)pqM * kPqKsub * sizeof(float) + (size_t)nprobe * sizeof(float) +
+                              (size_t)kRun * (sizeof(uint2) + sizeof(int));
         int64_t mb = std::max<int64_t>(1, (int64_t)(kCandBudget / perQuery));
         if (mb >= kBN) mb = mb / kBN * kBN;
         mb = std::min<int64_t>(mb, m);
@@ -422,21 +523,53 @@ struct IvfIndex::Impl {
             const int nb = (int)std::min<int64_t>(mb, m - b0);
             const int64_t nPad = roundUp(nb, kBN);
             const float* src = dq + b0 * dim;
-            qbuf.ensure((size_t)nPad * dpad * sizeof(float));
-            qnorm.ensure((size_t)nPad * sizeof(float));
+            int32_t* bIds = ids ? ids + b0 * k : nullptr;
+            float* bVals = vals ? vals + b0 * k : nullptr;
             probe.ensure((size_t)nb * nprobe * sizeof(int));
-            launch_pack_rows(src, nb, dim, qbuf.as<float>(), nPad, dpad, s);
             const float* probeQ = src;
             if (metric == Metric::Cosine) {
                 // normalised queries (reference src/IvfIndex.mm:773-780) for the
                 // probe (row-major, dim columns) and the fine scan
-                launch_normalize_rows(qbuf.as<float>(), nb, dpad, s);
                 qrm.ensure((size_t)nb * dim * sizeof(float));
                 launch_pack_rows(src, nb, dim, qrm.as<float>(), nb, dim, s);
                 launch_normalize_rows(qrm.as<float>(), nb, dim, s);
                 probeQ = qrm.as<float>();
             }
             coarse->searchDevice(probeQ, nb, nprobe, probe.as<int32_t>(), nullptr, s);
+            if (pq()) {
+                lut.ensure((size_t)nb * pqM * kPqKsub * sizeof(float));
+                base.ensure((size_t)nb * nprobe * sizeof(float));
+                launch_pq_lut(probeQ, nb, dim, dPqc.as<float>(), dNorms.as<float>(), pqM, dsub, lut.as<float>(), s);
+                launch_pq_base(probeQ, nb, dim, dCentD.as<float>(), probe.as<int>(), nprobe, base.as<float>(), s);
+                if (!doRerank) {
+                    searchBatch(nb, k, nprobe, bIds, bVals, s);
+                    continue;
+                }
+                shortIds.ensure((size_t)nb * kRun * sizeof(int));
+                searchBatch(nb, kRun, nprobe, shortIds.as<int32_t>(), nullptr, s);
+                // exact keys of the shortlist, ties in shortlist order
+                // (src/IvfPqIndex.mm:600-625)
+                rrCand.ensure((size_t)nb * kRun * sizeof(uint2));
+                rrCnt.ensure((size_t)nb * sizeof(int));
+                rrSel.ensure((size_t)nb * k * sizeof(int));
+                const int rm = metric == Metric::L2 ? 0 : 1;
+                launch_rerank_keys(probeQ, nb, dim, dFull.as<float>(), shortIds.as<int>(), kRun, rm,
+                                   rrCand.as<uint2>(), rrCnt.as<int>(), s);
+                SelectParams sp;
+                std::memset(&sp, 0, sizeof sp);
+                sp.cand = rrCand.as<uint2>(); sp.cnt = rrCnt.as<int>();
+                sp.nsplit = 1; sp.cap = kRun; sp.nq = nb; sp.k = k; sp.j = k; sp.j2 = k;
+                sp.metric = rm;
+                sp.out_ids = rrSel.as<int32_t>(); sp.out_vals = bVals; sp.out_stride = k;
+                sp.expect = kRun;
+                launch_select(sp, s);
+                if (bIds) launch_rerank_ids(shortIds.as<int>(), kRun, rrSel.as<int>(), nb, k, bIds, s);
+                continue;
+            }
+            qbuf.ensure((size_t)nPad * dpad * sizeof(float));
+            qnorm.ensure((size_t)nPad * sizeof(float));
+            launch_pack_rows(src, nb, dim, qbuf.as<float>(), nPad, dpad, s);
+            if (metric == Metric::Cosine) launch_normalize_rows(qbuf.as<float>(), nb, dpad, s);
             const void* qs = qbuf.p;
             if (storage != kF32) {
                 qh.ensure((size_t)nPad * dpad * esize);
@@ -444,16 +577,21 @@ struct IvfIndex::Impl {
                 qs = qh.p;
             }
             if (metric == Metric::L2) launch_row_norms(qs, nb, dpad, storage, qnorm.as<float>(), s);
-            searchBatch(nb, k, nprobe, ids ? ids + b0 * k : nullptr, vals ? vals + b0 * k : nullptr, s);
+            searchBatch(nb, k, nprobe, bIds, bVals, s);
         }
         HIPC(hipStreamSynchronize(s));
         return k;
     }
 };
 
-IvfIndex::IvfIndex(int dim, Metric metric, int nlist, Storage storage) : d_(new Impl) {
+IvfIndex::IvfIndex(int dim, Metric metric, int nlist, Storage storage, int pqM) : d_(new Impl) {
     if (dim <= 0 || nlist <= 0) throw BadArg("IVF index: dim and nlist must be >= 1");
     if (storage != kF32 && storage != kF16 && storage != kBF16) throw BadArg("unknown storage type");
+    if (pqM < 0 || (pqM > 0 && (dim % pqM != 0 || pqM > kMaxSubquantizers)))
+        throw BadArg("IVF-PQ index: m must divide dim and be at most 128");
+    if (pqM > 0 && metric == Metric::InnerProduct) throw BadArg("IVF-PQ index: inner product is not supported");
+    d_->pqM = pqM;
+    d_->dsub = pqM > 0 ? dim / pqM : 0;
     d_->dim = dim;
     d_->dpad = (int)roundUp(dim, kBK);
     d_->metric = metric;
@@ -505,7 +643,21 @@ void IvfIndex::buildDevice(const float* rows, int n, hipStream_t s) {
     d_->buildFrom(rows, n, hipMemcpyDeviceToDevice, s ? s : d_->stream);
 }
 
-int IvfIndex::search(const float* q, int m, int k, int nprobe, int32_t* ids, float* dists) {
+void IvfIndex::setRerank(bool enable) { d_->rerankReq = enable; }
+int IvfIndex::subquantizers() const { return d_->pqM; }
+const std::vector<float>& IvfIndex::pqCentroids() const { return d_->hPqc; }
+
+std::vector<uint8_t> IvfIndex::codes() const {
+    Impl& I = *d_;
+    std::vector<uint8_t> out;
+    if (!I.built || !I.pq()) return out;
+    I.setDevice();
+    out.resize((size_t)I.n * I.pqM);
+    HIPC(hipMemcpy(out.data(), I.dCodes.p, out.size(), hipMemcpyDeviceToHost));
+    return out;
+}
+
+int IvfIndex::search(const float* q, int m, int k, int nprobe, int32_t* ids, float* dists, int rerank) {
     Impl& I = *d_;
     if (!I.devOk) throw NotReady("no usable HIP device: IVF search needs a gfx950 GPU");
     if (!I.built) throw NotReady("IVF index is not built");
@@ -517,7 +669,7 @@ int IvfIndex::search(const float* q, int m, int k, int nprobe, int32_t* ids, flo
     I.outIds.ensure((size_t)m * kk * sizeof(int32_t));
     I.outVals.ensure((size_t)m * kk * sizeof(float));
     HIPC(hipMemcpyAsync(I.qin.p, q, (size_t)m * I.dim * sizeof(float), hipMemcpyHostToDevice, s));
-    const int used = I.searchDev(I.qin.as<float>(), m, k, nprobe, ids ? I.outIds.as<int32_t>() : nullptr,
+    const int used = I.searchDev(I.qin.as<float>(), m, k, nprobe, rerank, ids ? I.outIds.as<int32_t>() : nullptr,
                                  dists ? I.outVals.as<float>() : nullptr, s);
     if (ids) HIPC(hipMemcpyAsync(ids, I.outIds.p, (size_t)m * used * sizeof(int32_t), hipMemcpyDeviceToHost, s));
     if (dists) HIPC(hipMemcpyAsync(dists, I.outVals.p, (size_t)m * used * sizeof(float), hipMemcpyDeviceToHost, s));
@@ -525,8 +677,9 @@ int IvfIndex::search(const float* q, int m, int k, int nprobe, int32_t* ids, flo
     return used;
 }
 
-int IvfIndex::searchDevice(const float* q, int m, int k, int nprobe, int32_t* ids, float* dists, hipStream_t s) {
-    return d_->searchDev(q, m, k, nprobe, ids, dists, s ? s : d_->stream);
+int IvfIndex::searchDevice(const float* q, int m, int k, int nprobe, int32_t* ids, float* dists, hipStream_t s,
+                           int rerank) {
+    return d_->searchDev(q, m, k, nprobe, rerank, ids, dists, s ? s : d_->stream);
 }
 
 void IvfIndex::probe(const float* q, int m, int nprobe, int32_t* cells) {

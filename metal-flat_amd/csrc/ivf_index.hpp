@@ -30,7 +30,10 @@ public:
 
     // storage: element type of the stored rows and of the queries in the fine
     // scan (as FlatIndex); the coarse probe is always fp32.
-    IvfIndex(int dim, Metric metric, int nlist, Storage storage = kF32);
+    // pqM > 0: an IVF-PQ index (reference include/metalflat/IvfPqIndex.h:37-99):
+    // rows stored as pqM one-byte residual PQ codes (pqM divides dim, <= 128;
+    // L2 or Cosine), searched by asymmetric distance; storage is unused.
+    IvfIndex(int dim, Metric metric, int nlist, Storage storage = kF32, int pqM = 0);
     ~IvfIndex();
     IvfIndex(const IvfIndex&) = delete;
     IvfIndex& operator=(const IvfIndex&) = delete;
@@ -50,9 +53,20 @@ public:
 
     // Top-k over each query's nprobe nearest cells. Returns k_used (0 when
     // m == 0); outputs m * k_used, row stride k_used, either nullable.
-    int search(const float* host_queries, int m, int k, int nprobe, int32_t* ids, float* dists);
+    // IVF-PQ: the ADC top-k; with rerank > k on an index built after
+    // setRerank(true), the ADC top-min(rerank, size, 1024) re-ranked by exact
+    // distance (reference src/IvfPqIndex.mm:552-627).
+    int search(const float* host_queries, int m, int k, int nprobe, int32_t* ids, float* dists, int rerank = 0);
     int searchDevice(const float* dev_queries, int m, int k, int nprobe, int32_t* dev_ids, float* dev_dists,
-                     hipStream_t stream);
+                     hipStream_t stream, int rerank = 0);
+
+    // IVF-PQ: keep the full rows for exact reranking (latched by build()).
+    void setRerank(bool enable);
+    int subquantizers() const;   // pqM (0: a plain IVF index)
+    // IVF-PQ, after build: sub-centroids pqM x 256 x (dim / pqM); codes
+    // size() x pqM in cell order (row slot of reorderedIds()).
+    const std::vector<float>& pqCentroids() const;
+    std::vector<uint8_t> codes() const;
 
     // The coarse stage alone: m x nprobe nearest cells, nearest first (host).
     void probe(const float* host_queries, int m, int nprobe, int32_t* cells);

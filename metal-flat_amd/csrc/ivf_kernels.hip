@@ -103,19 +103,19 @@ __global__ void ivf_runs_kernel(const int* __restrict__ keys, int n, int nlist, 
     if (i == n - 1 || keys[i + 1] != c) eEnd[c] = i + 1;
 }
 
-// A cell's n entries: wide tiles of kBN, then the rest in narrow tiles of
+// A cell's n entries: wide tiles of W, then the rest in narrow tiles of
 // kIvfNarrow -- unless more than narrowMax remain, which take one more wide
-// tile (a tile's cost is its rows times its width; narrowMax = kBN - kIvfNarrow:
+// tile (a tile's cost is its rows times its width; narrowMax = W - kIvfNarrow:
 // up to three narrow tiles are cheaper than a wide one). narrowMax = 0: wide
 // only; narrowMax < 0: narrow only.
-__device__ __forceinline__ void ivf_split(int n, int narrowMax, int& wide, int& narrow) {
+__host__ __device__ inline void ivf_split(int n, int W, int narrowMax, int& wide, int& narrow) {
     if (narrowMax < 0) {
         wide = 0;
         narrow = (n + kIvfNarrow - 1) / kIvfNarrow;
         return;
     }
-    wide = n / kBN;
-    const int rem = n - wide * kBN;
+    wide = n / W;
+    const int rem = n - wide * W;
     if (rem > narrowMax) {
         ++wide;
         narrow = 0;
@@ -126,32 +126,32 @@ __device__ __forceinline__ void ivf_split(int n, int narrowMax, int& wide, int& 
 
 // tiles of cell cellOrder[i]: wide in tilesW[i], narrow in tilesN[i]
 __global__ void ivf_tiles_kernel(const int* __restrict__ cellOrder, const int* __restrict__ eStart,
-                                 const int* __restrict__ eEnd, int nlist, int narrowMax, int* __restrict__ tilesW,
-                                 int* __restrict__ tilesN) {
+                                 const int* __restrict__ eEnd, int nlist, int W, int narrowMax,
+                                 int* __restrict__ tilesW, int* __restrict__ tilesN) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nlist) return;
     const int c = cellOrder[i];
     int w, nn;
-    ivf_split(eEnd[c] - eStart[c], narrowMax, w, nn);
+    ivf_split(eEnd[c] - eStart[c], W, narrowMax, w, nn);
     tilesW[i] = w;
     tilesN[i] = nn;
 }
 
 __global__ void ivf_work_kernel(const int* __restrict__ cellOrder, const int* __restrict__ eEnd,
                                 const int* __restrict__ eStart, const int* __restrict__ tEndW,
-                                const int* __restrict__ tEndN, int nlist, int narrowMax, int4* __restrict__ work,
-                                int4* __restrict__ workN, int* __restrict__ nwork) {
+                                const int* __restrict__ tEndN, int nlist, int W, int narrowMax,
+                                int4* __restrict__ work, int4* __restrict__ workN, int* __restrict__ nwork) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nlist) return;
     const int c = cellOrder[i];
     const int e0 = eStart[c];
     const int cnt = eEnd[c] - e0;
     int nw, nn;
-    ivf_split(cnt, narrowMax, nw, nn);
+    ivf_split(cnt, W, narrowMax, nw, nn);
     const int t0 = tEndW[i] - nw;
-    for (int t = 0; t < nw; ++t) work[t0 + t] = make_int4(c, e0 + t * kBN, min(kBN, cnt - t * kBN), 0);
+    for (int t = 0; t < nw; ++t) work[t0 + t] = make_int4(c, e0 + t * W, min(W, cnt - t * W), 0);
     const int n0 = tEndN[i] - nn;
-    const int base = nw * kBN;
+    const int base = nw * W;
     for (int t = 0; t < nn; ++t)
         workN[n0 + t] = make_int4(c, e0 + base + t * kIvfNarrow, min(kIvfNarrow, cnt - base - t * kIvfNarrow), 0);
     if (i == nlist - 1) {
@@ -219,7 +219,7 @@ void launch_ivf_finalize(int32_t* ids, int m, int k, const int* pos, const int* 
 
 int IvfWorkTable::maxWork(int m, int ranks, int nlist) const {
     const int64_t e = (int64_t)m * ranks;
-    const int64_t w = (e + kBN - 1) / kBN + nlist;
+    const int64_t w = (e + wideW - 1) / wideW + nlist;
     if (w > 0x7FFFFFFF) throw std::runtime_error("ivf: too many work items");
     return (int)w;
 }
@@ -227,8 +227,8 @@ int IvfWorkTable::maxWork(int m, int ranks, int nlist) const {
 int IvfWorkTable::maxWorkNarrow(int m, int ranks, int nlist, int narrowMax) const {
     const int64_t e = (int64_t)m * ranks;
     int64_t w = (e + kIvfNarrow - 1) / kIvfNarrow + nlist;
-    if (narrowMax >= 0)   // at most ceil(min(narrowMax, kBN - 1) / kIvfNarrow) per cell
-        w = std::min<int64_t>(w, (int64_t)nlist * ((std::min(narrowMax, kBN - 1) + kIvfNarrow - 1) / kIvfNarrow));
+    if (narrowMax >= 0)   // at most ceil(min(narrowMax, wideW - 1) / kIvfNarrow) per cell
+        w = std::min<int64_t>(w, (int64_t)nlist * ((std::min(narrowMax, wideW - 1) + kIvfNarrow - 1) / kIvfNarrow));
     if (w > 0x7FFFFFFF) throw std::runtime_error("ivf: too many work items");
     return (int)w;
 }
@@ -319,14 +319,15 @@ void IvfWorkTable::build(const int* probe, int m, int np, int ranks, int nlist, 
           "SortPairs");
     ivf_runs_kernel<<<(ne + 255) / 256, 256, 0, s>>>(keysOut, ne, nlist, eStart, eEnd);
     check(hipGetLastError(), "ivf_runs");
-    ivf_tiles_kernel<<<(nlist + 255) / 256, 256, 0, s>>>(cellOrder, eStart, eEnd, nlist, narrowMax, tiles, tilesN);
+    ivf_tiles_kernel<<<(nlist + 255) / 256, 256, 0, s>>>(cellOrder, eStart, eEnd, nlist, wideW, narrowMax, tiles,
+                                                          tilesN);
     check(hipGetLastError(), "ivf_tiles");
     t = tempBytes;
     check(hipcub::DeviceScan::InclusiveSum(temp, t, (const int*)tiles, tEnd, nlist, s), "InclusiveSum");
     t = tempBytes;
     check(hipcub::DeviceScan::InclusiveSum(temp, t, (const int*)tilesN, tEndN, nlist, s), "InclusiveSum");
-    ivf_work_kernel<<<(nlist + 255) / 256, 256, 0, s>>>(cellOrder, eEnd, eStart, tEnd, tEndN, nlist, narrowMax, work,
-                                                         workN, nwork);
+    ivf_work_kernel<<<(nlist + 255) / 256, 256, 0, s>>>(cellOrder, eEnd, eStart, tEnd, tEndN, nlist, wideW, narrowMax,
+                                                         work, workN, nwork);
     check(hipGetLastError(), "ivf_work");
     prof_end(tok, s);
 }
@@ -355,17 +356,10 @@ void IvfWorkTable::buildHost(const int* probe, int m, int np, int nlist, const i
         const int c = cellOrder[i];
         const int e0 = hStart[(size_t)c], cnt = hCnt[(size_t)c + 1];
         int wide, narrow;
-        if (narrowMax < 0) {
-            wide = 0;
-            narrow = (cnt + kIvfNarrow - 1) / kIvfNarrow;
-        } else {
-            wide = cnt / kBN;
-            const int rem = cnt - wide * kBN;
-            if (rem > narrowMax) { ++wide; narrow = 0; }
-            else narrow = (rem + kIvfNarrow - 1) / kIvfNarrow;
-        }
-        for (int t = 0; t < wide; ++t) hWork.push_back(make_int4(c, e0 + t * kBN, std::min(kBN, cnt - t * kBN), 0));
-        const int base = wide * kBN;
+        ivf_split(cnt, wideW, narrowMax, wide, narrow);
+        for (int t = 0; t < wide; ++t)
+            hWork.push_back(make_int4(c, e0 + t * wideW, std::min(wideW, cnt - t * wideW), 0));
+        const int base = wide * wideW;
         for (int t = 0; t < narrow; ++t)
             hWorkN.push_back(make_int4(c, e0 + base + t * kIvfNarrow, std::min(kIvfNarrow, cnt - base - t * kIvfNarrow), 0));
     }

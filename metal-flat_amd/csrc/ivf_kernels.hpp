@@ -29,9 +29,9 @@ constexpr int kIvfNarrow = 32;   // entries per narrow work item (one 32-query b
 // Work table of one fine-scan pass over the entries e = q * np + r of queries
 // q < m and ranks r < ranks (ranks = 1: the nearest cell only; ranks = np: all):
 //   ent        the entries sorted by (cell, e) -- a stable sort by cell
-//   work[w]    wide items (cell, first entry, entries <= 128, 0): each cell's
-//              entries in runs of 128, cells in the order cellOrder gives
-//              (decreasing size)
+//   work[w]    wide items (cell, first entry, entries <= wideW, 0): each
+//              cell's entries in runs of wideW, cells in the order cellOrder
+//              gives (decreasing size)
 //   workN[w]   narrow items (entries <= 32): the last n mod 128 entries of a
 //              cell when at most narrowMax of them remain (else they take one
 //              more wide item); narrowMax = 96 balances the two tile costs,
@@ -40,6 +40,7 @@ constexpr int kIvfNarrow = 32;   // entries per narrow work item (one 32-query b
 // maxWork() / maxWorkNarrow() bound them (the grids of the scan launches).
 // Keeps its scratch between calls.
 struct IvfWorkTable {
+    int wideW = 128;   // entries per wide work item (set before build)
     int* ent = nullptr;
     int4* work = nullptr;
     int4* workN = nullptr;

@@ -52,10 +52,13 @@ uint32_t bounded(std::mt19937& rng, uint32_t range) {   // uniform in [0, range)
 }  // namespace
 
 int kmeansTrainDevice(const float* dData, int n, int dim, int nlistReq, int iters, int maxPointsPerCentroid,
-                      float* dCentOut, int32_t* dAssignOut, int32_t* dOrderOut, int32_t* cellStart, hipStream_t s) {
+                      float* dCentOut, int32_t* dAssignOut, int32_t* dOrderOut, int32_t* cellStart, hipStream_t s,
+                      bool wrapSeeds) {
     if (n < 1 || dim < 1 || nlistReq < 1 || iters < 0 || maxPointsPerCentroid < 0)
         throw BadArg("kmeans: n, dim, nlist must be >= 1 and iters, max_points_per_centroid >= 0");
-    const int nlist = std::min(nlistReq, n);
+    // wrapSeeds: nlist stays nlistReq even above n, seed c being point perm[c mod n]
+    // (reference src/Internal.h:241-248, the PQ sub-quantizers' 256 cells)
+    const int nlist = wrapSeeds ? nlistReq : std::min(nlistReq, n);
     FlatIndex assigner(dim, Metric::L2);
     if (!assigner.ready()) throw NotReady("no usable HIP device: k-means needs a gfx950 GPU");
 
@@ -69,8 +72,10 @@ int kmeansTrainDevice(const float* dData, int n, int dim, int nlistReq, int iter
     if (maxPointsPerCentroid > 0 && (int64_t)maxPointsPerCentroid * nlist < n) trainN = maxPointsPerCentroid * nlist;
 
     const size_t rowB = (size_t)dim * sizeof(float);
-    DevMem dPerm((size_t)n * sizeof(int));
-    HIPC(hipMemcpyAsync(dPerm.p, perm.data(), (size_t)n * sizeof(int), hipMemcpyHostToDevice, s));
+    if (nlist > n)
+        for (int c = n; c < nlist; ++c) perm.push_back(perm[(size_t)(c % n)]);
+    DevMem dPerm(perm.size() * sizeof(int));
+    HIPC(hipMemcpyAsync(dPerm.p, perm.data(), perm.size() * sizeof(int), hipMemcpyHostToDevice, s));
     float* dCent = dCentOut;
     launch_gather_points(dData, dPerm.as<int>(), nlist, dim, dCent, s);
     const float* dTrain = dData;

@@ -37,7 +37,9 @@ int kmeansTrain(const float* points, int n, int dim, int nlistReq, int iters, in
 // cell counts: points n x dim, centroids nlist x dim, assign / order n
 // (nullable) are device pointers, cellStart (nlist + 1, nullable) is host
 // memory. Returns nlist.
+// wrapSeeds: nlist = nlistReq even above n (seeds wrap around the permutation).
 int kmeansTrainDevice(const float* points, int n, int dim, int nlistReq, int iters, int maxPointsPerCentroid,
-                      float* centroids, int32_t* assign, int32_t* order, int32_t* cellStart, hipStream_t s);
+                      float* centroids, int32_t* assign, int32_t* order, int32_t* cellStart, hipStream_t s,
+                      bool wrapSeeds = false);
 
 }  // namespace mflat_amd

@@ -81,6 +81,12 @@ struct mflat_ivf_index {
     mflat_ivf_index(int d, Metric m, int nl, mflat_amd::Storage st) : idx(d, m, nl, st) {}
 };
 
+struct mflat_ivfpq_index {
+    mflat_amd::IvfIndex idx;
+    std::mutex mu;
+    mflat_ivfpq_index(int d, Metric m, int nl, int sub) : idx(d, m, nl, mflat_amd::kF32, sub) {}
+};
+
 extern "C" {
 
 MFLAT_API const char* mflat_version(void) { return "0.1.0"; }
@@ -340,6 +346,119 @@ MFLAT_API mflat_status_t mflat_ivf_coarse(const mflat_ivf_index_t* h, float* oc,
         if (oc) std::memcpy(oc, c.data(), c.size() * sizeof(float));
         if (ocs) std::memcpy(ocs, cs.data(), cs.size() * sizeof(int32_t));
         if (orid) std::memcpy(orid, r.data(), r.size() * sizeof(int32_t));
+        return MFLAT_OK;
+    });
+}
+
+MFLAT_API mflat_ivfpq_index_t* mflat_ivfpq_create(int dim, mflat_metric_t metric, int nlist, int m_sub,
+                                                 mflat_status_t* st) {
+    // reference c/mflat.cpp:162-167 (IP unsupported); m_sub above 128 is this
+    // build's own limit (one query's lookup table in LDS)
+    if (dim <= 0 || nlist <= 0 || m_sub <= 0 || dim % m_sub != 0 || m_sub > 128 ||
+        metric == MFLAT_METRIC_INNER_PRODUCT) {
+        if (st) *st = MFLAT_ERR_BAD_ARG;
+        return nullptr;
+    }
+    try {
+        auto* h = new mflat_ivfpq_index(dim, conv(metric), nlist, m_sub);
+        if (st) *st = MFLAT_OK;
+        return h;
+    } catch (const std::bad_alloc&) {
+        if (st) *st = MFLAT_ERR_ALLOC;
+        return nullptr;
+    } catch (...) {
+        if (st) *st = MFLAT_ERR_INTERNAL;
+        return nullptr;
+    }
+}
+
+MFLAT_API void mflat_ivfpq_free(mflat_ivfpq_index_t* h) { delete h; }
+MFLAT_API void mflat_ivfpq_set_rerank(mflat_ivfpq_index_t* h, int enable) {
+    if (!h) return;
+    std::lock_guard<std::mutex> lk(h->mu);
+    h->idx.setRerank(enable != 0);
+}
+MFLAT_API int mflat_ivfpq_ready(const mflat_ivfpq_index_t* h) { return (h && h->idx.ready()) ? 1 : 0; }
+MFLAT_API int mflat_ivfpq_size(const mflat_ivfpq_index_t* h) { return h ? h->idx.size() : 0; }
+MFLAT_API int mflat_ivfpq_dim(const mflat_ivfpq_index_t* h) { return h ? h->idx.dim() : 0; }
+MFLAT_API int mflat_ivfpq_nlist(const mflat_ivfpq_index_t* h) { return h ? h->idx.nlist() : 0; }
+MFLAT_API int mflat_ivfpq_subquantizers(const mflat_ivfpq_index_t* h) { return h ? h->idx.subquantizers() : 0; }
+
+MFLAT_API mflat_status_t mflat_ivfpq_build(mflat_ivfpq_index_t* h, const float* v, int n) {
+    if (!h || !v) return MFLAT_ERR_NULL_ARG;
+    if (n <= 0) return MFLAT_ERR_BAD_ARG;
+    return guarded([&] {
+        std::lock_guard<std::mutex> lk(h->mu);
+        h->idx.build(v, n);
+        return MFLAT_OK;
+    });
+}
+
+MFLAT_API mflat_status_t mflat_ivfpq_search(mflat_ivfpq_index_t* h, const float* q, int m, int k, int nprobe,
+                                            int rerank, int32_t* oi, float* od, int* ok) {
+    if (!h || !q) return MFLAT_ERR_NULL_ARG;
+    if (m < 0 || k < 1 || nprobe < 1 || rerank < 0) return MFLAT_ERR_BAD_ARG;
+    if (!h->idx.ready()) return MFLAT_ERR_NOT_READY;
+    if (m == 0) {
+        if (ok) *ok = 0;
+        return MFLAT_OK;
+    }
+    return guarded([&] {
+        std::lock_guard<std::mutex> lk(h->mu);
+        const int used = h->idx.search(q, m, k, nprobe, oi, od, rerank);
+        if (ok) *ok = used;
+        return MFLAT_OK;
+    });
+}
+
+MFLAT_API mflat_status_t mflat_ivfpq_search_device(mflat_ivfpq_index_t* h, const float* q, int m, int k, int nprobe,
+                                                   int rerank, int32_t* oi, float* od, int* ok, void* stream) {
+    if (!h || !q) return MFLAT_ERR_NULL_ARG;
+    if (m < 0 || k < 1 || nprobe < 1 || rerank < 0) return MFLAT_ERR_BAD_ARG;
+    if (!h->idx.ready()) return MFLAT_ERR_NOT_READY;
+    if (m == 0) {
+        if (ok) *ok = 0;
+        return MFLAT_OK;
+    }
+    return guarded([&] {
+        std::lock_guard<std::mutex> lk(h->mu);
+        const int used = h->idx.searchDevice(q, m, k, nprobe, oi, od, static_cast<hipStream_t>(stream), rerank);
+        if (ok) *ok = used;
+        return MFLAT_OK;
+    });
+}
+
+MFLAT_API mflat_status_t mflat_ivfpq_probe(mflat_ivfpq_index_t* h, const float* q, int m, int nprobe,
+                                           int32_t* cells) {
+    if (!h || !q || !cells) return MFLAT_ERR_NULL_ARG;
+    if (m < 0 || nprobe < 1) return MFLAT_ERR_BAD_ARG;
+    if (!h->idx.ready()) return MFLAT_ERR_NOT_READY;
+    return guarded([&] {
+        std::lock_guard<std::mutex> lk(h->mu);
+        h->idx.probe(q, m, nprobe, cells);
+        return MFLAT_OK;
+    });
+}
+
+MFLAT_API mflat_status_t mflat_ivfpq_coarse(const mflat_ivfpq_index_t* h, float* oc, int32_t* ocs, int32_t* orid,
+                                            float* opqc, uint8_t* ocodes) {
+    if (!h) return MFLAT_ERR_NULL_ARG;
+    if (!h->idx.ready()) return MFLAT_ERR_NOT_READY;
+    auto* hh = const_cast<mflat_ivfpq_index_t*>(h);
+    return guarded([&] {
+        std::lock_guard<std::mutex> lk(hh->mu);
+        const auto& c = h->idx.centroids();
+        const auto& cs = h->idx.cellStart();
+        const auto& r = h->idx.reorderedIds();
+        const auto& pqc = h->idx.pqCentroids();
+        if (oc) std::memcpy(oc, c.data(), c.size() * sizeof(float));
+        if (ocs) std::memcpy(ocs, cs.data(), cs.size() * sizeof(int32_t));
+        if (orid) std::memcpy(orid, r.data(), r.size() * sizeof(int32_t));
+        if (opqc) std::memcpy(opqc, pqc.data(), pqc.size() * sizeof(float));
+        if (ocodes) {
+            const std::vector<uint8_t> codes = h->idx.codes();
+            std::memcpy(ocodes, codes.data(), codes.size());
+        }
         return MFLAT_OK;
     });
 }

@@ -75,6 +75,21 @@ SIGNATURES = {
                                         POINTER(c_int), c_void_p]),
     "mflat_ivf_probe": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "mflat_ivf_coarse": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p]),
+    "mflat_ivfpq_create": (c_void_p, [c_int, c_int, c_int, c_int, POINTER(c_int)]),
+    "mflat_ivfpq_free": (None, [c_void_p]),
+    "mflat_ivfpq_set_rerank": (None, [c_void_p, c_int]),
+    "mflat_ivfpq_ready": (c_int, [c_void_p]),
+    "mflat_ivfpq_size": (c_int, [c_void_p]),
+    "mflat_ivfpq_dim": (c_int, [c_void_p]),
+    "mflat_ivfpq_nlist": (c_int, [c_void_p]),
+    "mflat_ivfpq_subquantizers": (c_int, [c_void_p]),
+    "mflat_ivfpq_build": (c_int, [c_void_p, c_void_p, c_int]),
+    "mflat_ivfpq_search": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
+                                   POINTER(c_int)]),
+    "mflat_ivfpq_search_device": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
+                                          POINTER(c_int), c_void_p]),
+    "mflat_ivfpq_probe": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "mflat_ivfpq_coarse": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "mflat_profile_enable": (None, [c_int]),
     "mflat_profile_reset": (None, []),
     "mflat_profile_read": (c_int, [c_char_p, POINTER(c_double), POINTER(c_longlong)]),
@@ -308,6 +323,103 @@ class IvfIndex:
         _check(load().mflat_ivf_coarse(self._h, cent.ctypes.data, start.ctypes.data, rid.ctypes.data),
                "mflat_ivf_coarse")
         return cent, start, rid[:n]
+
+
+class IvfPqIndex:
+    """Python view of one mflat_ivfpq_index_t (reference IvfPqIndex.h:37-99)."""
+
+    def __init__(self, dim: int, metric: int = MFLAT_METRIC_L2, nlist: int = 64, m_sub: int = 8,
+                 rerank: bool = False):
+        lib = load()
+        st = c_int(-1)
+        self._h = lib.mflat_ivfpq_create(int(dim), int(metric), int(nlist), int(m_sub), ctypes.byref(st))
+        if not self._h:
+            raise MflatError(st.value, "mflat_ivfpq_create")
+        if rerank:
+            lib.mflat_ivfpq_set_rerank(self._h, 1)
+        self.dim = int(dim)
+        self.metric = int(metric)
+        self.m_sub = int(m_sub)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            load().mflat_ivfpq_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def handle(self):
+        return self._h
+
+    def ready(self) -> bool:
+        return load().mflat_ivfpq_ready(self._h) == 1
+
+    def size(self) -> int:
+        return load().mflat_ivfpq_size(self._h)
+
+    def nlist(self) -> int:
+        return load().mflat_ivfpq_nlist(self._h)
+
+    def build(self, vectors) -> None:
+        v = _f32(vectors).reshape(-1, self.dim)
+        _check(load().mflat_ivfpq_build(self._h, v.ctypes.data, v.shape[0]), "mflat_ivfpq_build")
+
+    def search(self, queries, k: int, nprobe: int, rerank: int = 0):
+        """Returns (ids int32 [m, k_used], distances float32 [m, k_used], k_used)."""
+        q = _f32(queries).reshape(-1, self.dim)
+        m = q.shape[0]
+        kk = max(1, min(int(k), load().mflat_max_k()))
+        ids = np.full((max(m, 1), kk), -7, dtype=np.int32)
+        dist = np.full((max(m, 1), kk), np.nan, dtype=np.float32)
+        used = c_int(-1)
+        _check(load().mflat_ivfpq_search(self._h, q.ctypes.data, m, int(k), int(nprobe), int(rerank),
+                                          ids.ctypes.data, dist.ctypes.data, ctypes.byref(used)),
+               "mflat_ivfpq_search")
+        ku = used.value
+        return (ids.reshape(-1)[: m * ku].reshape(m, ku).copy(),
+                dist.reshape(-1)[: m * ku].reshape(m, ku).copy(), ku)
+
+    def search_device(self, q, k: int, nprobe: int, out_ids, out_dist, rerank: int = 0, stream=None) -> int:
+        used = c_int(-1)
+        _check(load().mflat_ivfpq_search_device(
+            self._h, q.data_ptr(), q.shape[0], int(k), int(nprobe), int(rerank),
+            out_ids.data_ptr() if out_ids is not None else None,
+            out_dist.data_ptr() if out_dist is not None else None,
+            ctypes.byref(used), _stream_ptr(stream)), "mflat_ivfpq_search_device")
+        return used.value
+
+    def probe(self, queries, nprobe: int) -> np.ndarray:
+        q = _f32(queries).reshape(-1, self.dim)
+        m = q.shape[0]
+        npb = max(1, min(int(nprobe), self.nlist()))
+        cells = np.full((max(m, 1), npb), -7, dtype=np.int32)
+        _check(load().mflat_ivfpq_probe(self._h, q.ctypes.data, m, int(nprobe), cells.ctypes.data),
+               "mflat_ivfpq_probe")
+        return cells[:m].copy()
+
+    def coarse(self):
+        """(centroids [nlist, dim], cell_start [nlist + 1], reordered_ids [n],
+        pq_centroids [m_sub, 256, dim / m_sub], codes [n, m_sub] in cell order)."""
+        nl, n, M = self.nlist(), self.size(), self.m_sub
+        cent = np.empty((nl, self.dim), np.float32)
+        start = np.empty(nl + 1, np.int32)
+        rid = np.empty(max(n, 1), np.int32)
+        pqc = np.empty((M, 256, self.dim // M), np.float32)
+        codes = np.empty((max(n, 1), M), np.uint8)
+        _check(load().mflat_ivfpq_coarse(self._h, cent.ctypes.data, start.ctypes.data, rid.ctypes.data,
+                                         pqc.ctypes.data, codes.ctypes.data), "mflat_ivfpq_coarse")
+        return cent, start, rid[:n], pqc, codes[:n]
 
 
 def kmeans_train(points, nlist: int, iters: int, max_points_per_centroid: int = 256):

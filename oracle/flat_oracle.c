@@ -31,6 +31,13 @@
  *                        top-k over the rows of its cells in probe order (rows
  *                        lo..hi of the cell-ordered payload), strict '>'
  *                        insertion, ids through reorderedIds, cells < 0 skipped
+ *   orc_ivfpq_search     src/IvfPqIndex.mm:383-445 (searchCpu, residual mode) with
+ *                        the tables of src/PqTrainer.h:84-116: lut = ||p||^2 -
+ *                        2 q_m.p, T = 2 c_m.p, base = sqL2(q, c); dist = base +
+ *                        sum_m (lut + T) in ascending m; strict '>' on -dist;
+ *                        value = dist
+ *   orc_pq_rerank        src/IvfPqIndex.mm:598-625: exact score over a shortlist,
+ *                        strict '>' in shortlist order, -1 entries skipped
  *
  * Build with -ffp-contract=off so no multiply-add is fused: the sums are the
  * plain sequential fp32 sums the reference's C++ source spells out.
@@ -329,4 +336,136 @@ int orc_ivf_search(const float* rdb, const int32_t* rid, const int32_t* cell_sta
         if (jobs[t].status != 0) rc = -1;
     }
     return rc;
+}
+
+/* IVF-PQ ADC search (residual). cent nlist x dim; cs/rid the CSR; codes n x M
+   bytes in cell order; pqc M x 256 x dsub. q already normalised for Cosine. */
+typedef struct {
+    const float* cent; const int32_t* cs; const int32_t* rid; const uint8_t* codes; const float* pqc;
+    const float* norms; const float* T; int M; int dsub; int dim;
+    const float* q; const int32_t* probed; int nprobe; int k;
+    int32_t* ids; float* vals; int64_t lo, hi; int status;
+} orc_pq_job_t;
+
+static void* orc_pq_worker(void* arg) {
+    orc_pq_job_t* j = (orc_pq_job_t*)arg;
+    const int M = j->M, K = 256;
+    float* lut = (float*)malloc(sizeof(float) * (size_t)M * K);
+    float* bs = (float*)malloc(sizeof(float) * (size_t)j->k);
+    int32_t* bi = (int32_t*)malloc(sizeof(int32_t) * (size_t)j->k);
+    if (!lut || !bs || !bi) { free(lut); free(bs); free(bi); j->status = -1; return NULL; }
+    for (int64_t qi = j->lo; qi < j->hi; ++qi) {
+        const float* q = j->q + qi * j->dim;
+        for (int mm = 0; mm < M; ++mm)
+            for (int c = 0; c < K; ++c)
+                lut[mm * K + c] = j->norms[mm * K + c] -
+                                  2.0f * orc_dot(q + mm * j->dsub, j->pqc + ((int64_t)mm * K + c) * j->dsub, j->dsub);
+        for (int i = 0; i < j->k; ++i) { bs[i] = -INFINITY; bi[i] = -1; }
+        for (int pp = 0; pp < j->nprobe; ++pp) {
+            const int32_t c = j->probed[qi * j->nprobe + pp];
+            if (c < 0) continue;
+            const float base = orc_sql2(q, j->cent + (int64_t)c * j->dim, j->dim);
+            const float* Tc = j->T + (int64_t)c * M * K;
+            for (int64_t r = j->cs[c]; r < j->cs[c + 1]; ++r) {
+                const uint8_t* code = j->codes + r * M;
+                float dist = base;
+                for (int mm = 0; mm < M; ++mm) dist += lut[mm * K + code[mm]] + Tc[mm * K + code[mm]];
+                const float s = -dist;
+                if (s > bs[0]) {
+                    int pos = 0;
+                    while (pos + 1 < j->k && s > bs[pos + 1]) {
+                        bs[pos] = bs[pos + 1];
+                        bi[pos] = bi[pos + 1];
+                        ++pos;
+                    }
+                    bs[pos] = s;
+                    bi[pos] = j->rid[r];
+                }
+            }
+        }
+        for (int i = 0; i < j->k; ++i) {
+            const int src = j->k - 1 - i;
+            j->ids[qi * j->k + i] = bi[src];
+            j->vals[qi * j->k + i] = -bs[src];
+        }
+    }
+    free(lut); free(bs); free(bi);
+    j->status = 0;
+    return NULL;
+}
+
+int orc_ivfpq_search(const float* cent, int nlist, const int32_t* cs, const int32_t* rid, const uint8_t* codes,
+                     const float* pqc, int M, int dim, const float* q, int64_t m, const int32_t* probed, int nprobe,
+                     int k, int32_t* out_ids, float* out_vals, int threads) {
+    if (k < 1 || m < 0 || dim <= 0 || M <= 0 || dim % M != 0 || nprobe < 1) return -2;
+    const int dsub = dim / M, K = 256;
+    float* norms = (float*)malloc(sizeof(float) * (size_t)M * K);
+    float* T = (float*)malloc(sizeof(float) * (size_t)nlist * M * K);
+    if (!norms || !T) { free(norms); free(T); return -1; }
+    for (int e = 0; e < M * K; ++e) norms[e] = orc_dot(pqc + (int64_t)e * dsub, pqc + (int64_t)e * dsub, dsub);
+    for (int c = 0; c < nlist; ++c)
+        for (int mm = 0; mm < M; ++mm)
+            for (int jj = 0; jj < K; ++jj)
+                T[((int64_t)c * M + mm) * K + jj] =
+                    2.0f * orc_dot(cent + (int64_t)c * dim + mm * dsub, pqc + ((int64_t)mm * K + jj) * dsub, dsub);
+    if (threads < 1) threads = 1;
+    if (threads > 256) threads = 256;
+    pthread_t tid[256];
+    orc_pq_job_t jobs[256];
+    const int64_t chunk = (m + threads - 1) / threads;
+    int started = 0, rc = 0;
+    for (int t = 0; t < threads; ++t) {
+        const int64_t lo = (int64_t)t * chunk;
+        const int64_t hi = lo + chunk < m ? lo + chunk : m;
+        if (lo >= hi) break;
+        orc_pq_job_t jj = {cent, cs, rid, codes, pqc, norms, T, M, dsub, dim, q, probed, nprobe, k,
+                           out_ids, out_vals, lo, hi, 0};
+        jobs[t] = jj;
+        if (threads == 1) { orc_pq_worker(&jobs[t]); started = -1; break; }
+        if (pthread_create(&tid[t], NULL, orc_pq_worker, &jobs[t]) != 0) { rc = -1; break; }
+        ++started;
+    }
+    if (started < 0) rc = jobs[0].status;
+    for (int t = 0; t < started; ++t) {
+        pthread_join(tid[t], NULL);
+        if (jobs[t].status != 0) rc = -1;
+    }
+    free(norms); free(T);
+    return rc;
+}
+
+/* Exact rerank of a shortlist (nq x kRun ids, -1 skipped): metric 0 L2 (score
+   -sqL2), otherwise dot; k best by strict '>' in shortlist order; value =
+   scoreToValue (sqL2 / dot; unfilled +inf / -inf). */
+int orc_pq_rerank(const float* full, int dim, int metric, const float* q, int64_t m, const int32_t* shortIds,
+                  int kRun, int k, int32_t* out_ids, float* out_vals) {
+    float* bs = (float*)malloc(sizeof(float) * (size_t)k);
+    int32_t* bi = (int32_t*)malloc(sizeof(int32_t) * (size_t)k);
+    if (!bs || !bi) { free(bs); free(bi); return -1; }
+    const int sm = metric == ORC_L2 ? ORC_L2 : ORC_IP;
+    for (int64_t qi = 0; qi < m; ++qi) {
+        for (int i = 0; i < k; ++i) { bs[i] = -INFINITY; bi[i] = -1; }
+        for (int i = 0; i < kRun; ++i) {
+            const int32_t id = shortIds[qi * kRun + i];
+            if (id < 0) continue;
+            const float s = orc_score(sm, q + qi * dim, full + (int64_t)id * dim, dim);
+            if (s > bs[0]) {
+                int pos = 0;
+                while (pos + 1 < k && s > bs[pos + 1]) {
+                    bs[pos] = bs[pos + 1];
+                    bi[pos] = bi[pos + 1];
+                    ++pos;
+                }
+                bs[pos] = s;
+                bi[pos] = id;
+            }
+        }
+        for (int i = 0; i < k; ++i) {
+            const int src = k - 1 - i;
+            out_ids[qi * k + i] = bi[src];
+            out_vals[qi * k + i] = orc_score_to_value(sm, bs[src]);
+        }
+    }
+    free(bs); free(bi);
+    return 0;
 }

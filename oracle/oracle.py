@@ -47,6 +47,12 @@ def lib():
         o.orc_ivf_search.restype = c_int
         o.orc_ivf_search.argtypes = [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int64, c_void_p,
                                      c_int, c_int, c_void_p, c_void_p, c_int]
+        o.orc_ivfpq_search.restype = c_int
+        o.orc_ivfpq_search.argtypes = [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                       c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p, c_void_p, c_int]
+        o.orc_pq_rerank.restype = c_int
+        o.orc_pq_rerank.argtypes = [c_void_p, c_int, c_int, c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p,
+                                    c_void_p]
         o.orc_brute_lex.restype = c_int
         o.orc_brute_lex.argtypes = [c_void_p, c_int64, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p]
         _o = o
@@ -230,15 +236,17 @@ def kmeans_update(pts, assign, nlist, cent, reseed):
     return out
 
 
-def kmeans_train(points, nlist, iters, max_points_per_centroid=256):
+def kmeans_train(points, nlist, iters, max_points_per_centroid=256, wrap=False):
     """Returns (centroids, assign, cell_start, order) as the library's
-    mflat_kmeans_train defines them."""
+    mflat_kmeans_train defines them. wrap: nlist stays as given above n, seed c
+    being point perm[c mod n] (the PQ sub-quantizers' 256 cells,
+    src/Internal.h:241-248)."""
     points = _f32(points)
     n, d = points.shape
-    nlist = min(nlist, n)
+    nlist = nlist if wrap else min(nlist, n)
     rng = MT19937Stream(12345)
     perm = seed_permutation(n, rng)
-    cent = points[perm[:nlist]].copy()
+    cent = points[perm[np.arange(nlist) % n]].copy()
     train_n = n
     if max_points_per_centroid > 0 and max_points_per_centroid * nlist < n:
         train_n = max_points_per_centroid * nlist
@@ -327,4 +335,66 @@ def ivf_search(db, cell_start, rid, q, k, probed, metric=0, threads=1, payload=N
                               probed.ctypes.data, probed.shape[1], k, ids.ctypes.data, vals.ctypes.data, threads)
     if rc != 0:
         raise RuntimeError(f"orc_ivf_search rc={rc}")
+    return ids, vals
+
+
+# ---- IVF-PQ (the compressed index's checker) ----------------------------------
+# Restates IvfPqIndex's build (src/IvfPqIndex.mm:286-340: coarse cells as IVF,
+# residual PQ with 256-cell k-means per sub-space over all rows, codes = the
+# final assignments) and its CPU search (:383-445) and rerank (:598-625).
+
+PQ_KSUB = 256
+
+
+def pq_train(residuals, M, iters=IVF_TRAIN_ITERS):
+    """(pqc [M, 256, dsub], codes [n, M] uint8 in row order): k-means of each
+    sub-space (every row trains; seeds wrap when n < 256)."""
+    r = _f32(residuals)
+    n, d = r.shape
+    dsub = d // M
+    pqc = np.empty((M, PQ_KSUB, dsub), np.float32)
+    codes = np.empty((n, M), np.uint8)
+    for mm in range(M):
+        sub = np.ascontiguousarray(r[:, mm * dsub:(mm + 1) * dsub])
+        c, a, _, _ = kmeans_train(sub, PQ_KSUB, iters, 0, wrap=True)
+        pqc[mm] = c
+        codes[:, mm] = a
+    return pqc, codes
+
+
+def ivfpq_search(cent, cell_start, rid, codes_cell, pqc, q, k, probed, metric=0, threads=1):
+    """searchCpu of the residual IVF-PQ index over given probed cells: ids and
+    ADC distances [m, k]. codes_cell: n x M codes in cell order."""
+    q = normalize_rows(q) if metric == 2 else _f32(q)
+    cent = _f32(cent)
+    pqc = _f32(pqc)
+    M = pqc.shape[0]
+    codes_cell = np.ascontiguousarray(codes_cell, np.uint8)
+    start = np.ascontiguousarray(cell_start, np.int32)
+    rid = np.ascontiguousarray(rid, np.int32)
+    probed = np.ascontiguousarray(probed, np.int32)
+    m, d = q.shape
+    ids = np.empty((m, k), np.int32)
+    vals = np.empty((m, k), np.float32)
+    rc = lib().orc_ivfpq_search(cent.ctypes.data, cent.shape[0], start.ctypes.data, rid.ctypes.data,
+                                codes_cell.ctypes.data, pqc.ctypes.data, M, d, q.ctypes.data, m, probed.ctypes.data,
+                                probed.shape[1], k, ids.ctypes.data, vals.ctypes.data, threads)
+    if rc != 0:
+        raise RuntimeError(f"orc_ivfpq_search rc={rc}")
+    return ids, vals
+
+
+def pq_rerank(full, q, short_ids, k, metric=0):
+    """Exact rerank of a shortlist (metric 0 L2, 2 Cosine: rows and queries
+    normalised, ranked by dot)."""
+    full = normalize_rows(full) if metric == 2 else _f32(full)
+    q = normalize_rows(q) if metric == 2 else _f32(q)
+    short_ids = np.ascontiguousarray(short_ids, np.int32)
+    m, d = q.shape
+    ids = np.empty((m, k), np.int32)
+    vals = np.empty((m, k), np.float32)
+    rc = lib().orc_pq_rerank(full.ctypes.data, d, 0 if metric == 0 else 1, q.ctypes.data, m, short_ids.ctypes.data,
+                             short_ids.shape[1], k, ids.ctypes.data, vals.ctypes.data)
+    if rc != 0:
+        raise RuntimeError(f"orc_pq_rerank rc={rc}")
     return ids, vals

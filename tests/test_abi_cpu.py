@@ -219,3 +219,37 @@ def test_ivf_arguments():
     hx = lib.mflat_ivf_create_ex(8, 1, 3, mflat.MFLAT_STORAGE_BF16, ctypes.byref(st))
     assert hx and lib.mflat_ivf_storage(hx) == mflat.MFLAT_STORAGE_BF16
     lib.mflat_ivf_free(hx)
+
+
+def test_ivfpq_arguments():
+    """reference c/mflat.cpp:161-198: create / build / search checks."""
+    lib = mflat.load()
+    st = ctypes.c_int(-1)
+    for dim, metric, nl, m in ((0, 0, 4, 2), (8, 0, 0, 2), (8, 0, 4, 0), (8, 0, 4, 3),
+                               (8, mflat.MFLAT_METRIC_INNER_PRODUCT, 4, 2), (256, 0, 4, 256)):
+        assert not lib.mflat_ivfpq_create(dim, metric, nl, m, ctypes.byref(st)), (dim, metric, nl, m)
+        assert st.value == mflat.MFLAT_ERR_BAD_ARG
+    lib.mflat_ivfpq_free(None)
+    lib.mflat_ivfpq_set_rerank(None, 1)
+    for f in (lib.mflat_ivfpq_ready, lib.mflat_ivfpq_size, lib.mflat_ivfpq_dim, lib.mflat_ivfpq_nlist,
+              lib.mflat_ivfpq_subquantizers):
+        assert f(None) == 0
+    h = lib.mflat_ivfpq_create(8, mflat.MFLAT_METRIC_COSINE, 6, 4, ctypes.byref(st))
+    assert h and st.value == mflat.MFLAT_OK
+    assert lib.mflat_ivfpq_ready(h) == 0 and lib.mflat_ivfpq_dim(h) == 8
+    assert lib.mflat_ivfpq_nlist(h) == 6 and lib.mflat_ivfpq_subquantizers(h) == 4
+    lib.mflat_ivfpq_set_rerank(h, 1)
+    x = np.zeros((3, 8), np.float32)
+    assert lib.mflat_ivfpq_build(None, x.ctypes.data, 3) == mflat.MFLAT_ERR_NULL_ARG
+    assert lib.mflat_ivfpq_build(h, x.ctypes.data, 0) == mflat.MFLAT_ERR_BAD_ARG
+    s = lib.mflat_ivfpq_search
+    assert s(h, None, 1, 1, 1, 0, None, None, None) == mflat.MFLAT_ERR_NULL_ARG
+    for m, k, npb, rr in ((-1, 1, 1, 0), (1, 0, 1, 0), (1, 1, 0, 0), (1, 1, 1, -1)):
+        assert s(h, x.ctypes.data, m, k, npb, rr, None, None, None) == mflat.MFLAT_ERR_BAD_ARG
+    assert s(h, x.ctypes.data, 1, 1, 1, 0, None, None, None) == mflat.MFLAT_ERR_NOT_READY
+    assert lib.mflat_ivfpq_coarse(h, None, None, None, None, None) == mflat.MFLAT_ERR_NOT_READY
+    probe = mflat.FlatIndex(4)
+    if not probe.ready():
+        assert lib.mflat_ivfpq_build(h, x.ctypes.data, 3) == mflat.MFLAT_ERR_NOT_READY
+    probe.close()
+    lib.mflat_ivfpq_free(h)
