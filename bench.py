@@ -272,6 +272,118 @@ def ivf_bench(args):
     print(json.dumps(out), flush=True)
 
 
+def ivfpq_bench(args):
+    """IVF-PQ search (mflat_ivfpq_*) on C2's database and queries: nlist and
+    nprobe by the reference bench's IVF rule, m_sub = 16 (16-byte codes for
+    d = 128, the reference header's example), k = 10 (the reference's IVF-PQ
+    serves k <= 64), rerank 16 k (the header's suggestion). A step is one search
+    of the whole batch (device pointers). roofline: the ADC fine scan (ivf_scan
+    family) is bound by LDS gathers -- M table reads of 4 bytes per candidate
+    per query; achieved = those bytes / its time against the LDS read peak
+    (128 B per clock per CU, 256 CUs, 2.4 GHz)."""
+    import numpy as np
+    import datagen
+    import hipmem
+    import mflat
+    import oracle
+
+    mflat.load()
+    x, q = datagen.gmm()
+    if args.nq:
+        q = q[: args.nq]
+    nb, d = x.shape
+    nq = q.shape[0]
+    k = 10
+    M = 16
+    rerank = args.rerank if args.rerank >= 0 else 16 * k
+    nlist = args.nlist or max(64, int(np.sqrt(nb)))
+    nprobe = args.nprobe or max(1, nlist // 16)
+    log(f"[bench] ivfpq: nb={nb} d={d} nq={nq} k={k} nlist={nlist} nprobe={nprobe} m_sub={M} rerank={rerank}")
+    idx = mflat.IvfPqIndex(d, mflat.MFLAT_METRIC_L2, nlist, M, rerank=rerank > k)
+    t0 = time.perf_counter()
+    idx.build(x)
+    build_s = time.perf_counter() - t0
+    log(f"[bench] ivfpq build {build_s:.2f}s")
+    cent, start, rid, pqc, codes = idx.coarse()
+    probed = idx.probe(q, nprobe)
+    rows = int(np.diff(start.astype(np.int64))[probed].sum())
+
+    qd = hipmem.DeviceArray.from_numpy(q)
+    ids = hipmem.DeviceArray((nq, k), np.int32)
+    dist = hipmem.DeviceArray((nq, k), np.float32)
+    for _ in range(args.warmup):
+        idx.search_device(qd, k, nprobe, ids, dist, rerank=rerank)
+    hipmem.synchronize()
+    mflat.profile_reset()
+    mflat.profile_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        idx.search_device(qd, k, nprobe, ids, dist, rerank=rerank)
+    hipmem.synchronize()
+    elapsed = time.perf_counter() - t0
+    mflat.profile_enable(False)
+    kern = {}
+    for fam in ("ivf_scan", "ivf_bound", "scan_filter", "select", "norms", "prep"):
+        ms, n = mflat.profile_read(fam)
+        if n:
+            kern[fam] = {"total_ms": round(ms, 4), "launches": n, "mean_ms": round(ms / n, 4)}
+    gi = ids.numpy()
+    log(f"[bench] ivfpq {args.steps} steps in {elapsed:.3f}s")
+    lds_bytes = 4.0 * M * rows   # table reads of the scan per search
+    peak = 128.0 * 256 * 2.4e9 / 1e9
+    ach = lds_bytes * args.steps / (kern["ivf_scan"]["total_ms"] / 1000.0) / 1e9
+    flat = mflat.FlatIndex(d, mflat.MFLAT_METRIC_L2)
+    flat.add(x)
+    fi, _, _ = flat.search(q, k)
+    flat.close()
+    recall = float(np.mean([len(set(gi[r].tolist()) & set(fi[r].tolist())) / k for r in range(nq)]))
+    out = {
+        "metric": f"QPS, IVF-PQ L2 d={d} nb={nb} nlist={nlist} nprobe={nprobe} m={M} k={k} rerank={rerank} (1 GPU)",
+        "value": round(nq * args.steps / elapsed, 2),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1000.0 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8 codes, fp32 tables",
+        "data": "synthetic",
+        "config": {"workload": f"IVF-PQ over C2's database and queries (GMM 1024 centres, sigma 0.3, seed 1), "
+                               f"nlist={nlist}, nprobe={nprobe}, m_sub={M}, k={k}, rerank={rerank}",
+                   "nb": nb, "d": d, "nq": nq, "k": k, "nlist": nlist, "nprobe": nprobe, "m_sub": M,
+                   "rerank": rerank, "parallelism": "single GPU"},
+        "roofline": {"bound": "lds", "achieved": round(ach, 2), "peak": peak, "unit": "GB/s",
+                     "frac": round(ach / peak, 4), "traffic": None},
+        "kernels": kern,
+        "probed_rows_per_query": round(rows / nq, 1),
+        "recall_vs_exact_flat": round(recall, 5),
+        "code_bytes": int(nb * M),
+        "build_s": round(build_s, 3),
+    }
+    if not args.no_cpu_baseline:
+        for threads, key in ((1, "cpu_baseline"), (host_threads(), "cpu_baseline_all_cores")):
+            log(f"[bench] ivfpq cpu baseline ({threads} threads) ...")
+            t0 = time.perf_counter()
+            oracle.ivfpq_search(cent, start, rid, codes, pqc, q[:threads], rerank if rerank > k else k,
+                                probed[:threads], 0, threads=threads)
+            one = max(time.perf_counter() - t0, 1e-6) / threads
+            n = int(max(1, min(nq, 12.0 / one)))
+            t0 = time.perf_counter()
+            kr = rerank if rerank > k else k
+            si, _ = oracle.ivfpq_search(cent, start, rid, codes, pqc, q[:n], kr, probed[:n], 0, threads=threads)
+            oi = oracle.pq_rerank(x, q[:n], si, k, 0)[0] if rerank > k else si
+            dt = time.perf_counter() - t0
+            agree = float(np.mean([len(set(oi[r].tolist()) & set(gi[r].tolist())) / k for r in range(n)]))
+            out[key] = {"value": n / dt, "unit": "queries/s", "cores": threads, "kind": "port",
+                        "sample": f"first {n} of the {nq} queries over the same probed cells (searchCpu and "
+                                  f"rerank restatement), {dt:.1f} s on {threads} host thread(s); GPU/oracle id "
+                                  f"agreement on the sample {agree:.5f}"}
+    idx.close()
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -287,6 +399,9 @@ def main():
                          "count instead: one JSON line with ms per training iteration")
     ap.add_argument("--ivf", action="store_true",
                     help="time IVF search (mflat_ivf_*) on C2's database and queries instead")
+    ap.add_argument("--ivfpq", action="store_true",
+                    help="time IVF-PQ search (mflat_ivfpq_*) on C2's database and queries instead")
+    ap.add_argument("--rerank", type=int, default=-1, help="--ivfpq: rerank shortlist (default 16 k)")
     ap.add_argument("--nlist", type=int, default=0, help="--ivf: cells (default max(64, sqrt(nb)))")
     ap.add_argument("--nprobe", type=int, default=0, help="--ivf: probed cells (default nlist / 16)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -318,6 +433,9 @@ def main():
 
     if args.ivf:
         ivf_bench(args)
+        return
+    if args.ivfpq:
+        ivfpq_bench(args)
         return
 
     import numpy as np

@@ -140,7 +140,16 @@ int adc_tile_queries(int M) {
     return t < 1 ? 1 : t > kAdcMaxTq ? kAdcMaxTq : t;
 }
 
-// MV: M known at compile time (codes loaded as MV / 4 words), 0: any M
+// One lookup of a combined table: byte offset a of the code's entry plus a
+// compile-time offset (query tile slot and sub-space), which the compiler folds
+// into the ds_read immediate.
+__device__ __forceinline__ float lds_at(const float* base, uint32_t a, int off) {
+    return *(const float*)((const char*)base + a + off);
+}
+
+// MV: M known at compile time (codes loaded with vector loads, TQ = 64 / MV
+// query slots unrolled: the M byte offsets of a row are computed once and
+// serve every query), 0: any M (runtime loops)
 template <int PASS, int MV>
 __global__ void __launch_bounds__(256) adc_scan_kernel(AdcParams p) {
     extern __shared__ float sL[];   // [tq][M][256]
@@ -163,12 +172,35 @@ __global__ void __launch_bounds__(256) adc_scan_kernel(AdcParams p) {
         sCnt[tid] = 0;
     }
     __syncthreads();
+    // combined tables: lut of the query + the cell's cross table (tab floats
+    // each, a multiple of 4: float4 copies)
     const int tab = M * kPqKsub;
-    const float* Tc = p.T + (int64_t)c * tab;
-    for (int i = tid; i < ne * tab; i += 256) {
-        const int t = i / tab;
-        const int o = i - t * tab;
-        sL[i] = p.lut[(int64_t)sQi[t] * tab + o] + Tc[o];
+    const int tab4 = tab / 4;
+    const float4* Tc = (const float4*)(p.T + (int64_t)c * tab);
+    float4* sL4 = (float4*)sL;
+    auto add4 = [](float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); };
+    if constexpr (MV > 0) {
+        // every load of the thread's share in flight at once: PER float4 of
+        // the cross table, reused by the TQ queries (empty slots copy slot 0's)
+        constexpr int TQ = 64 / MV, PER = MV / 4;
+        float4 tv[PER], lv[TQ][PER];
+#pragma unroll
+        for (int j = 0; j < PER; ++j) tv[j] = Tc[tid + j * 256];
+#pragma unroll
+        for (int t = 0; t < TQ; ++t) {
+            const float4* lq = (const float4*)(p.lut + (int64_t)sQi[t < ne ? t : 0] * tab);
+#pragma unroll
+            for (int j = 0; j < PER; ++j) lv[t][j] = lq[tid + j * 256];
+        }
+#pragma unroll
+        for (int t = 0; t < TQ; ++t)
+#pragma unroll
+            for (int j = 0; j < PER; ++j) sL4[t * tab4 + tid + j * 256] = add4(lv[t][j], tv[j]);
+    } else {
+        for (int t = 0; t < ne; ++t) {
+            const float4* lq = (const float4*)(p.lut + (int64_t)sQi[t] * tab);
+            for (int o = tid; o < tab4; o += 256) sL4[t * tab4 + o] = add4(lq[o], Tc[o]);
+        }
     }
     __syncthreads();
 
@@ -186,23 +218,52 @@ __global__ void __launch_bounds__(256) adc_scan_kernel(AdcParams p) {
             if (sp < p.cap) p.cand[sr * p.cap + sp] = v;
         }
     };
-    for (int r = tid; r < rows; r += 256) {
-        const int64_t row = beg + r;
-        if constexpr (MV > 0) {
-            uint32_t cw[MV / 4];
-            const uint32_t* src = (const uint32_t*)(p.codes + row * MV);
+    if constexpr (MV > 0) {
+        constexpr int TQ = 64 / MV;   // == adc_tile_queries(MV); slots >= ne are computed, never emitted
+        constexpr int NW = MV / 4;    // code words per row
+        // the next row's codes load while the current row is summed
+        auto load_codes = [&](int r, uint32_t* cw) {
+            const uint8_t* src = p.codes + (int64_t)(beg + r) * MV;
+            if constexpr (NW == 2) {
+                const uint2 v = *(const uint2*)src;
+                cw[0] = v.x; cw[1] = v.y;
+            } else {
 #pragma unroll
-            for (int w = 0; w < MV / 4; ++w) cw[w] = src[w];
-            for (int t = 0; t < ne; ++t) {
-                const float* L = sL + t * tab;
-                float dist = sBase[t];
-#pragma unroll
-                for (int m = 0; m < MV; ++m) dist = dist + L[m * kPqKsub + ((cw[m >> 2] >> ((m & 3) * 8)) & 255u)];
-                const int id = sPos[t] + r;
-                if (dist < sTk[t] || (dist == sTk[t] && id <= sTi[t])) emit(t, dist, id);
+                for (int w = 0; w < NW; w += 4) {
+                    const uint4 v = *(const uint4*)(src + w * 4);
+                    cw[w] = v.x; cw[w + 1] = v.y; cw[w + 2] = v.z; cw[w + 3] = v.w;
+                }
             }
-        } else {
-            const uint8_t* code = p.codes + row * M;
+        };
+        uint32_t nx[NW];
+        if (tid < rows) load_codes(tid, nx);
+        for (int r = tid; r < rows; r += 256) {
+            uint32_t cw[NW];
+#pragma unroll
+            for (int w = 0; w < NW; ++w) cw[w] = nx[w];
+            if (r + 256 < rows) load_codes(r + 256, nx);
+            uint32_t a[MV];   // byte offset of the row's entry in table m (without m * 1 KiB)
+#pragma unroll
+            for (int m = 0; m < MV; ++m) a[m] = ((cw[m >> 2] >> ((m & 3) * 8)) & 255u) * 4u;
+            float dist[TQ];
+#pragma unroll
+            for (int t = 0; t < TQ; ++t) dist[t] = sBase[t];
+#pragma unroll
+            for (int m = 0; m < MV; ++m) {
+#pragma unroll
+                for (int t = 0; t < TQ; ++t)
+                    dist[t] = dist[t] + lds_at(sL, a[m], (t * MV + m) * kPqKsub * (int)sizeof(float));
+            }
+#pragma unroll
+            for (int t = 0; t < TQ; ++t) {
+                if (t >= ne) break;
+                const int id = sPos[t] + r;
+                if (dist[t] < sTk[t] || (dist[t] == sTk[t] && id <= sTi[t])) emit(t, dist[t], id);
+            }
+        }
+    } else {
+        for (int r = tid; r < rows; r += 256) {
+            const uint8_t* code = p.codes + (int64_t)(beg + r) * M;
             for (int t = 0; t < ne; ++t) {
                 const float* L = sL + t * tab;
                 float dist = sBase[t];
@@ -310,7 +371,9 @@ void launch_pq_base(const float* q, int nq, int dim, const float* cent, const in
 
 template <int PASS>
 static void launch_adc_p(const AdcParams& p, int grid, size_t lds, hipStream_t s) {
-    switch (p.M) {
+    // the specialised kernels hold 64 / M query slots
+    const int M = p.tq == adc_tile_queries(p.M) ? p.M : 0;
+    switch (M) {
         case 8: adc_scan_kernel<PASS, 8><<<grid, 256, lds, s>>>(p); break;
         case 16: adc_scan_kernel<PASS, 16><<<grid, 256, lds, s>>>(p); break;
         case 32: adc_scan_kernel<PASS, 32><<<grid, 256, lds, s>>>(p); break;
