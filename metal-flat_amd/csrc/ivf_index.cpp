@@ -127,7 +127,7 @@ struct IvfIndex::Impl {
 
     // per-search workspace
     DevBuf qin, outIds, outVals, qbuf, qh, qnorm, qrm, probe, pos, posOut, cand, cnt;
-    DevBuf tauAk, tauAi, tauKk, tauKi, status;
+    DevBuf tauAk, tauAi, tauKk, tauKi, tauRk, tauRi, status;
     DevBuf cQ, cQn, cTk, cTi, cIdx, cProbe, cPos;
     DevBuf lut, base, cLut, cBase, shortIds, rrCand, rrCnt, rrSel;
     IvfWorkTable wt;
@@ -402,6 +402,24 @@ struct IvfIndex::Impl {
             sp.tau_k_key = tauAk.as<float>(); sp.tau_k_id = tauAi.as<int>();
             sp.expect = std::min(sr, std::max(maxCell, 1));
             launch_select(sp, s);
+            if (pq() && maxCell > sr) {
+                // A2 (PQ): each query's nearest cell in full under A's bound,
+                // one region of capB rows (rows past it are dropped: the k-th
+                // of any k stored rows is still a bound); the smaller bound
+                // stays. ADC keys repeat where rows share codes, so a sample
+                // of a large cell can miss a whole group of equal keys and
+                // leave a bound that admits most probed rows; A2 costs one
+                // more scan of the nearest cell.
+                const int cr = capB(k, nprobe);
+                tauRk.ensure((size_t)mb * 4); tauRi.ensure((size_t)mb * 4);
+                wt.build(probe.as<int>(), mb, nprobe, 1, nlist, dCellOrder.as<int>(), narrowMax(), s);
+                scanPass(kPassSample, mb, 1, nprobe, 1, cr, qr, tauAk.as<float>(), tauAi.as<int>(), pos.as<int>(), s);
+                SelectParams sr2 = selectParams(mb, 1, cr, k);
+                sr2.tau_k_key = tauRk.as<float>(); sr2.tau_k_id = tauRi.as<int>();
+                sr2.expect = cr;
+                launch_select(sr2, s);
+                launch_tau_min(tauAk.as<float>(), tauAi.as<int>(), tauRk.as<float>(), tauRi.as<int>(), mb, s);
+            }
         }
         // B: every probed cell under the bound
         const int cb = capB(k, nprobe);
@@ -414,6 +432,32 @@ struct IvfIndex::Impl {
         wt.build(probe.as<int>(), mb, nprobe, nprobe, nlist, dCellOrder.as<int>(), narrowMax(), s);
         scanPass(kPassFull, mb, nprobe, nprobe, nprobe + 1, cb, qr, tauAk.as<float>(), tauAi.as<int>(),
                  pos.as<int>(), s, true);
+        if (std::getenv("MFLAT_TRACE")) {
+            std::vector<int> c((size_t)mb * (nprobe + 1));
+            HIPC(hipMemcpyAsync(c.data(), cnt.p, c.size() * sizeof(int), hipMemcpyDeviceToHost, s));
+            HIPC(hipStreamSynchronize(s));
+            int64_t tot = 0, spilt = 0;
+            std::vector<int64_t> perq((size_t)mb, 0);
+            for (size_t i = 0; i < c.size(); ++i) {
+                tot += c[i];
+                perq[i / (size_t)(nprobe + 1)] += c[i];
+                if (i % (size_t)(nprobe + 1) == (size_t)nprobe) spilt += c[i];
+            }
+            const int worst = (int)(std::max_element(perq.begin(), perq.end()) - perq.begin());
+            float wk = 0.0f;
+            int wi = 0;
+            HIPC(hipMemcpyAsync(&wk, tauAk.as<float>() + worst, 4, hipMemcpyDeviceToHost, s));
+            HIPC(hipMemcpyAsync(&wi, tauAi.as<int>() + worst, 4, hipMemcpyDeviceToHost, s));
+            HIPC(hipStreamSynchronize(s));
+            std::fprintf(stderr, "[mflat trace] ivf: most survivors at batch query %d, bound (%g, %d)\n", worst,
+                         (double)wk, wi);
+            std::sort(perq.begin(), perq.end());
+            std::fprintf(stderr,
+                         "[mflat trace] ivf: full pass stored %.1f survivors per query (%.1f spilled; median %lld, "
+                         "p99 %lld, max %lld), k %d\n",
+                         (double)tot / mb, (double)spilt / mb, (long long)perq[(size_t)mb / 2],
+                         (long long)perq[(size_t)mb * 99 / 100], (long long)perq[(size_t)mb - 1], k);
+        }
         {
             SelectParams sp = selectParams(mb, nprobe + 1, cb, k);
             sp.out_ids = posIds; sp.out_vals = oVals;

@@ -141,7 +141,9 @@ __global__ void ivf_work_kernel(const int* __restrict__ cellOrder, const int* __
                                 const int* __restrict__ eStart, const int* __restrict__ tEndW,
                                 const int* __restrict__ tEndN, int nlist, int W, int narrowMax,
                                 int4* __restrict__ work, int4* __restrict__ workN, int* __restrict__ nwork) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    // one wave per cell: its lanes write the cell's items
+    const int i = blockIdx.x * (blockDim.x / 64) + (int)(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     if (i >= nlist) return;
     const int c = cellOrder[i];
     const int e0 = eStart[c];
@@ -149,12 +151,12 @@ __global__ void ivf_work_kernel(const int* __restrict__ cellOrder, const int* __
     int nw, nn;
     ivf_split(cnt, W, narrowMax, nw, nn);
     const int t0 = tEndW[i] - nw;
-    for (int t = 0; t < nw; ++t) work[t0 + t] = make_int4(c, e0 + t * W, min(W, cnt - t * W), 0);
+    for (int t = lane; t < nw; t += 64) work[t0 + t] = make_int4(c, e0 + t * W, min(W, cnt - t * W), 0);
     const int n0 = tEndN[i] - nn;
     const int base = nw * W;
-    for (int t = 0; t < nn; ++t)
+    for (int t = lane; t < nn; t += 64)
         workN[n0 + t] = make_int4(c, e0 + base + t * kIvfNarrow, min(kIvfNarrow, cnt - base - t * kIvfNarrow), 0);
-    if (i == nlist - 1) {
+    if (i == nlist - 1 && lane == 0) {
         nwork[0] = tEndW[i];
         nwork[1] = tEndN[i];
     }
@@ -326,8 +328,8 @@ void IvfWorkTable::build(const int* probe, int m, int np, int ranks, int nlist, 
     check(hipcub::DeviceScan::InclusiveSum(temp, t, (const int*)tiles, tEnd, nlist, s), "InclusiveSum");
     t = tempBytes;
     check(hipcub::DeviceScan::InclusiveSum(temp, t, (const int*)tilesN, tEndN, nlist, s), "InclusiveSum");
-    ivf_work_kernel<<<(nlist + 255) / 256, 256, 0, s>>>(cellOrder, eEnd, eStart, tEnd, tEndN, nlist, wideW, narrowMax,
-                                                         work, workN, nwork);
+    ivf_work_kernel<<<(nlist + 3) / 4, 256, 0, s>>>(cellOrder, eEnd, eStart, tEnd, tEndN, nlist, wideW, narrowMax,
+                                                     work, workN, nwork);
     check(hipGetLastError(), "ivf_work");
     prof_end(tok, s);
 }

@@ -1349,7 +1349,15 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
         if (inLds) {
             for (int e = tid; e < c; e += 256) f(sBuf[e]);
         } else {
-            for (int e = tid; e < c; e += 256) f(fetch(e));
+            // eight candidates per thread in flight (offset searches and loads)
+            for (int e0 = tid; e0 < c; e0 += 8 * 256) {
+                uint64_t v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = e0 + u * 256 < c ? fetch(e0 + u * 256) : 0ull;
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (e0 + u * 256 < c) f(v[u]);
+            }
         }
     };
 

@@ -33,16 +33,46 @@ static int grid_of(int64_t n, int block, int cap = 65536) {
     return (int)(g < 1 ? 1 : g > cap ? cap : g);
 }
 
-// fp32 restatements, no fused multiply-add (reference src/Distance.h:26-37)
+// fp32 restatements, no fused multiply-add (reference src/Distance.h:26-37);
+// 16-byte aligned operands of a length divisible by 4 load as float4, the
+// terms still accumulate one at a time in ascending order.
+__device__ __forceinline__ bool vec4_ok(const float* a, const float* b, int n) {
+    return ((((uintptr_t)a | (uintptr_t)b) & 15u) == 0) && (n & 3) == 0;
+}
 __device__ __forceinline__ float dot_seq(const float* a, const float* b, int n) {
 #pragma clang fp contract(off)
     float acc = 0.0f;
+    if (vec4_ok(a, b, n)) {
+        const float4* a4 = (const float4*)a;
+        const float4* b4 = (const float4*)b;
+        for (int i = 0; i < n / 4; ++i) {
+            const float4 x = a4[i], y = b4[i];
+            acc += x.x * y.x;
+            acc += x.y * y.y;
+            acc += x.z * y.z;
+            acc += x.w * y.w;
+        }
+        return acc;
+    }
     for (int i = 0; i < n; ++i) acc += a[i] * b[i];
     return acc;
 }
 __device__ __forceinline__ float sql2_seq(const float* a, const float* b, int n) {
 #pragma clang fp contract(off)
     float acc = 0.0f;
+    if (vec4_ok(a, b, n)) {
+        const float4* a4 = (const float4*)a;
+        const float4* b4 = (const float4*)b;
+        for (int i = 0; i < n / 4; ++i) {
+            const float4 x = a4[i], y = b4[i];
+            const float e0 = x.x - y.x, e1 = x.y - y.y, e2 = x.z - y.z, e3 = x.w - y.w;
+            acc += e0 * e0;
+            acc += e1 * e1;
+            acc += e2 * e2;
+            acc += e3 * e3;
+        }
+        return acc;
+    }
     for (int i = 0; i < n; ++i) {
         const float e = a[i] - b[i];
         acc += e * e;
