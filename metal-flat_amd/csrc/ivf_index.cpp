@@ -372,7 +372,11 @@ struct IvfIndex::Impl {
             const int v = std::atoi(e);
             if (v >= 1) return v;
         }
-        return nprobe == 1 ? capR() : pow2ceil(std::max(4 * k, 256));
+        if (nprobe == 1) return capR();
+        // PQ: the bound is the k-th of the whole nearest cell (A covers it, or
+        // A2 does), so that cell's region holds at most k survivors and the
+        // others rarely more than a few
+        return pq() ? pow2ceil(std::max(2 * k, 128)) : pow2ceil(std::max(4 * k, 256));
     }
 
     // Search mb staged queries (qbuf / qh, norms in qnorm, probes in probe).

@@ -164,6 +164,7 @@ __global__ void pq_base_kernel(const float* __restrict__ q, int nq, int dim, con
 }
 
 constexpr int kAdcMaxTq = 16;
+constexpr int kAdcBlock = 512;   // threads of an ADC work item (M x 64 float4 of a table: a multiple of it for M >= 8)
 
 int adc_tile_queries(int M) {
     const int t = (64 * 1024) / (M * kPqKsub * (int)sizeof(float));
@@ -181,7 +182,7 @@ __device__ __forceinline__ float lds_at(const float* base, uint32_t a, int off) 
 // query slots unrolled: the M byte offsets of a row are computed once and
 // serve every query), 0: any M (runtime loops)
 template <int PASS, int MV>
-__global__ void __launch_bounds__(256) adc_scan_kernel(AdcParams p) {
+__global__ void __launch_bounds__(kAdcBlock) adc_scan_kernel(AdcParams p) {
     extern __shared__ float sL[];   // [tq][M][256]
     __shared__ int sQi[kAdcMaxTq], sReg[kAdcMaxTq], sPos[kAdcMaxTq], sCnt[kAdcMaxTq], sTi[kAdcMaxTq];
     __shared__ float sBase[kAdcMaxTq], sTk[kAdcMaxTq];
@@ -212,24 +213,25 @@ __global__ void __launch_bounds__(256) adc_scan_kernel(AdcParams p) {
     if constexpr (MV > 0) {
         // every load of the thread's share in flight at once: PER float4 of
         // the cross table, reused by the TQ queries (empty slots copy slot 0's)
-        constexpr int TQ = 64 / MV, PER = MV / 4;
+        constexpr int TQ = 64 / MV, PER = MV * 64 / kAdcBlock;
+        static_assert(PER >= 1 && PER * kAdcBlock == MV * 64, "table share per thread");
         float4 tv[PER], lv[TQ][PER];
 #pragma unroll
-        for (int j = 0; j < PER; ++j) tv[j] = Tc[tid + j * 256];
+        for (int j = 0; j < PER; ++j) tv[j] = Tc[tid + j * kAdcBlock];
 #pragma unroll
         for (int t = 0; t < TQ; ++t) {
             const float4* lq = (const float4*)(p.lut + (int64_t)sQi[t < ne ? t : 0] * tab);
 #pragma unroll
-            for (int j = 0; j < PER; ++j) lv[t][j] = lq[tid + j * 256];
+            for (int j = 0; j < PER; ++j) lv[t][j] = lq[tid + j * kAdcBlock];
         }
 #pragma unroll
         for (int t = 0; t < TQ; ++t)
 #pragma unroll
-            for (int j = 0; j < PER; ++j) sL4[t * tab4 + tid + j * 256] = add4(lv[t][j], tv[j]);
+            for (int j = 0; j < PER; ++j) sL4[t * tab4 + tid + j * kAdcBlock] = add4(lv[t][j], tv[j]);
     } else {
         for (int t = 0; t < ne; ++t) {
             const float4* lq = (const float4*)(p.lut + (int64_t)sQi[t] * tab);
-            for (int o = tid; o < tab4; o += 256) sL4[t * tab4 + o] = add4(lq[o], Tc[o]);
+            for (int o = tid; o < tab4; o += kAdcBlock) sL4[t * tab4 + o] = add4(lq[o], Tc[o]);
         }
     }
     __syncthreads();
@@ -267,11 +269,11 @@ __global__ void __launch_bounds__(256) adc_scan_kernel(AdcParams p) {
         };
         uint32_t nx[NW];
         if (tid < rows) load_codes(tid, nx);
-        for (int r = tid; r < rows; r += 256) {
+        for (int r = tid; r < rows; r += kAdcBlock) {
             uint32_t cw[NW];
 #pragma unroll
             for (int w = 0; w < NW; ++w) cw[w] = nx[w];
-            if (r + 256 < rows) load_codes(r + 256, nx);
+            if (r + kAdcBlock < rows) load_codes(r + kAdcBlock, nx);
             uint32_t a[MV];   // byte offset of the row's entry in table m (without m * 1 KiB)
 #pragma unroll
             for (int m = 0; m < MV; ++m) a[m] = ((cw[m >> 2] >> ((m & 3) * 8)) & 255u) * 4u;
@@ -292,7 +294,7 @@ __global__ void __launch_bounds__(256) adc_scan_kernel(AdcParams p) {
             }
         }
     } else {
-        for (int r = tid; r < rows; r += 256) {
+        for (int r = tid; r < rows; r += kAdcBlock) {
             const uint8_t* code = p.codes + (int64_t)(beg + r) * M;
             for (int t = 0; t < ne; ++t) {
                 const float* L = sL + t * tab;
@@ -307,22 +309,58 @@ __global__ void __launch_bounds__(256) adc_scan_kernel(AdcParams p) {
     if (tid < ne) p.cnt[sReg[tid]] = p.spill && sCnt[tid] > p.cap ? p.cap : sCnt[tid];
 }
 
-__global__ void rerank_keys_kernel(const float* __restrict__ q, int nq, int dim, const float* __restrict__ full,
-                                   const int* __restrict__ shortIds, int kRun, int metric, uint2* __restrict__ cand,
-                                   int* __restrict__ cnt) {
+// One block per 256 (query, shortlist slot) pairs. The rows go through LDS
+// in chunks of 32 columns (coalesced: 32 lanes read one row's chunk), padded
+// to 33 floats a row so the summing threads -- one per pair, columns in
+// ascending order across the chunks -- read distinct banks.
+constexpr int kRrCols = 32;
+__global__ void __launch_bounds__(256) rerank_keys_kernel(const float* __restrict__ q, int nq, int dim,
+                                                          const float* __restrict__ full,
+                                                          const int* __restrict__ shortIds, int kRun, int metric,
+                                                          uint2* __restrict__ cand, int* __restrict__ cnt) {
+#pragma clang fp contract(off)
+    __shared__ float sX[256 * (kRrCols + 1)];
+    __shared__ int sId[256];
     const int64_t total = (int64_t)nq * kRun;
-    for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
-         e += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t i = e / kRun;
-        const int j = (int)(e - i * kRun);
-        const int id = shortIds[e];
-        if (id < 0) continue;
-        const float* qq = q + i * dim;
-        const float* x = full + (int64_t)id * dim;
-        const float key = metric == 0 ? sql2_seq(qq, x, dim) : -dot_seq(qq, x, dim);
-        cand[e] = make_uint2(__float_as_uint(key + 0.0f), (unsigned)j);
-        if (j == kRun - 1 || shortIds[e + 1] < 0) cnt[i] = j + 1;   // padding sits at the end
+    const int64_t e0 = (int64_t)blockIdx.x * 256;
+    const int tid = threadIdx.x;
+    const int64_t e = e0 + tid;
+    sId[tid] = e < total ? shortIds[e] : -1;
+    const int64_t i = e < total ? e / kRun : 0;
+    const float* qq = q + i * dim;
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < dim; c0 += kRrCols) {
+        const int w = min(kRrCols, dim - c0);
+        float qv[kRrCols];   // the query's chunk, loaded in one batch
+#pragma unroll
+        for (int j = 0; j < kRrCols; ++j) qv[j] = j < w ? qq[c0 + j] : 0.0f;
+        __syncthreads();   // sId visible; the previous chunk consumed
+#pragma unroll 8
+        for (int f = tid; f < 256 * kRrCols; f += 256) {
+            const int r = f / kRrCols, col = f - r * kRrCols;
+            const int id = sId[r];
+            sX[r * (kRrCols + 1) + col] = (id >= 0 && col < w) ? full[(int64_t)id * dim + c0 + col] : 0.0f;
+        }
+        __syncthreads();
+        const float* x = sX + tid * (kRrCols + 1);
+        if (metric == 0) {
+#pragma unroll
+            for (int j = 0; j < kRrCols; ++j)
+                if (j < w) {
+                    const float d = qv[j] - x[j];
+                    acc += d * d;
+                }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kRrCols; ++j)
+                if (j < w) acc += qv[j] * x[j];
+        }
     }
+    if (e >= total || sId[tid] < 0) return;
+    const int j = (int)(e - i * kRun);
+    const float key = metric == 0 ? acc : -acc;
+    cand[e] = make_uint2(__float_as_uint(key + 0.0f), (unsigned)j);
+    if (j == kRun - 1 || shortIds[e + 1] < 0) cnt[i] = j + 1;   // padding sits at the end
 }
 
 __global__ void count_zero_kernel(int* __restrict__ cnt, int n) {
@@ -404,11 +442,11 @@ static void launch_adc_p(const AdcParams& p, int grid, size_t lds, hipStream_t s
     // the specialised kernels hold 64 / M query slots
     const int M = p.tq == adc_tile_queries(p.M) ? p.M : 0;
     switch (M) {
-        case 8: adc_scan_kernel<PASS, 8><<<grid, 256, lds, s>>>(p); break;
-        case 16: adc_scan_kernel<PASS, 16><<<grid, 256, lds, s>>>(p); break;
-        case 32: adc_scan_kernel<PASS, 32><<<grid, 256, lds, s>>>(p); break;
-        case 64: adc_scan_kernel<PASS, 64><<<grid, 256, lds, s>>>(p); break;
-        default: adc_scan_kernel<PASS, 0><<<grid, 256, lds, s>>>(p); break;
+        case 8: adc_scan_kernel<PASS, 8><<<grid, kAdcBlock, lds, s>>>(p); break;
+        case 16: adc_scan_kernel<PASS, 16><<<grid, kAdcBlock, lds, s>>>(p); break;
+        case 32: adc_scan_kernel<PASS, 32><<<grid, kAdcBlock, lds, s>>>(p); break;
+        case 64: adc_scan_kernel<PASS, 64><<<grid, kAdcBlock, lds, s>>>(p); break;
+        default: adc_scan_kernel<PASS, 0><<<grid, kAdcBlock, lds, s>>>(p); break;
     }
 }
 
@@ -445,7 +483,9 @@ void launch_rerank_keys(const float* q, int nq, int dim, const float* full, cons
     void* tok;
     prof_begin(kFamPrep, s, &tok);
     count_zero_kernel<<<(nq + 255) / 256, 256, 0, s>>>(cnt, nq);
-    rerank_keys_kernel<<<grid_of((int64_t)nq * kRun, 256), 256, 0, s>>>(q, nq, dim, full, shortIds, kRun, metric,
+    const int64_t blocks = ((int64_t)nq * kRun + 255) / 256;
+    if (blocks > 0x7FFFFFFF) throw std::runtime_error("rerank_keys: too many pairs");
+    rerank_keys_kernel<<<(unsigned)blocks, 256, 0, s>>>(q, nq, dim, full, shortIds, kRun, metric,
                                                                       cand, cnt);
     prof_end(tok, s);
     check(hipGetLastError(), "rerank_keys");
