@@ -407,18 +407,18 @@ struct IvfIndex::Impl {
             sp.expect = std::min(sr, std::max(maxCell, 1));
             launch_select(sp, s);
             if (pq() && maxCell > sr) {
-                // A2 (PQ): each query's nearest cell in full under A's bound,
-                // one region of capB rows (rows past it are dropped: the k-th
-                // of any k stored rows is still a bound); the smaller bound
-                // stays. ADC keys repeat where rows share codes, so a sample
-                // of a large cell can miss a whole group of equal keys and
-                // leave a bound that admits most probed rows; A2 costs one
-                // more scan of the nearest cell.
+                // A2 (PQ): A's cells in full under A's bound (A's work table),
+                // one region of capB rows per (query, rank) (rows past it are
+                // dropped: the k-th of any k stored rows is still a bound); the
+                // smaller bound stays. ADC keys repeat where rows share codes,
+                // so a sample of a large cell can miss a whole group of equal
+                // keys and leave a bound that admits most probed rows; A2 costs
+                // one more scan of the nearest cells.
                 const int cr = capB(k, nprobe);
                 tauRk.ensure((size_t)mb * 4); tauRi.ensure((size_t)mb * 4);
-                wt.build(probe.as<int>(), mb, nprobe, 1, nlist, dCellOrder.as<int>(), narrowMax(), s);
-                scanPass(kPassSample, mb, 1, nprobe, 1, cr, qr, tauAk.as<float>(), tauAi.as<int>(), pos.as<int>(), s);
-                SelectParams sr2 = selectParams(mb, 1, cr, k);
+                scanPass(kPassSample, mb, ra, nprobe, ra, cr, qr, tauAk.as<float>(), tauAi.as<int>(), pos.as<int>(),
+                         s);
+                SelectParams sr2 = selectParams(mb, ra, cr, k);
                 sr2.tau_k_key = tauRk.as<float>(); sr2.tau_k_id = tauRi.as<int>();
                 sr2.expect = cr;
                 launch_select(sr2, s);

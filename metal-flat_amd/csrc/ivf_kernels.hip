@@ -199,6 +199,138 @@ void launch_gather_i32(const int* src, const int* idx, int n, int width, int* ds
     check(hipGetLastError(), "gather_i32");
 }
 
+// Counting-sort build of the work table (nlist <= kHistCells): block b
+// counts the entries [b * chunk, (b + 1) * chunk) per cell in LDS into
+// H[c * G + b]; an exclusive scan of H (cell-major) gives each block its first
+// slot in every cell's run; the scatter then places the entries (their order
+// within a cell follows LDS atomics). Three launches where a radix sort of the
+// same keys takes a merge cascade of some twenty.
+constexpr int kHistCells = 32768;
+constexpr int kHistBlock = 1024;
+
+__device__ __forceinline__ int ivf_entry_cell(const int* __restrict__ probe, int np, int ranks, int nlist,
+                                              const int* __restrict__ pos, int posLimit, int64_t i, int& e) {
+    const int q = (int)(i / ranks);
+    e = q * np + (int)(i - (int64_t)q * ranks);
+    const int c = probe[e];
+    return (c >= 0 && c < nlist && (pos == nullptr || pos[e] < posLimit)) ? c : -1;
+}
+
+__global__ void __launch_bounds__(kHistBlock) ivf_hist_kernel(const int* __restrict__ probe, int m, int np,
+                                                              int ranks, int nlist, const int* __restrict__ pos,
+                                                              int posLimit, int chunk, int G, int* __restrict__ H) {
+    extern __shared__ int sH[];
+    for (int c = threadIdx.x; c < nlist; c += kHistBlock) sH[c] = 0;
+    __syncthreads();
+    const int64_t n = (int64_t)m * ranks;
+    const int64_t i0 = (int64_t)blockIdx.x * chunk;
+    const int64_t i1 = i0 + chunk < n ? i0 + chunk : n;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += kHistBlock) {
+        int e;
+        const int c = ivf_entry_cell(probe, np, ranks, nlist, pos, posLimit, i, e);
+        if (c >= 0) atomicAdd(&sH[c], 1);
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < nlist; c += kHistBlock) H[(int64_t)c * G + blockIdx.x] = sH[c];
+}
+
+__global__ void __launch_bounds__(kHistBlock) ivf_scatter_kernel(const int* __restrict__ probe, int m, int np,
+                                                                 int ranks, int nlist, const int* __restrict__ pos,
+                                                                 int posLimit, int chunk, int G,
+                                                                 const int* __restrict__ H, const int* __restrict__ O,
+                                                                 int* __restrict__ ent, int* __restrict__ eStart,
+                                                                 int* __restrict__ eEnd) {
+    extern __shared__ int sCur[];
+    for (int c = threadIdx.x; c < nlist; c += kHistBlock) sCur[c] = O[(int64_t)c * G + blockIdx.x];
+    __syncthreads();
+    const int64_t n = (int64_t)m * ranks;
+    const int64_t i0 = (int64_t)blockIdx.x * chunk;
+    const int64_t i1 = i0 + chunk < n ? i0 + chunk : n;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += kHistBlock) {
+        int e;
+        const int c = ivf_entry_cell(probe, np, ranks, nlist, pos, posLimit, i, e);
+        if (c >= 0) ent[atomicAdd(&sCur[c], 1)] = e;
+    }
+    if (blockIdx.x == 0)
+        for (int c = threadIdx.x; c < nlist; c += kHistBlock) {
+            const int64_t last = (int64_t)c * G + G - 1;
+            eStart[c] = O[(int64_t)c * G];
+            eEnd[c] = O[last] + H[last];
+        }
+}
+
+// One block: every cell's item counts (ivf_split), their exclusive sums in
+// cellOrder order (baseW / baseN), then one wave per cell writes its items.
+__global__ void __launch_bounds__(kHistBlock) ivf_items_kernel(const int* __restrict__ cellOrder,
+                                                               const int* __restrict__ eStart,
+                                                               const int* __restrict__ eEnd, int nlist, int W,
+                                                               int narrowMax, int* __restrict__ baseW,
+                                                               int* __restrict__ baseN, int4* __restrict__ work,
+                                                               int4* __restrict__ workN, int* __restrict__ nwork) {
+    constexpr int kWaves = kHistBlock / 64;
+    __shared__ int sW[kWaves], sN[kWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int per = (nlist + kHistBlock - 1) / kHistBlock;
+    const int i0 = min(nlist, tid * per), i1 = min(nlist, i0 + per);
+    int sw = 0, sn = 0;
+    for (int i = i0; i < i1; ++i) {
+        const int c = cellOrder[i];
+        int w, nn;
+        ivf_split(eEnd[c] - eStart[c], W, narrowMax, w, nn);
+        sw += w;
+        sn += nn;
+    }
+    int xw = sw, xn = sn;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int a = __shfl_up(xw, off, 64), b = __shfl_up(xn, off, 64);
+        if (lane >= off) {
+            xw += a;
+            xn += b;
+        }
+    }
+    if (lane == 63) {
+        sW[wave] = xw;
+        sN[wave] = xn;
+    }
+    __syncthreads();
+    int bw = xw - sw, bn = xn - sn, tw = 0, tn = 0;
+    for (int w = 0; w < kWaves; ++w) {
+        if (w < wave) {
+            bw += sW[w];
+            bn += sN[w];
+        }
+        tw += sW[w];
+        tn += sN[w];
+    }
+    for (int i = i0; i < i1; ++i) {
+        const int c = cellOrder[i];
+        int w, nn;
+        ivf_split(eEnd[c] - eStart[c], W, narrowMax, w, nn);
+        baseW[i] = bw;
+        baseN[i] = bn;
+        bw += w;
+        bn += nn;
+    }
+    if (tid == 0) {
+        nwork[0] = tw;
+        nwork[1] = tn;
+    }
+    __threadfence();
+    __syncthreads();
+    for (int i = wave; i < nlist; i += kWaves) {
+        const int c = cellOrder[i];
+        const int e0 = eStart[c];
+        const int cnt = eEnd[c] - e0;
+        int nw, nn;
+        ivf_split(cnt, W, narrowMax, nw, nn);
+        const int t0 = baseW[i];
+        for (int t = lane; t < nw; t += 64) work[t0 + t] = make_int4(c, e0 + t * W, min(W, cnt - t * W), 0);
+        const int n0 = baseN[i], base = nw * W;
+        for (int t = lane; t < nn; t += 64)
+            workN[n0 + t] = make_int4(c, e0 + base + t * kIvfNarrow, min(kIvfNarrow, cnt - base - t * kIvfNarrow), 0);
+    }
+}
+
 void launch_ivf_positions(const int* probe, int m, int np, const int* cellSize, int* pos, hipStream_t s) {
     if (m <= 0) return;
     void* tok;
@@ -240,12 +372,13 @@ IvfWorkTable::~IvfWorkTable() { release(); }
 void IvfWorkTable::release() {
     for (void** p : {(void**)&ent, (void**)&work, (void**)&workN, (void**)&nwork, (void**)&keysIn, (void**)&keysOut,
                      (void**)&valsIn, (void**)&eEnd, (void**)&eStart, (void**)&tiles, (void**)&tEnd,
-                     (void**)&tilesN, (void**)&tEndN, &temp}) {
+                     (void**)&tilesN, (void**)&tEndN, (void**)&hist, (void**)&histOff, &temp}) {
         if (*p) (void)hipFree(*p);
         *p = nullptr;
     }
     tempBytes = 0;
     capE = capWork = capWorkN = capCells = 0;
+    capHist = 0;
 }
 
 void IvfWorkTable::reserve(int ne, int mw, int mn, int nlist) {
@@ -291,7 +424,51 @@ void IvfWorkTable::build(const int* probe, int m, int np, int ranks, int nlist, 
     const int mn = maxWorkNarrow(m, ranks, nlist, narrowMax);
     reserve(ne, mw, mn, nlist);
 
-
+    if (nlist <= kHistCells) {
+        const int chunk = (int)std::max<int64_t>(4096, (ne64 + 1023) / 1024);
+        const int G = (int)((ne64 + chunk - 1) / chunk);
+        const int64_t nh = (int64_t)nlist * G;
+        if (nh > capHist) {
+            for (int** p : {&hist, &histOff}) {
+                if (*p) (void)hipFree(*p);
+                *p = nullptr;
+            }
+            for (int** p : {&hist, &histOff}) check(hipMalloc((void**)p, (size_t)nh * sizeof(int)), "hipMalloc(hist)");
+            capHist = nh;
+        }
+        size_t need = 0;
+        check(hipcub::DeviceScan::ExclusiveSum(nullptr, need, (const int*)hist, histOff, (int)nh, s),
+              "ExclusiveSum (size)");
+        need = std::max(need, (size_t)16);
+        if (need > tempBytes) {
+            if (temp) (void)hipFree(temp);
+            temp = nullptr;
+            check(hipMalloc(&temp, need), "hipMalloc(ivf temp)");
+            tempBytes = need;
+        }
+        static const bool attr = [] {
+            for (const void* f : {(const void*)ivf_hist_kernel, (const void*)ivf_scatter_kernel})
+                if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kHistCells * 4) != hipSuccess)
+                    throw std::runtime_error("ivf work table: cannot raise the dynamic LDS limit");
+            return true;
+        }();
+        (void)attr;
+        const size_t lds = (size_t)nlist * sizeof(int);
+        void* tok;
+        prof_begin(kFamPrep, s, &tok);
+        ivf_hist_kernel<<<G, kHistBlock, lds, s>>>(probe, m, np, ranks, nlist, pos, posLimit, chunk, G, hist);
+        check(hipGetLastError(), "ivf_hist");
+        size_t t = tempBytes;
+        check(hipcub::DeviceScan::ExclusiveSum(temp, t, (const int*)hist, histOff, (int)nh, s), "ExclusiveSum");
+        ivf_scatter_kernel<<<G, kHistBlock, lds, s>>>(probe, m, np, ranks, nlist, pos, posLimit, chunk, G, hist,
+                                                      histOff, ent, eStart, eEnd);
+        check(hipGetLastError(), "ivf_scatter");
+        ivf_items_kernel<<<1, kHistBlock, 0, s>>>(cellOrder, eStart, eEnd, nlist, wideW, narrowMax, tEnd, tEndN, work,
+                                                  workN, nwork);
+        check(hipGetLastError(), "ivf_items");
+        prof_end(tok, s);
+        return;
+    }
 
     int bits = 1;
     while ((1 << bits) <= nlist) ++bits;   // keys 0 .. nlist

@@ -28,7 +28,8 @@ constexpr int kIvfNarrow = 32;   // entries per narrow work item (one 32-query b
 
 // Work table of one fine-scan pass over the entries e = q * np + r of queries
 // q < m and ranks r < ranks (ranks = 1: the nearest cell only; ranks = np: all):
-//   ent        the entries sorted by (cell, e) -- a stable sort by cell
+//   ent        the entries grouped by cell (within a cell in no particular
+//              order on the device; ascending e from buildHost)
 //   work[w]    wide items (cell, first entry, entries <= wideW, 0): each
 //              cell's entries in runs of wideW, cells in the order cellOrder
 //              gives (decreasing size)
@@ -68,6 +69,9 @@ private:
     int* tEnd = nullptr;
     int* tilesN = nullptr;
     int* tEndN = nullptr;
+    int* hist = nullptr;      // counting-sort build: per-block cell counts, cell-major
+    int* histOff = nullptr;   // ... and their exclusive sums
+    int64_t capHist = 0;
     void* temp = nullptr;
     size_t tempBytes = 0;
     std::vector<int> hEnt, hCnt, hStart;
