@@ -59,17 +59,26 @@ __global__ void gather_i32_kernel(const int* __restrict__ src, const int* __rest
     }
 }
 
-// one thread per query: an exclusive running sum over its probe ranks
-__global__ void ivf_positions_kernel(const int* __restrict__ probe, int m, int np, const int* __restrict__ cellSize,
-                                     int* __restrict__ pos) {
-    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+// one wave per query: an exclusive running sum over its probe ranks, 64
+// ranks at a time
+__global__ void __launch_bounds__(256) ivf_positions_kernel(const int* __restrict__ probe, int m, int np,
+                                                            const int* __restrict__ cellSize, int* __restrict__ pos) {
+    const int q = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     if (q >= m) return;
     const int64_t b = (int64_t)q * np;
     int run = 0;
-    for (int r = 0; r < np; ++r) {
-        pos[b + r] = run;
-        const int c = probe[b + r];
-        run += c >= 0 ? cellSize[c] : 0;   // -1: no cell (a query without finite distances)
+    for (int r0 = 0; r0 < np; r0 += 64) {
+        const int r = r0 + lane;
+        const int c = r < np ? probe[b + r] : -1;
+        const int v = c >= 0 ? cellSize[c] : 0;   // -1: no cell (a query without finite distances)
+        int x = v;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int t = __shfl_up(x, off, 64);
+            if (lane >= off) x += t;
+        }
+        if (r < np) pos[b + r] = run + x - v;
+        run += __shfl(x, 63, 64);
     }
 }
 
@@ -204,7 +213,7 @@ void launch_gather_i32(const int* src, const int* idx, int n, int width, int* ds
 // H[c * G + b]; an exclusive scan of H (cell-major) gives each block its first
 // slot in every cell's run; the scatter then places the entries (their order
 // within a cell follows LDS atomics). Three launches where a radix sort of the
-// same keys takes a merge cascade of some twenty.
+// same keys takes a merge cascade of some twenty; two more write the items.
 constexpr int kHistCells = 32768;
 constexpr int kHistBlock = 1024;
 
@@ -259,14 +268,13 @@ __global__ void __launch_bounds__(kHistBlock) ivf_scatter_kernel(const int* __re
         }
 }
 
-// One block: every cell's item counts (ivf_split), their exclusive sums in
-// cellOrder order (baseW / baseN), then one wave per cell writes its items.
-__global__ void __launch_bounds__(kHistBlock) ivf_items_kernel(const int* __restrict__ cellOrder,
-                                                               const int* __restrict__ eStart,
-                                                               const int* __restrict__ eEnd, int nlist, int W,
-                                                               int narrowMax, int* __restrict__ baseW,
-                                                               int* __restrict__ baseN, int4* __restrict__ work,
-                                                               int4* __restrict__ workN, int* __restrict__ nwork) {
+// One block: every cell's item counts (ivf_split) and their inclusive sums in
+// cellOrder order (tEndW / tEndN, as the scans of the radix path give them).
+__global__ void __launch_bounds__(kHistBlock) ivf_tile_sums_kernel(const int* __restrict__ cellOrder,
+                                                                   const int* __restrict__ eStart,
+                                                                   const int* __restrict__ eEnd, int nlist, int W,
+                                                                   int narrowMax, int* __restrict__ tEndW,
+                                                                   int* __restrict__ tEndN) {
     constexpr int kWaves = kHistBlock / 64;
     __shared__ int sW[kWaves], sN[kWaves];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -293,41 +301,19 @@ __global__ void __launch_bounds__(kHistBlock) ivf_items_kernel(const int* __rest
         sN[wave] = xn;
     }
     __syncthreads();
-    int bw = xw - sw, bn = xn - sn, tw = 0, tn = 0;
-    for (int w = 0; w < kWaves; ++w) {
-        if (w < wave) {
-            bw += sW[w];
-            bn += sN[w];
-        }
-        tw += sW[w];
-        tn += sN[w];
+    int bw = xw - sw, bn = xn - sn;
+    for (int w = 0; w < wave; ++w) {
+        bw += sW[w];
+        bn += sN[w];
     }
     for (int i = i0; i < i1; ++i) {
         const int c = cellOrder[i];
         int w, nn;
         ivf_split(eEnd[c] - eStart[c], W, narrowMax, w, nn);
-        baseW[i] = bw;
-        baseN[i] = bn;
         bw += w;
         bn += nn;
-    }
-    if (tid == 0) {
-        nwork[0] = tw;
-        nwork[1] = tn;
-    }
-    __threadfence();
-    __syncthreads();
-    for (int i = wave; i < nlist; i += kWaves) {
-        const int c = cellOrder[i];
-        const int e0 = eStart[c];
-        const int cnt = eEnd[c] - e0;
-        int nw, nn;
-        ivf_split(cnt, W, narrowMax, nw, nn);
-        const int t0 = baseW[i];
-        for (int t = lane; t < nw; t += 64) work[t0 + t] = make_int4(c, e0 + t * W, min(W, cnt - t * W), 0);
-        const int n0 = baseN[i], base = nw * W;
-        for (int t = lane; t < nn; t += 64)
-            workN[n0 + t] = make_int4(c, e0 + base + t * kIvfNarrow, min(kIvfNarrow, cnt - base - t * kIvfNarrow), 0);
+        tEndW[i] = bw;
+        tEndN[i] = bn;
     }
 }
 
@@ -335,7 +321,7 @@ void launch_ivf_positions(const int* probe, int m, int np, const int* cellSize, 
     if (m <= 0) return;
     void* tok;
     prof_begin(kFamPrep, s, &tok);
-    ivf_positions_kernel<<<(m + 255) / 256, 256, 0, s>>>(probe, m, np, cellSize, pos);
+    ivf_positions_kernel<<<(m + 3) / 4, 256, 0, s>>>(probe, m, np, cellSize, pos);
     prof_end(tok, s);
     check(hipGetLastError(), "ivf_positions");
 }
@@ -463,9 +449,11 @@ void IvfWorkTable::build(const int* probe, int m, int np, int ranks, int nlist, 
         ivf_scatter_kernel<<<G, kHistBlock, lds, s>>>(probe, m, np, ranks, nlist, pos, posLimit, chunk, G, hist,
                                                       histOff, ent, eStart, eEnd);
         check(hipGetLastError(), "ivf_scatter");
-        ivf_items_kernel<<<1, kHistBlock, 0, s>>>(cellOrder, eStart, eEnd, nlist, wideW, narrowMax, tEnd, tEndN, work,
-                                                  workN, nwork);
-        check(hipGetLastError(), "ivf_items");
+        ivf_tile_sums_kernel<<<1, kHistBlock, 0, s>>>(cellOrder, eStart, eEnd, nlist, wideW, narrowMax, tEnd, tEndN);
+        check(hipGetLastError(), "ivf_tile_sums");
+        ivf_work_kernel<<<(nlist + 3) / 4, 256, 0, s>>>(cellOrder, eEnd, eStart, tEnd, tEndN, nlist, wideW,
+                                                         narrowMax, work, workN, nwork);
+        check(hipGetLastError(), "ivf_work");
         prof_end(tok, s);
         return;
     }

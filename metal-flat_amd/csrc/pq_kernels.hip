@@ -363,6 +363,64 @@ __global__ void __launch_bounds__(256) rerank_keys_kernel(const float* __restric
     if (j == kRun - 1 || shortIds[e + 1] < 0) cnt[i] = j + 1;   // padding sits at the end
 }
 
+// dim % 4 == 0: one wave per 64 (query, slot) pairs. The 64 shortlist rows
+// load in 64-column blocks as float4 lanes (16 lanes a row, four rows an
+// instruction), go to LDS column-major with a 65-float stride (lane i then
+// reads column j of its row from bank (i + j) mod 32) and each lane sums its
+// pair's columns in ascending order.
+constexpr int kRrBlk = 64;
+__global__ void __launch_bounds__(64) rerank_rows_kernel(const float* __restrict__ q, int nq, int dim,
+                                                         const float* __restrict__ full,
+                                                         const int* __restrict__ shortIds, int kRun, int metric,
+                                                         uint2* __restrict__ cand, int* __restrict__ cnt) {
+#pragma clang fp contract(off)
+    __shared__ float sX[kRrBlk * 65];
+    const int lane = threadIdx.x;
+    const int64_t total = (int64_t)nq * kRun;
+    const int64_t e = (int64_t)blockIdx.x * 64 + lane;
+    const bool live = e < total;
+    const int myId = live ? shortIds[e] : -1;
+    const int64_t i = live ? e / kRun : 0;
+    const float* qq = q + i * dim;
+    const int quarter = lane >> 4, c4 = (lane & 15) * 4;
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < dim; c0 += kRrBlk) {
+        const int w = min(kRrBlk, dim - c0);
+        float4 v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int id = __shfl(myId, 4 * u + quarter, 64);
+            v[u] = (id >= 0 && c4 < w) ? *(const float4*)(full + (int64_t)id * dim + c0 + c4)
+                                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        __syncthreads();   // the previous block's columns are summed
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int row = 4 * u + quarter;
+            sX[(c4 + 0) * 65 + row] = v[u].x;
+            sX[(c4 + 1) * 65 + row] = v[u].y;
+            sX[(c4 + 2) * 65 + row] = v[u].z;
+            sX[(c4 + 3) * 65 + row] = v[u].w;
+        }
+        __syncthreads();
+        if (metric == 0) {
+#pragma unroll 16
+            for (int j = 0; j < w; ++j) {
+                const float d = qq[c0 + j] - sX[j * 65 + lane];
+                acc += d * d;
+            }
+        } else {
+#pragma unroll 16
+            for (int j = 0; j < w; ++j) acc += qq[c0 + j] * sX[j * 65 + lane];
+        }
+    }
+    if (!live || myId < 0) return;
+    const int j = (int)(e - i * kRun);
+    const float key = metric == 0 ? acc : -acc;
+    cand[e] = make_uint2(__float_as_uint(key + 0.0f), (unsigned)j);
+    if (j == kRun - 1 || shortIds[e + 1] < 0) cnt[i] = j + 1;   // padding sits at the end
+}
+
 __global__ void count_zero_kernel(int* __restrict__ cnt, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) cnt[i] = 0;
@@ -483,10 +541,14 @@ void launch_rerank_keys(const float* q, int nq, int dim, const float* full, cons
     void* tok;
     prof_begin(kFamPrep, s, &tok);
     count_zero_kernel<<<(nq + 255) / 256, 256, 0, s>>>(cnt, nq);
-    const int64_t blocks = ((int64_t)nq * kRun + 255) / 256;
-    if (blocks > 0x7FFFFFFF) throw std::runtime_error("rerank_keys: too many pairs");
-    rerank_keys_kernel<<<(unsigned)blocks, 256, 0, s>>>(q, nq, dim, full, shortIds, kRun, metric,
-                                                                      cand, cnt);
+    const int64_t pairs = (int64_t)nq * kRun;
+    if ((pairs + 63) / 64 > 0x7FFFFFFF) throw std::runtime_error("rerank_keys: too many pairs");
+    if (dim % 4 == 0)   // float4 rows (the store is 256-byte aligned)
+        rerank_rows_kernel<<<(unsigned)((pairs + 63) / 64), 64, 0, s>>>(q, nq, dim, full, shortIds, kRun, metric,
+                                                                        cand, cnt);
+    else
+        rerank_keys_kernel<<<(unsigned)((pairs + 255) / 256), 256, 0, s>>>(q, nq, dim, full, shortIds, kRun, metric,
+                                                                           cand, cnt);
     prof_end(tok, s);
     check(hipGetLastError(), "rerank_keys");
 }
