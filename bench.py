@@ -57,6 +57,8 @@ MEASURED_TRAFFIC_BYTES = {
     ("C5", 2_000_000, "f32"): 34.27e9,
     # IVF fine scan (both launches of a search), C2's data, nlist 1000, nprobe 62
     ("IVF", 1000, 62, "f32"): 4.66e9,
+    # IVF-PQ ADC full pass, C2's data, nlist 1000, nprobe 62, m_sub 16 (lookup tables, codes, cross tables)
+    ("IVFPQ", 1000, 62, 16): 10.61e9,
 }
 
 WORKLOADS = {
@@ -278,9 +280,10 @@ def ivfpq_bench(args):
     d = 128, the reference header's example), k = 10 (the reference's IVF-PQ
     serves k <= 64), rerank 16 k (the header's suggestion). A step is one search
     of the whole batch (device pointers). roofline: the ADC fine scan (ivf_scan
-    family) is bound by LDS gathers -- M table reads of 4 bytes per candidate
-    per query; achieved = those bytes / its time against the LDS read peak
-    (128 B per clock per CU, 256 CUs, 2.4 GHz)."""
+    family) is bound by LDS gathers, neither HBM nor MFMA -- M table reads of
+    4 bytes per (query, probed row); achieved = those bytes / its time against
+    the LDS read peak (128 B per clock per CU, 256 CUs, 2.4 GHz); traffic = its
+    measured HBM bytes (FETCH_SIZE + WRITE_SIZE, scaled as for the flat scan)."""
     import numpy as np
     import datagen
     import hipmem
@@ -355,7 +358,8 @@ def ivfpq_bench(args):
                    "nb": nb, "d": d, "nq": nq, "k": k, "nlist": nlist, "nprobe": nprobe, "m_sub": M,
                    "rerank": rerank, "parallelism": "single GPU"},
         "roofline": {"bound": "lds", "achieved": round(ach, 2), "peak": peak, "unit": "GB/s",
-                     "frac": round(ach / peak, 4), "traffic": None},
+                     "frac": round(ach / peak, 4),
+                     "traffic": MEASURED_TRAFFIC_BYTES.get(("IVFPQ", nlist, nprobe, M)) if nq == 10_000 else None},
         "kernels": kern,
         "probed_rows_per_query": round(rows / nq, 1),
         "recall_vs_exact_flat": round(recall, 5),

@@ -16,6 +16,8 @@
 //            scan position) of what it stored is a GUARANTEED bound -- the k-th
 //            best over a subset of the probed rows is never better than the
 //            k-th best over all of them (skipped for nprobe = 1)
+//   A2       (IVF-PQ, when a cell outgrows the sample) A's cells in full under
+//            A's bound; the smaller of the two bounds stays
 //   B scan   all probed cells with that bound, into one region per (query,
 //            cell) plus a spill region per query for what overflows them;
 //            select the k best of the stored survivors. Exact unless the spill
