@@ -1340,7 +1340,15 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
                 for (int e = 0; e < n; ++e) sBuf[o + e] = composite(src[e]);
             }
         } else {
-            for (int e = tid; e < c; e += 256) sBuf[e] = fetch(e);
+            // eight offset searches and loads per thread in flight
+            for (int e0 = tid; e0 < c; e0 += 8 * 256) {
+                uint64_t v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = e0 + u * 256 < c ? fetch(e0 + u * 256) : 0ull;
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (e0 + u * 256 < c) sBuf[e0 + u * 256] = v[u];
+            }
         }
     }
     __syncthreads();

@@ -99,7 +99,7 @@ def test_rerank_off_without_stored_rows(gpu_ok):
         parity.exact(a[0], a[1], b[0], b[1])
 
 
-@pytest.mark.parametrize("d,M", [(12, 3), (24, 6), (96, 32), (64, 64)])
+@pytest.mark.parametrize("d,M", [(12, 3), (24, 6), (96, 32), (64, 64), (16, 1), (16, 2), (128, 128), (40, 20)])
 def test_subquantizer_counts(gpu_ok, d, M):
     x, q = datagen.gmm(nb=8_000, nq=200, d=d, ncenters=32, seed=36 + M)
     with build(x, 16, M) as idx:
@@ -138,3 +138,23 @@ def test_device_entry_point_matches_host(gpu_ok):
             dv = hipmem.DeviceArray((256, 10), np.float32)
             assert idx.search_device(dq, 10, 6, di, dv, rerank=rr) == 10
             parity.exact(di.numpy(), dv.numpy(), hi, hv)
+
+
+def test_single_probe_and_all_cells(gpu_ok):
+    x, q = datagen.gmm(nb=12_000, nq=150, d=32, ncenters=32, seed=41)
+    with build(x, 24, 8) as idx:
+        check(idx, q, 20, 1, L2)    # nearest cell only
+        check(idx, q, 20, 24, L2)   # every cell
+        check(idx, q, 20, 500, L2)  # nprobe clamped to nlist
+
+
+def test_cosine_zero_rows_and_queries(gpu_ok):
+    x, q = datagen.gmm(nb=6_000, nq=100, d=32, ncenters=16, seed=42)
+    x[::97] = 0.0   # zero rows stay zero under normalisation
+    q[::13] = 0.0
+    with build(x, 12, 8, COS, rerank=True) as idx:
+        check(idx, q, 15, 4, COS)
+        short, _, _ = idx.search(q, 60, 4)
+        gi, gv, _ = idx.search(q, 15, 4, rerank=60)
+    oi, ov = oracle.pq_rerank(x, q, short, 15, COS)
+    parity.exact(gi, gv, oi, ov)
