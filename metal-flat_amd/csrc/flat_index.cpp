@@ -98,8 +98,15 @@ int chooseJ(int k, double lambda, double tail) {
 // database and wants many more, smaller workgroups).
 // minTiles: fewest kBM-row tiles per split (a scan_resident workgroup needs
 // two tiles to give each of its four waves a 64-row slice).
+// concurrent (> 0): workgroups of the MFMA scan that run at once
+// (scan_concurrency). The launch's nqb x nsplit equal workgroups run in rounds
+// of that many; a last round of a few leaves the chip idle for most of a
+// round (C2: 79 x 26 = 2054 workgroups in rounds of 512 -- 10% of the scan).
+// The split count is then chosen in [want, 3 want] to minimise
+// rounds x (tiles per split + 1), a partial round of fraction f costing
+// 0.5 + 0.5 f of a full one (its workgroups run alone, faster).
 void splitPlan(int64_t nrows, int nq, int dpad, int storage, int64_t& rowsPerSplit, int& nsplit,
-               bool allowSmall = true, int64_t minTiles = 1) {
+               bool allowSmall = true, int64_t minTiles = 1, int concurrent = 0) {
     const int nqb = (nq + kBN - 1) / kBN;
     const int64_t ntiles = std::max<int64_t>(1, (nrows + kBM - 1) / kBM);
     const int64_t target = allowSmall && small_scan_fits(nq, dpad, storage) ? kTargetWGSmall : kTargetWG;
@@ -111,6 +118,27 @@ void splitPlan(int64_t nrows, int nq, int dpad, int storage, int64_t& rowsPerSpl
     want = std::min<int64_t>(want, kMaxSplit);
     want = std::min(want, std::max<int64_t>(1, ntiles / minTiles));
     want = std::min(want, ntiles);
+    if (concurrent > 0 && !(allowSmall && small_scan_fits(nq, dpad, storage))) {
+        const int64_t lo = want;   // fewer, longer splits measured slower on short scans (C1, samples)
+        const int64_t hi = std::min<int64_t>({3 * want, kMaxSplit, std::max<int64_t>(1, ntiles / minTiles), ntiles});
+        auto cost = [&](int64_t ns) {
+            const int64_t tps = (ntiles + ns - 1) / ns;
+            const int64_t w = (int64_t)nqb * ((ntiles + tps - 1) / tps);
+            const int64_t full = w / concurrent, rem = w % concurrent;
+            const double rounds = (double)full + (rem ? 0.5 + 0.5 * (double)rem / concurrent : 0.0);
+            return rounds * ((double)tps + 1.0);
+        };
+        int64_t best = want;
+        double bestCost = cost(want);
+        for (int64_t ns = lo; ns <= hi; ++ns) {
+            const double c = cost(ns);
+            if (c < bestCost - 1e-9) {
+                bestCost = c;
+                best = ns;
+            }
+        }
+        want = best;
+    }
     const int64_t tps = (ntiles + want - 1) / want;
     nsplit = (int)((ntiles + tps - 1) / tps);
     rowsPerSplit = tps * kBM;
@@ -181,6 +209,14 @@ struct FlatIndex::Impl {
     int kernMetric() const { return metric == Metric::L2 ? 0 : 1; }
     float emptyValue() const { return metric == Metric::L2 ? INFINITY : -INFINITY; }
 
+    // Workgroups of each pass's MFMA scan that fit the device at once (the
+    // split plan's tail rule), queried once per pass.
+    mutable int conc[4] = {-1, -1, -1, -1};
+    int concurrency(int pass) const {
+        if (conc[pass] < 0) conc[pass] = scan_concurrency(dpad, storage, kernMetric(), pass);
+        return conc[pass];
+    }
+
     void setDevice() const {
         if (device >= 0) HIPC(hipSetDevice(device));
     }
@@ -207,7 +243,7 @@ struct FlatIndex::Impl {
         // a sample level and its select.
         if (nb <= std::max<int64_t>(2 * r, kSelLds)) {
             pl.direct = true;
-            splitPlan(nb, (int)mb, dpad, storage, pl.rps1, pl.nsplit1);
+            splitPlan(nb, (int)mb, dpad, storage, pl.rps1, pl.nsplit1, true, 1, concurrency(kPassFull));
             pl.cap1 = (int)pl.rps1;
             pl.perQuery = (size_t)pl.nsplit1 * pl.cap1;
             return pl;
@@ -222,9 +258,9 @@ struct FlatIndex::Impl {
         // time per query block of kBN); ~1% misses balances the two.
         pl.j = chooseJ(k, lambda, 0.01);
         pl.j2 = chooseJ(k, lambda, 1e-9);
-        splitPlan(r, (int)mb, dpad, storage, pl.rps0, pl.nsplit0);
+        splitPlan(r, (int)mb, dpad, storage, pl.rps0, pl.nsplit0, true, 1, concurrency(kPassSample));
         pl.cap0 = (int)pl.rps0;
-        splitPlan(nb, (int)mb, dpad, storage, pl.rps1, pl.nsplit1);
+        splitPlan(nb, (int)mb, dpad, storage, pl.rps1, pl.nsplit1, true, 1, concurrency(kPassFull));
         const double e1 = (double)pl.j * (double)nb / (double)r;   // expected survivors
         const int64_t perSplit = (int64_t)(2.0 * e1 / pl.nsplit1) + 64;
         pl.cap1 = std::max<int>({2 * k, 64, pow2ceil(perSplit)});
@@ -262,7 +298,7 @@ struct FlatIndex::Impl {
         }
         if (!pl.Rb) return;
         pl.strideb = (int)(nb / pl.Rb);
-        splitPlan(pl.Rb, (int)mb, dpad, storage, pl.rpsb, pl.nsplitb);
+        splitPlan(pl.Rb, (int)mb, dpad, storage, pl.rpsb, pl.nsplitb, true, 1, concurrency(kPassSample));
         const double eb = (double)pl.j * (double)pl.Rb / (double)r;   // expected stored per query
         pl.capb = std::max<int>(32, pow2ceil((int64_t)(4.0 * eb / pl.nsplitb) + 16));
         // the full pass now expects jb nb / Rb survivors
@@ -385,7 +421,7 @@ struct FlatIndex::Impl {
             ScanParams p;
             std::memset(&p, 0, sizeof p);
             p.X = X.p; p.xnorm = xn.as<float>(); p.xnorm_max = xnMax; p.nrows = nb;
-            splitPlan(nb, mb, dpad, storage, p.rows_per_split, p.nsplit);
+            splitPlan(nb, mb, dpad, storage, p.rows_per_split, p.nsplit, true, 1, concurrency(kPassArgmin));
             p.id_stride = 1;
             p.Q = Q; p.qnorm = qn; p.nq = mb; p.nqb = (mb + kBN - 1) / kBN; p.dpad = dpad;
             p.cap = 1;
@@ -502,7 +538,8 @@ struct FlatIndex::Impl {
             // Retries run the kernel family of the passes their bounds came
             // from (the whole batch's), so every bound is compared with keys
             // computed the same way (a guaranteed bound must admit its own rows).
-            splitPlan(nb, nf, dpad, storage, rps, nsplit, batchSmall, batchSmall ? 1 : kRetryMinTiles);
+            splitPlan(nb, nf, dpad, storage, rps, nsplit, batchSmall, batchSmall ? 1 : kRetryMinTiles,
+                      concurrency(kPassRetry));
             const int cap = std::max(2 * k, 64);
             scan(X.p, xn.as<float>(), nb, rps, nsplit, 1, cQ.p, cQn.as<float>(), nf,
                  cTk.as<float>(), cTi.as<int>(), cap, s, kPassRetry, batchSmall);

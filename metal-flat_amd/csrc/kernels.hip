@@ -1883,6 +1883,64 @@ bool small_scan_fits(int nq, int dpad, int storage) {
     return nq >= 1 && nq <= kSmallMaxQ && small_lds_bytes(nq, dpad, storage) <= kSmallMaxLds;
 }
 
+// The function launch_scan_filter starts for a batch too large for scan_small,
+// and its dynamic LDS (for the occupancy query).
+template <int S, int M>
+static const void* resident_fn(int pass, int dpad) {
+    auto f = [](const void* k) {
+        allow_resident_lds(k);
+        return k;
+    };
+    if (pass == kPassArgmin) {
+        static const void* a = f((const void*)scan_resident_kernel<S, M, kPassArgmin, 0, false, 4>);
+        return a;
+    }
+    const int G = S != kF32 && dpad == 96 ? 3 : S != kF32 && dpad == 128 ? 4 : 0;
+#define MFLAT_RES_FN(P, GG)                                                                 \
+    if (pass == P && G == GG) {                                                             \
+        static const void* k = f((const void*)scan_resident_kernel<S, M, P, GG, false, 4>); \
+        return k;                                                                           \
+    }
+    MFLAT_RES_FN(kPassSample, 0) MFLAT_RES_FN(kPassRetry, 0) MFLAT_RES_FN(kPassFull, 0)
+    if constexpr (S != kF32) {
+        MFLAT_RES_FN(kPassSample, 3) MFLAT_RES_FN(kPassRetry, 3) MFLAT_RES_FN(kPassFull, 3)
+        MFLAT_RES_FN(kPassSample, 4) MFLAT_RES_FN(kPassRetry, 4) MFLAT_RES_FN(kPassFull, 4)
+    }
+#undef MFLAT_RES_FN
+    return nullptr;
+}
+template <int S, int M>
+static const void* tiled_fn(int pass) {
+    if (pass == kPassSample) return (const void*)scan_filter_kernel<S, M, kPassSample>;
+    if (pass == kPassRetry) return (const void*)scan_filter_kernel<S, M, kPassRetry>;
+    if (pass == kPassArgmin) return (const void*)scan_filter_kernel<S, M, kPassArgmin>;
+    return (const void*)scan_filter_kernel<S, M, kPassFull>;
+}
+template <int S>
+static const void* scan_fn(int dpad, int metric, int pass, size_t& lds) {
+    if (resident_scan_fits(dpad, S)) {
+        lds = resident_lds_bytes(dpad, S);
+        return metric == 0 ? resident_fn<S, 0>(pass, dpad) : resident_fn<S, 1>(pass, dpad);
+    }
+    lds = 0;
+    return metric == 0 ? tiled_fn<S, 0>(pass) : tiled_fn<S, 1>(pass);
+}
+
+int scan_concurrency(int dpad, int storage, int metric, int pass) {
+    size_t lds = 0;
+    const void* f = storage == kF32 ? scan_fn<kF32>(dpad, metric, pass, lds)
+                    : storage == kF16 ? scan_fn<kF16>(dpad, metric, pass, lds)
+                                      : scan_fn<kBF16>(dpad, metric, pass, lds);
+    int dev = 0, cus = 0, per = 0;
+    if (!f || hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, f, 256, lds) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return per > 0 && cus > 0 ? per * cus : 0;
+}
+
 void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, hipStream_t s, bool allowSmall) {
     if (storage != kF32 && storage != kF16 && storage != kBF16)
         throw std::runtime_error("scan_filter: unknown storage type");

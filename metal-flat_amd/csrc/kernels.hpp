@@ -179,6 +179,9 @@ void launch_max_norm(const float* xn, int64_t n, unsigned* out, hipStream_t s);
 // other must not mix it with the other two (allowSmall = false).
 bool small_scan_fits(int nq, int dpad, int storage);
 bool resident_scan_fits(int dpad, int storage);
+// Workgroups of the scan that launch_scan_filter runs (outside scan_small's
+// range) that fit the current device at once (occupancy x CUs); 0 if unknown.
+int scan_concurrency(int dpad, int storage, int metric, int pass);
 void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, hipStream_t s,
                         bool allowSmall = true);
 // IVF fine scan (scan_resident over the work items of ScanParams::ivf_*; the
