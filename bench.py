@@ -48,9 +48,9 @@ PEAK_HBM_GBS = 8000.0
 # committed under profiles/. Keyed by (config, nq, storage); reported as
 # roofline.traffic for the configuration it was measured on, null otherwise.
 MEASURED_TRAFFIC_BYTES = {
-    ("C2", 10_000, "f32"): 4.82e9,
-    ("C2", 10_000, "f16"): 2.457e9,
-    ("C3", 10_000, "f32"): 286.5e9,
+    ("C2", 10_000, "f32"): 4.76e9,
+    ("C2", 10_000, "f16"): 2.298e9,
+    ("C3", 10_000, "f32"): 287.8e9,
     ("C4", 1, "f32"): 3.880e9,
     ("C4", 1, "f16"): 1.960e9,
     ("C4", 64, "f16"): 1.972e9,
