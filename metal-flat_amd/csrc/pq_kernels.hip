@@ -137,9 +137,45 @@ __global__ void pq_codes_kernel(const int* __restrict__ subAssign, const int* __
         codes[s * M + mm] = (uint8_t)subAssign[rid[s]];
 }
 
-// lut[i][m][j] = norms[m][j] - 2 * dot(q_i[m], pqc[m][j]) (src/Distance.h:86-88)
-__global__ void pq_lut_kernel(const float* __restrict__ q, int nq, int dim, const float* __restrict__ pqc,
-                              const float* __restrict__ norms, int M, int dsub, float* __restrict__ lut) {
+// lut[i][m][j] = norms[m][j] - 2 * dot(q_i[m], pqc[m][j]) (src/Distance.h:86-88).
+// One block per (16 queries, sub-space m): thread j keeps sub-centroid j in
+// registers and writes entry j of the 16 queries' tables (coalesced rows); the
+// queries' sub-vectors sit in LDS. dsub <= 32 here; larger sub-spaces take
+// pq_lut_wide_kernel.
+constexpr int kLutQ = 16;
+constexpr int kLutMaxDsub = 32;
+__global__ void __launch_bounds__(kPqKsub) pq_lut_kernel(const float* __restrict__ q, int nq, int dim,
+                                                          const float* __restrict__ pqc,
+                                                          const float* __restrict__ norms, int M, int dsub,
+                                                          float* __restrict__ lut) {
+#pragma clang fp contract(off)
+    __shared__ float sq[kLutQ * kLutMaxDsub];
+    const int m = blockIdx.y;
+    const int i0 = blockIdx.x * kLutQ;
+    const int j = threadIdx.x;
+    for (int e = j; e < kLutQ * dsub; e += kPqKsub) {
+        const int t = e / dsub, c = e - t * dsub;
+        sq[e] = i0 + t < nq ? q[(int64_t)(i0 + t) * dim + m * dsub + c] : 0.0f;
+    }
+    float pc[kLutMaxDsub];
+    const float* cj = pqc + ((int64_t)m * kPqKsub + j) * dsub;
+#pragma unroll
+    for (int c = 0; c < kLutMaxDsub; ++c) pc[c] = c < dsub ? cj[c] : 0.0f;
+    const float nj = norms[m * kPqKsub + j];
+    __syncthreads();
+    const int64_t tab = (int64_t)M * kPqKsub;
+    for (int t = 0; t < kLutQ && i0 + t < nq; ++t) {
+        const float* qs = sq + t * dsub;
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kLutMaxDsub; ++c)
+            if (c < dsub) acc += qs[c] * pc[c];
+        lut[(int64_t)(i0 + t) * tab + m * kPqKsub + j] = nj - 2.0f * acc;
+    }
+}
+
+__global__ void pq_lut_wide_kernel(const float* __restrict__ q, int nq, int dim, const float* __restrict__ pqc,
+                                   const float* __restrict__ norms, int M, int dsub, float* __restrict__ lut) {
 #pragma clang fp contract(off)
     const int tab = M * kPqKsub;
     const int64_t total = (int64_t)nq * tab;
@@ -480,7 +516,12 @@ void launch_pq_lut(const float* q, int nq, int dim, const float* pqc, const floa
     if (nq <= 0) return;
     void* tok;
     prof_begin(kFamPrep, s, &tok);
-    pq_lut_kernel<<<grid_of((int64_t)nq * M * kPqKsub, 256), 256, 0, s>>>(q, nq, dim, pqc, norms, M, dsub, lut);
+    if (dsub <= kLutMaxDsub && (nq + kLutQ - 1) / kLutQ <= 0x7FFFFFFF && M <= 65535)
+        pq_lut_kernel<<<dim3((unsigned)((nq + kLutQ - 1) / kLutQ), (unsigned)M), kPqKsub, 0, s>>>(q, nq, dim, pqc,
+                                                                                              norms, M, dsub, lut);
+    else
+        pq_lut_wide_kernel<<<grid_of((int64_t)nq * M * kPqKsub, 256), 256, 0, s>>>(q, nq, dim, pqc, norms, M, dsub,
+                                                                                 lut);
     prof_end(tok, s);
     check(hipGetLastError(), "pq_lut");
 }
