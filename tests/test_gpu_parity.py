@@ -173,6 +173,25 @@ def test_gmm_l2_k100(gpu_ok):
     parity.tolerant(gi, gd, oi, od, x, q, 0)
 
 
+def test_batch_composition_invariant(gpu_ok):
+    """Full C2: a query's results do not depend on the batch it comes in. The
+    batch size sets the launch plan (query blocks, the split count chosen by
+    the tail rule, sample size, speculative rank, retries), but every plan
+    computes each (query, row) key the same way and selects exactly, so the
+    10,000-query batch and sub-batches of 1,000 / 200 / 65 queries (all above
+    the streaming kernel's 64) must agree bit for bit."""
+    x, q = datagen.gmm()
+    with mflat.FlatIndex(x.shape[1], L2) as idx:
+        idx.add(x)
+        ai, ad, _ = idx.search(q, 100)
+        for lo, hi in ((0, 1000), (3000, 3200), (7000, 7065)):
+            print(f"[parity] C2 sub-batch {lo}:{hi}", flush=True)
+            bi, bd, _ = idx.search(q[lo:hi], 100)
+            assert np.array_equal(bi, ai[lo:hi]) and np.array_equal(bd, ad[lo:hi])
+    fi, fd = orc(x, q[:60], 100, L2)
+    parity.tolerant(ai[:60], ad[:60], fi, fd, x, q[:60], 0)
+
+
 def test_unit_ip_d768(gpu_ok):
     """Reduced C3: unit-normalised N(0, I), d=768, inner product, k=100."""
     x, q = datagen.unit_normal(nb=40_000, nq=200, seed=2)
