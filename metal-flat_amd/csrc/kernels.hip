@@ -758,17 +758,34 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     {
         const int rowP = p.dpad * ES / 16;
         const fx4* qg = (const fx4*)p.Q + (int64_t)qb * kBN * rowP;
-        for (int i = tid; i < TQ * rowP; i += 256) {
-            const int row = i / rowP;
-            const int c = i - row * rowP;
-            fx4 v;
-            if constexpr (IVF) {
-                const int q = sQi[row];
-                v = q >= 0 ? ((const fx4*)p.Q)[(int64_t)q * rowP + c] : fx4{0.0f, 0.0f, 0.0f, 0.0f};
-            } else {
-                v = qg[(int64_t)row * rowP + c];
+        // eight 16-byte pieces per thread in flight (a work item of the IVF
+        // scan is short enough for serial load latencies here to show)
+        const int npc = TQ * rowP;
+        for (int i0 = tid; i0 < npc; i0 += 8 * 256) {
+            fx4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = i0 + u * 256;
+                v[u] = fx4{0.0f, 0.0f, 0.0f, 0.0f};
+                if (i < npc) {
+                    const int row = i / rowP;
+                    const int c = i - row * rowP;
+                    if constexpr (IVF) {
+                        const int q = sQi[row];
+                        if (q >= 0) v[u] = ((const fx4*)p.Q)[(int64_t)q * rowP + c];
+                    } else {
+                        v[u] = qg[(int64_t)row * rowP + c];
+                    }
+                }
             }
-            *(fx4*)((char*)sQr + row * ldqB + c * 16) = v;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = i0 + u * 256;
+                if (i < npc) {
+                    const int row = i / rowP;
+                    *(fx4*)((char*)sQr + row * ldqB + (i - row * rowP) * 16) = v[u];
+                }
+            }
         }
     }
     if (tid < TQ) {
