@@ -161,7 +161,8 @@ def kmeans_bench(iters):
 
 
 def ivf_bench(args):
-    """IVF search (mflat_ivf_*) on C2's database and queries: nlist and nprobe by
+    """IVF search (mflat_ivf_*) on C2's database and queries (or, --config C3,
+    C3's: d = 768 inner product, which runs 32-query work items only): nlist and nprobe by
     the reference bench's rule (bench/bench.mm:96-101: nlist = max(64, sqrt(N)),
     nprobe = max(1, nlist / 16)) unless given, k = C2's 100. A step is one search
     of the whole query batch (device pointers, inputs resident in HBM); the build
@@ -177,7 +178,12 @@ def ivf_bench(args):
     import oracle
 
     mflat.load()
-    x, q = datagen.gmm()
+    c3 = args.config == "C3"
+    if args.config not in ("C2", "C3"):
+        raise SystemExit("--ivf runs on C2's or C3's data")
+    x, q = datagen.unit_normal() if c3 else datagen.gmm()
+    metric = mflat.MFLAT_METRIC_INNER_PRODUCT if c3 else mflat.MFLAT_METRIC_L2
+    mname = "inner product" if c3 else "L2"
     if args.nq:
         q = q[: args.nq]
     nb, d = x.shape
@@ -187,7 +193,7 @@ def ivf_bench(args):
     nprobe = args.nprobe or max(1, nlist // 16)
     storage = mflat.STORAGE_NAMES[args.storage]
     log(f"[bench] ivf: nb={nb} d={d} nq={nq} k={k} nlist={nlist} nprobe={nprobe} storage={args.storage}")
-    idx = mflat.IvfIndex(d, mflat.MFLAT_METRIC_L2, nlist, storage)
+    idx = mflat.IvfIndex(d, metric, nlist, storage)
     t0 = time.perf_counter()
     idx.build(x)
     build_s = time.perf_counter() - t0
@@ -222,13 +228,13 @@ def ivf_bench(args):
 
     peak = PEAK_FP32_MFMA_TFLOPS if storage == mflat.MFLAT_STORAGE_F32 else PEAK_F16_MFMA_TFLOPS
     ach = flop * args.steps / (kern["ivf_scan"]["total_ms"] / 1000.0) / 1e12
-    flat = mflat.FlatIndex(d, mflat.MFLAT_METRIC_L2)
+    flat = mflat.FlatIndex(d, metric)
     flat.add(x)
     fi, _, _ = flat.search(q, k)
     flat.close()
     recall = float(np.mean([len(set(gi[r].tolist()) & set(fi[r].tolist())) / k for r in range(nq)]))
     out = {
-        "metric": f"QPS, IVF L2 d={d} nb={nb} nlist={nlist} nprobe={nprobe} k={k} (1 GPU)",
+        "metric": f"QPS, IVF {mname} d={d} nb={nb} nlist={nlist} nprobe={nprobe} k={k} (1 GPU)",
         "value": round(nq * args.steps / elapsed, 2),
         "unit": "queries/s",
         "n_gpus": 1,
@@ -241,12 +247,15 @@ def ivf_bench(args):
         "dtype": {"f32": "fp32", "f16": "fp16 storage, fp32 accumulate",
                   "bf16": "bf16 storage, fp32 accumulate"}[args.storage],
         "data": "synthetic",
-        "config": {"workload": f"IVF over C2's database and queries (GMM 1024 centres, sigma 0.3, seed 1), "
+        "config": {"workload": (f"IVF over C3's database and queries (unit N(0,I), d=768, inner product, seed 2), "
+                                if c3 else
+                                f"IVF over C2's database and queries (GMM 1024 centres, sigma 0.3, seed 1), ") +
                                f"nlist={nlist}, nprobe={nprobe}, k={k}", "nb": nb, "d": d, "nq": nq, "k": k,
                    "nlist": nlist, "nprobe": nprobe, "storage": args.storage, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(ach / peak, 4),
-                     "traffic": MEASURED_TRAFFIC_BYTES.get(("IVF", nlist, nprobe, args.storage)) if nq == 10_000 else None},
+                     "traffic": MEASURED_TRAFFIC_BYTES.get(("IVF", nlist, nprobe, args.storage))
+                     if nq == 10_000 and not c3 else None},
         "kernels": kern,
         "probed_rows_per_query": round(rows / nq, 1),
         "recall_vs_exact_flat": round(recall, 5),
@@ -257,12 +266,12 @@ def ivf_bench(args):
         for threads, key in ((1, "cpu_baseline"), (host_threads(), "cpu_baseline_all_cores")):
             log(f"[bench] ivf cpu baseline ({threads} threads) ...")
             t0 = time.perf_counter()
-            oracle.ivf_search(None, start, rid, q[:threads], k, probed[:threads], 0, threads=threads,
-                              payload=payload)
+            oracle.ivf_search(None, start, rid, q[:threads], k, probed[:threads], 1 if c3 else 0,
+                              threads=threads, payload=payload)
             one = max(time.perf_counter() - t0, 1e-6) / threads
             n = int(max(1, min(nq, 12.0 / one)))
             t0 = time.perf_counter()
-            oi, _ = oracle.ivf_search(None, start, rid, q[:n], k, probed[:n], 0, threads=threads,
+            oi, _ = oracle.ivf_search(None, start, rid, q[:n], k, probed[:n], 1 if c3 else 0, threads=threads,
                                       payload=payload)
             dt = time.perf_counter() - t0
             agree = float(np.mean([len(set(oi[r].tolist()) & set(gi[r].tolist())) / k for r in range(n)]))

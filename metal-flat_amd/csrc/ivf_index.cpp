@@ -325,7 +325,7 @@ struct IvfIndex::Impl {
         p.ivf_cell_pad = dCellPad.as<int64_t>(); p.ivf_cell_size = dCellSize.as<int>();
         p.ivf_nprobe = nprobe; p.ivf_nreg = nreg; p.ivf_spill = spill ? 1 : 0; p.ivf_row_cap = rowCap;
         p.ivf_work = wt.work; p.ivf_nwork = wt.nwork;
-        launch_scan_ivf(p, kernMetric(), pass, storage, kBN, wt.maxWork(nq, ranks, nlist), s);
+        if (narrowMax() >= 0) launch_scan_ivf(p, kernMetric(), pass, storage, kBN, wt.maxWork(nq, ranks, nlist), s);
         p.ivf_work = wt.workN; p.ivf_nwork = wt.nwork + 1;
         launch_scan_ivf(p, kernMetric(), pass, storage, kIvfNarrow, wt.maxWorkNarrow(nq, ranks, nlist, narrowMax()),
                         s);
@@ -337,6 +337,7 @@ struct IvfIndex::Impl {
     // PQ work items: adc_tile_queries(M) queries, wide only.
     int narrowMax() const {
         if (pq()) return 0;
+        if (!resident_scan_fits(dpad, storage)) return -1;   // a 128-query tile exceeds LDS: 32-query items only
         if (const char* e = std::getenv("MFLAT_IVF_TILES")) {
             if (std::atoi(e) == 128) return 0;
             if (std::atoi(e) == 32) return -1;
@@ -553,8 +554,8 @@ struct IvfIndex::Impl {
         if (nprobe < 1) nprobe = 1;
         if (nprobe > nlist) nprobe = nlist;
         if (nprobe > kMaxProbe) throw BadArg("IVF search: nprobe above 1024 is not supported");
-        if (!pq() && !resident_scan_fits(dpad, storage))
-            throw BadArg("IVF search: the fine scan holds a 128-query tile in LDS (fp32 dim <= 128, fp16/bf16 dim <= 256)");
+        if (!pq() && !ivf_narrow_fits(dpad, storage))
+            throw BadArg("IVF search: the fine scan holds a 32-query tile in LDS (fp32 dim <= 1120, fp16/bf16 dim <= 2272)");
         // PQ rerank (src/IvfPqIndex.mm:583-585): a PQ shortlist of kRun rows,
         // re-ranked by exact distance, when rerank > k and the rows were kept
         const bool doRerank = pq() && rerank > k && fullStored;

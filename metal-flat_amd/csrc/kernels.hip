@@ -1807,10 +1807,11 @@ static void launch_small_s(const ScanParams& p, int metric, int pass, int nqb16,
     if (metric == 0) launch_small_m<S, 0>(p, pass, nqb16, lds, s);
     else launch_small_m<S, 1>(p, pass, nqb16, lds, s);
 }
-// Raises a kernel's dynamic-LDS limit to kResidentMaxLds (needed above the
-// default per-launch limit); throws if the runtime refuses.
+// Raises a kernel's dynamic-LDS limit to kResidentMaxLdsNarrow (needed above
+// the default per-launch limit; the launch's own size sets the occupancy);
+// throws if the runtime refuses.
 static void allow_resident_lds(const void* f) {
-    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kResidentMaxLds) != hipSuccess)
+    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kResidentMaxLdsNarrow) != hipSuccess)
         throw std::runtime_error("scan_resident: cannot raise the dynamic LDS limit");
 }
 template <int S, int M, int P, int G, bool IVF = false, int NB = 4>
@@ -1875,6 +1876,10 @@ static size_t resident_lds_bytes(int dpad, int storage, int tileQueries = kBN) {
 
 bool resident_scan_fits(int dpad, int storage) {
     return resident_lds_bytes(dpad, storage) <= kResidentMaxLds;
+}
+
+bool ivf_narrow_fits(int dpad, int storage) {
+    return resident_lds_bytes(dpad, storage, 32) <= kResidentMaxLdsNarrow;
 }
 
 template <int S, int M>
@@ -2007,8 +2012,8 @@ void launch_scan_ivf(const ScanParams& p, int metric, int pass, int storage, int
     if (grid <= 0) return;
     if (pass != kPassSample && pass != kPassFull) throw std::runtime_error("scan_ivf: bad pass");
     if (tileQueries != 128 && tileQueries != 32) throw std::runtime_error("scan_ivf: tiles hold 128 or 32 queries");
-    if (!resident_scan_fits(p.dpad, storage) || p.dpad % kBK != 0 || p.cap < 1 || p.ivf_nprobe < 1 ||
-        p.ivf_nreg < 1)
+    if (!(tileQueries == 128 ? resident_scan_fits(p.dpad, storage) : ivf_narrow_fits(p.dpad, storage)) ||
+        p.dpad % kBK != 0 || p.cap < 1 || p.ivf_nprobe < 1 || p.ivf_nreg < 1)
         throw std::runtime_error("scan_ivf: bad parameters");
     void* tok;
     prof_begin(pass == kPassSample ? kFamIvfBound : kFamIvfScan, s, &tok);

@@ -49,6 +49,7 @@ constexpr int kMaxSplit = 16384;  // most database splits one select block index
 constexpr int kSmallMaxQ = 64;                 // scan_small serves batches up to this size
 constexpr size_t kSmallMaxLds = 64 * 1024;     // ... whose query tile fits this much LDS
 constexpr size_t kResidentMaxLds = 68 * 1024;  // scan_resident: largest resident query tile
+constexpr size_t kResidentMaxLdsNarrow = 144 * 1024;  // ... of a 32-query IVF tile (one workgroup a CU)
 constexpr int kRing = 192;                     // scan_resident: staged survivors per wave
 
 // Element type of the stored database and of the queries (the ABI's
@@ -179,6 +180,9 @@ void launch_max_norm(const float* xn, int64_t n, unsigned* out, hipStream_t s);
 // other must not mix it with the other two (allowSmall = false).
 bool small_scan_fits(int nq, int dpad, int storage);
 bool resident_scan_fits(int dpad, int storage);
+// The IVF fine scan's 32-query tile fits LDS (fp32 dim <= 1120, fp16/bf16
+// dim <= 2272): the IVF index then runs narrow work items only.
+bool ivf_narrow_fits(int dpad, int storage);
 // Workgroups of the scan that launch_scan_filter runs (outside scan_small's
 // range) that fit the current device at once (occupancy x CUs); 0 if unknown.
 int scan_concurrency(int dpad, int storage, int metric, int pass);

@@ -218,3 +218,35 @@ def test_tile_widths_compute_identical_keys(gpu_ok, monkeypatch):
             parity.exact(got[0], got[1], ref[0], ref[1])
         monkeypatch.delenv("MFLAT_IVF_TILES")
         check(idx, x, q, 100, 10, L2)
+
+
+# ---- dims beyond the 128-query tile: 32-query work items only ---------------
+
+def test_large_dim_integer_exact(gpu_ok):
+    x, q = int_case(12_000, 150, 256, 16, seed=51)   # fp32 d = 256: a 128-query tile exceeds LDS
+    with build(x, 24) as idx:
+        check(idx, x, q, 20, 5, L2, exact=True)
+    with build(x, 24, IP) as idx:
+        check(idx, x, q, 100, 24, IP, exact=True)
+
+
+@pytest.mark.parametrize("d,metric", [(768, IP), (300, L2), (1120, COS)])
+def test_large_dim_float(gpu_ok, d, metric):
+    x, q = datagen.unit_normal(nb=8_000, nq=100, d=d, seed=52 + d)
+    with build(x, 16, metric) as idx:
+        check(idx, x, q, 10, 4, metric)
+
+
+@pytest.mark.parametrize("storage", [mflat.MFLAT_STORAGE_F16, mflat.MFLAT_STORAGE_BF16])
+def test_large_dim_reduced_storage(gpu_ok, storage):
+    x, q = datagen.unit_normal(nb=8_000, nq=100, d=512, seed=53)
+    with build(x, 16, L2, storage) as idx:
+        check(idx, x, q, 10, 4, L2, storage=storage)
+
+
+def test_dim_beyond_narrow_tile_is_bad_arg(gpu_ok):
+    x, q = datagen.unit_normal(nb=2_000, nq=4, d=1152, seed=54)
+    with build(x, 8) as idx:
+        with pytest.raises(mflat.MflatError) as e:
+            idx.search(q, 5, 2)
+        assert e.value.status == mflat.MFLAT_ERR_BAD_ARG
