@@ -158,3 +158,16 @@ def test_cosine_zero_rows_and_queries(gpu_ok):
         gi, gv, _ = idx.search(q, 15, 4, rerank=60)
     oi, ov = oracle.pq_rerank(x, q, short, 15, COS)
     parity.exact(gi, gv, oi, ov)
+
+
+@pytest.mark.parametrize("d,M", [(768, 16), (768, 48), (384, 96)])
+def test_large_dims(gpu_ok, d, M):
+    """Sub-spaces wider than the lookup-table kernel's 32 columns (768 / 16 = 48)
+    take its generic path; d = 768 rows also go through the exact rerank."""
+    x, q = datagen.unit_normal(nb=6_000, nq=80, d=d, seed=60 + M)
+    with build(x, 12, M, L2, rerank=True) as idx:
+        check(idx, q, 10, 3, L2)
+        short, _, _ = idx.search(q, 50, 3)
+        gi, gv, _ = idx.search(q, 10, 3, rerank=50)
+    oi, ov = oracle.pq_rerank(x, q, short, 10, L2)
+    parity.exact(gi, gv, oi, ov)
