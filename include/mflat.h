@@ -22,9 +22,7 @@
  *  - The IVF entry points (reference c/include/mflat.h:92-105) are here,
  *    with the same argument checks and result layout; IVF search serves
  *    k <= MFLAT_MAX_K and nprobe <= MFLAT_MAX_K on the device (the reference
- *    serves k > 64 on its CPU path, src/IvfIndex.mm:762-764), and the fine
- *    scan needs dim <= 1120 (fp32) or <= 2272 (fp16 / bf16 storage); above
- *    dim 128 (fp32) / 256 (fp16 / bf16) it runs 32-query work items only.
+ *    serves k > 64 on its CPU path, src/IvfIndex.mm:762-764); any dim.
  *  - The IVF-PQ entry points (reference c/include/mflat.h:107-129) are here with
  *    the reference C ABI's behaviour: residual PQ, no OPQ (the reference's C
  *    ABI reaches neither of its setResidual / setOpq switches); k up to

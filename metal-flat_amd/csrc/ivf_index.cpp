@@ -335,13 +335,17 @@ struct IvfIndex::Impl {
     // makes every work item wide / narrow; both compute the same keys, so the
     // results never depend on it.
     // PQ work items: adc_tile_queries(M) queries, wide only.
+    // Large d (a 128-query tile beyond scan_resident's LDS): 128-query items
+    // on the LDS-tiled kernel only, so every pass of a search computes its
+    // keys with the same kernel (MFLAT_IVF_TILES = 32 there picks 32-query
+    // scan_resident items instead, where their tile fits).
     int narrowMax() const {
         if (pq()) return 0;
-        if (!resident_scan_fits(dpad, storage)) return -1;   // a 128-query tile exceeds LDS: 32-query items only
         if (const char* e = std::getenv("MFLAT_IVF_TILES")) {
             if (std::atoi(e) == 128) return 0;
-            if (std::atoi(e) == 32) return -1;
+            if (std::atoi(e) == 32 && ivf_narrow_fits(dpad, storage)) return -1;
         }
+        if (!resident_scan_fits(dpad, storage)) return 0;
         return kBN - kIvfNarrow;
     }
     int wideWidth() const { return pq() ? adc_tile_queries(pqM) : kBN; }
@@ -554,8 +558,6 @@ struct IvfIndex::Impl {
         if (nprobe < 1) nprobe = 1;
         if (nprobe > nlist) nprobe = nlist;
         if (nprobe > kMaxProbe) throw BadArg("IVF search: nprobe above 1024 is not supported");
-        if (!pq() && !ivf_narrow_fits(dpad, storage))
-            throw BadArg("IVF search: the fine scan holds a 32-query tile in LDS (fp32 dim <= 1120, fp16/bf16 dim <= 2272)");
         // PQ rerank (src/IvfPqIndex.mm:583-585): a PQ shortlist of kRun rows,
         // re-ranked by exact distance, when rerank > k and the rows were kept
         const bool doRerank = pq() && rerank > k && fullStored;

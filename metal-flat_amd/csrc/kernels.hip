@@ -403,7 +403,12 @@ __device__ __forceinline__ void filter_group(const fx16 (&acc)[NB], int g4, int 
 // PASS only names the instantiation (0 = full database, 1 = row sample,
 // 2 = retry of a few queries), so profiles separate the passes; the code is
 // the same.
-template <int S, int METRIC, int PASS>
+// IVF: a workgroup takes one IVF work item (a cell and up to 128 of the
+// entries probing it) instead of a (query block, split): rows of that cell,
+// queries gathered by entry, survivors into the entries' regions (spill as
+// in scan_resident), ids = the row's scan position. The IVF index uses it
+// where a 128-query tile does not fit scan_resident's LDS (large d).
+template <int S, int METRIC, int PASS, bool IVF = false>
 __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     constexpr int ES = S == kF32 ? 4 : 2;   // element bytes
     __shared__ __attribute__((aligned(16))) float sX[2 * kBM * kLds];
@@ -411,6 +416,9 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     __shared__ __attribute__((aligned(16))) float sXn[2 * kBM];   // tile row norms, by tile parity
     __shared__ int sCnt[kBN];
     __shared__ unsigned long long sBest[kBN];   // argmin: per-query (ordered key, id)
+    __shared__ int sEnt[IVF ? kBN : 1];   // IVF: the item's entries (-1: empty slot)
+    __shared__ int sQi[IVF ? kBN : 1];    // ... their queries
+    __shared__ int sReg[IVF ? kBN : 1];   // ... their candidate regions
 
     // Workgroup -> (query block, split). Hardware deals consecutive ids
     // round-robin over the 8 XCDs; v renumbers them so each XCD owns a
@@ -419,16 +427,23 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     // cover kQGroup query blocks (1 MB of Q tiles at d = 128, kept in its 4 MB
     // L2) times a few splits, and each database tile they stream is shared by
     // kQGroup workgroups.
-    const int nwg = gridDim.x;
-    const int bid = blockIdx.x;
-    const int full = (nwg / 8) * 8;
-    const int v = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
-    const int grpSize = p.nqb < kQGroup ? p.nqb : kQGroup;
-    const int grp = v / (grpSize * p.nsplit);
-    const int r = v - grp * grpSize * p.nsplit;
-    const int inGrp = p.nqb - grp * grpSize < grpSize ? p.nqb - grp * grpSize : grpSize;
-    const int split = r / inGrp;
-    const int qb = grp * grpSize + (r - split * inGrp);
+    int qb = 0, split = 0;
+    int4 wk = make_int4(0, 0, 0, 0);   // IVF work item: (cell, first entry, entries, 0)
+    if constexpr (IVF) {
+        if ((int)blockIdx.x >= *p.ivf_nwork) return;
+        wk = p.ivf_work[blockIdx.x];
+    } else {
+        const int nwg = gridDim.x;
+        const int bid = blockIdx.x;
+        const int full = (nwg / 8) * 8;
+        const int v = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
+        const int grpSize = p.nqb < kQGroup ? p.nqb : kQGroup;
+        const int grp = v / (grpSize * p.nsplit);
+        const int r = v - grp * grpSize * p.nsplit;
+        const int inGrp = p.nqb - grp * grpSize < grpSize ? p.nqb - grp * grpSize : grpSize;
+        split = r / inGrp;
+        qb = grp * grpSize + (r - split * inGrp);
+    }
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -441,7 +456,15 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     if (tid < kBN) {
         sCnt[tid] = 0;
         sBest[tid] = ~0ull;
+        if constexpr (IVF) {
+            const int e = tid < wk.z ? p.ivf_ent[wk.y + tid] : -1;
+            const int q = e >= 0 ? e / p.ivf_nprobe : -1;
+            sEnt[tid] = e;
+            sQi[tid] = q;
+            sReg[tid] = e >= 0 ? q * p.ivf_nreg + (e - q * p.ivf_nprobe) : -1;
+        }
     }
+    if constexpr (IVF) __syncthreads();
 
     // Per-lane query state for the two query blocks this lane sees.
     // ft is the fast-reject bound, a NECESSARY condition for key <= tau:
@@ -456,11 +479,19 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     float tk[2], qn[2], ft[2];
     int ti[2];
     bool qv[2];
-    const int idb[2] = {0, 0};   // ids are row * id_stride
+    int idb[2] = {0, 0};   // ids are row * id_stride (+ the cell's first scan position, IVF)
 #pragma unroll
     for (int bn = 0; bn < 2; ++bn) {
-        const int q = qb * kBN + wn * 64 + bn * 32 + r32;
-        qv[bn] = q < p.nq;
+        int q;
+        if constexpr (IVF) {
+            const int ql = wn * 64 + bn * 32 + r32;
+            q = sQi[ql];
+            qv[bn] = q >= 0;
+            if (qv[bn]) idb[bn] = p.ivf_pos[sEnt[ql]];
+        } else {
+            q = qb * kBN + wn * 64 + bn * 32 + r32;
+            qv[bn] = q < p.nq;
+        }
         if (PASS == kPassArgmin) {   // running best of this lane, from "no bound"
             tk[bn] = INFINITY;
             ti[bn] = -1;
@@ -477,11 +508,25 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
         }
     }
 
-    const int64_t rows_pad = (p.nrows + kBM - 1) / kBM * kBM;
-    const int64_t rowBeg = (int64_t)split * p.rows_per_split;
-    int64_t rowEnd = rowBeg + p.rows_per_split;
-    if (rowEnd > rows_pad) rowEnd = rows_pad;
-    const int ntiles = rowEnd > rowBeg ? (int)((rowEnd - rowBeg) / kBM) : 0;
+    // Rows [rowBeg, rowBeg + kBM ntiles); filter rows count from rowOrg (IVF:
+    // the cell's first row), rows at or above rowLim are padding.
+    int64_t rowBeg, rowOrg, rowLim;
+    int ntiles;
+    if constexpr (IVF) {
+        rowBeg = p.ivf_cell_pad[wk.x];
+        rowOrg = 0;
+        rowLim = p.ivf_cell_size[wk.x];
+        if (p.ivf_row_cap > 0 && rowLim > p.ivf_row_cap) rowLim = p.ivf_row_cap;   // a cell's first rows only
+        ntiles = (int)((rowLim + kBM - 1) / kBM);
+    } else {
+        const int64_t rows_pad = (p.nrows + kBM - 1) / kBM * kBM;
+        rowBeg = (int64_t)split * p.rows_per_split;
+        int64_t rowEnd = rowBeg + p.rows_per_split;
+        if (rowEnd > rows_pad) rowEnd = rows_pad;
+        ntiles = rowEnd > rowBeg ? (int)((rowEnd - rowBeg) / kBM) : 0;
+        rowOrg = rowBeg;
+        rowLim = p.nrows;
+    }
     const int nk = S == kF32 ? p.dpad / kBK : (p.dpad + 63) / 64;
     const bool halfTail = S != kF32 && (p.dpad & 32) != 0;   // last chunk: 32 columns
     const int total = ntiles * nk;
@@ -491,6 +536,17 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     const int ldCol = (tid & 7) * 4;    // in floats = 16-byte pieces
     const char* Xb = (const char*)p.X + rowBeg * p.dpad * ES;
     const char* Qb = (const char*)p.Q + (int64_t)qb * kBN * p.dpad * ES;
+    // IVF: this thread's four query rows (ldRow + 32 i), gathered by entry
+    const char* qrow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (IVF) {
+            const int q = sQi[ldRow + 32 * i];
+            qrow[i] = q >= 0 ? (const char*)p.Q + (int64_t)q * p.dpad * ES : nullptr;
+        } else {
+            qrow[i] = Qb + (int64_t)(ldRow + 32 * i) * p.dpad * ES;
+        }
+    }
     fx4 rx[4], rq[4], rn;
     // The first chunk of every tile also brings the tile's 128 row norms
     // (threads 0..31, one float4 each) into sXn[tile & 1]; the epilogue of
@@ -507,7 +563,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
                                : 16 * (tid >> 7) + 4 * ((tid >> 4) & 3);
     auto gload = [&](int tile, int kc) {
         const char* xs = Xb + ((int64_t)tile * kBM) * p.dpad * ES + kc * 4096 + tid * 16;
-        const char* qs = Qb + kc * 128 + ldCol * 4;
+        const int qo = kc * 128 + ldCol * 4;
         const bool zx = S != kF32 && halfTail && kc == nk - 1 && tid >= 128;
         const bool zq = S != kF32 && halfTail && kc == nk - 1 && (tid & 7) >= 4;
 #pragma unroll
@@ -515,7 +571,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
             rx[i] = fx4{0.0f, 0.0f, 0.0f, 0.0f};
             rq[i] = fx4{0.0f, 0.0f, 0.0f, 0.0f};
             if (!zx) rx[i] = *(const fx4*)(xs + (int64_t)i * 32 * p.dpad * ES);
-            if (!zq) rq[i] = *(const fx4*)(qs + (int64_t)(ldRow + 32 * i) * p.dpad * ES);
+            if (!zq && qrow[i]) rq[i] = *(const fx4*)(qrow[i] + qo);
         }
         if (METRIC == 0 && kc == 0 && tid < kBM / 4)
             rn = *(const fx4*)(p.xnorm + rowBeg + (int64_t)tile * kBM + tid * 4);
@@ -605,7 +661,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
 
         if (kc == nk - 1) {
             // epilogue: keys, threshold test, append survivors
-            const int64_t tileRow0 = rowBeg + (int64_t)tile * kBM;
+            const int64_t tileRow0 = rowOrg + (int64_t)tile * kBM;
 #pragma unroll
             for (int bm = 0; bm < 2; ++bm) {
 #pragma unroll
@@ -614,15 +670,23 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
                     const int64_t r0 = tileRow0 + rl;
                     fx4 xn4 = {0.0f, 0.0f, 0.0f, 0.0f};
                     if (METRIC == 0) xn4 = xnr[bm][g4];
-                    filter_group<METRIC, PASS, 2, 2>(acc[bm], g4, 0, xn4, r0, p.nrows, p.id_stride, idb, p, tk,
-                                                  ti, qn, ft, qv,
+                    filter_group<METRIC, PASS, 2, 2>(acc[bm], g4, 0, xn4, r0, rowLim, IVF ? 1 : p.id_stride, idb,
+                                                  p, tk, ti, qn, ft, qv,
                                                   [&](int bn, float key, int id) {
                         const int ql = wn * 64 + bn * 32 + r32;
                         const int slot = atomicAdd(&sCnt[ql], 1);
-                        if (slot < p.cap) {
+                        const uint2 v = make_uint2(__float_as_uint(key), (unsigned)id);
+                        if constexpr (IVF) {
+                            if (slot < p.cap) {
+                                p.cand[(int64_t)sReg[ql] * p.cap + slot] = v;
+                            } else if (p.ivf_spill) {   // the query's spill region (global count)
+                                const int64_t sr = (int64_t)sQi[ql] * p.ivf_nreg + p.ivf_nprobe;
+                                const int sp = atomicAdd(&p.cnt[sr], 1);
+                                if (sp < p.cap) p.cand[sr * p.cap + sp] = v;
+                            }
+                        } else if (slot < p.cap) {
                             const int64_t q = (int64_t)qb * kBN + ql;
-                            p.cand[(q * p.nsplit + split) * p.cap + slot] =
-                                make_uint2(__float_as_uint(key), (unsigned)id);
+                            p.cand[(q * p.nsplit + split) * p.cap + slot] = v;
                         }
                     });
                 }
@@ -651,8 +715,12 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     }
     __syncthreads();
     if (tid < kBN) {
-        const int q = qb * kBN + tid;
-        if (q < p.nq) p.cnt[(int64_t)q * p.nsplit + split] = sCnt[tid];
+        if constexpr (IVF) {
+            if (sReg[tid] >= 0) p.cnt[sReg[tid]] = p.ivf_spill && sCnt[tid] > p.cap ? p.cap : sCnt[tid];
+        } else {
+            const int q = qb * kBN + tid;
+            if (q < p.nq) p.cnt[(int64_t)q * p.nsplit + split] = sCnt[tid];
+        }
     }
 }
 
@@ -1889,6 +1957,16 @@ static void launch_tiled(const ScanParams& p, int pass, int g, hipStream_t s) {
     else if (pass == kPassArgmin) scan_filter_kernel<S, M, kPassArgmin><<<g, 256, 0, s>>>(p);
     else scan_filter_kernel<S, M, kPassFull><<<g, 256, 0, s>>>(p);
 }
+template <int S, int M>
+static void launch_tiled_ivf(const ScanParams& p, int pass, int g, hipStream_t s) {
+    if (pass == kPassSample) scan_filter_kernel<S, M, kPassSample, true><<<g, 256, 0, s>>>(p);
+    else scan_filter_kernel<S, M, kPassFull, true><<<g, 256, 0, s>>>(p);
+}
+template <int S>
+static void launch_tiled_ivf_s(const ScanParams& p, int metric, int pass, int g, hipStream_t s) {
+    if (metric == 0) launch_tiled_ivf<S, 0>(p, pass, g, s);
+    else launch_tiled_ivf<S, 1>(p, pass, g, s);
+}
 template <int S>
 static void launch_tiled_s(const ScanParams& p, int metric, int pass, int g, hipStream_t s) {
     if (metric == 0) launch_tiled<S, 0>(p, pass, g, s);
@@ -2012,11 +2090,21 @@ void launch_scan_ivf(const ScanParams& p, int metric, int pass, int storage, int
     if (grid <= 0) return;
     if (pass != kPassSample && pass != kPassFull) throw std::runtime_error("scan_ivf: bad pass");
     if (tileQueries != 128 && tileQueries != 32) throw std::runtime_error("scan_ivf: tiles hold 128 or 32 queries");
-    if (!(tileQueries == 128 ? resident_scan_fits(p.dpad, storage) : ivf_narrow_fits(p.dpad, storage)) ||
-        p.dpad % kBK != 0 || p.cap < 1 || p.ivf_nprobe < 1 || p.ivf_nreg < 1)
+    // 128-query items whose tile does not fit scan_resident's LDS run the tiled kernel
+    const bool tiled = tileQueries == 128 && !resident_scan_fits(p.dpad, storage);
+    if (!(tileQueries == 128 || ivf_narrow_fits(p.dpad, storage)) || p.dpad % kBK != 0 || p.cap < 1 ||
+        p.ivf_nprobe < 1 || p.ivf_nreg < 1)
         throw std::runtime_error("scan_ivf: bad parameters");
     void* tok;
     prof_begin(pass == kPassSample ? kFamIvfBound : kFamIvfScan, s, &tok);
+    if (tiled) {
+        if (storage == kF32) launch_tiled_ivf_s<kF32>(p, metric, pass, grid, s);
+        else if (storage == kF16) launch_tiled_ivf_s<kF16>(p, metric, pass, grid, s);
+        else launch_tiled_ivf_s<kBF16>(p, metric, pass, grid, s);
+        prof_end(tok, s);
+        check_launch("scan_ivf_tiled");
+        return;
+    }
     const size_t lds = resident_lds_bytes(p.dpad, storage, tileQueries);
     const int nb = tileQueries / 32;
     if (storage == kF32) launch_ivf_s<kF32>(p, metric, pass, nb, grid, lds, s);

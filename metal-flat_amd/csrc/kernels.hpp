@@ -180,8 +180,8 @@ void launch_max_norm(const float* xn, int64_t n, unsigned* out, hipStream_t s);
 // other must not mix it with the other two (allowSmall = false).
 bool small_scan_fits(int nq, int dpad, int storage);
 bool resident_scan_fits(int dpad, int storage);
-// The IVF fine scan's 32-query tile fits LDS (fp32 dim <= 1120, fp16/bf16
-// dim <= 2272): the IVF index then runs narrow work items only.
+// The IVF fine scan's 32-query scan_resident tile fits LDS (fp32 dim <= 1120,
+// fp16/bf16 dim <= 2272).
 bool ivf_narrow_fits(int dpad, int storage);
 // Workgroups of the scan that launch_scan_filter runs (outside scan_small's
 // range) that fit the current device at once (occupancy x CUs); 0 if unknown.

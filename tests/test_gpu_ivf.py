@@ -220,7 +220,7 @@ def test_tile_widths_compute_identical_keys(gpu_ok, monkeypatch):
         check(idx, x, q, 100, 10, L2)
 
 
-# ---- dims beyond the 128-query tile: 32-query work items only ---------------
+# ---- dims beyond scan_resident's 128-query tile: the LDS-tiled kernel --------
 
 def test_large_dim_integer_exact(gpu_ok):
     x, q = int_case(12_000, 150, 256, 16, seed=51)   # fp32 d = 256: a 128-query tile exceeds LDS
@@ -244,9 +244,22 @@ def test_large_dim_reduced_storage(gpu_ok, storage):
         check(idx, x, q, 10, 4, L2, storage=storage)
 
 
-def test_dim_beyond_narrow_tile_is_bad_arg(gpu_ok):
-    x, q = datagen.unit_normal(nb=2_000, nq=4, d=1152, seed=54)
+@pytest.mark.parametrize("d", [1152, 2048])
+def test_very_large_dim(gpu_ok, d):
+    x, q = datagen.unit_normal(nb=3_000, nq=130, d=d, seed=54)
     with build(x, 8) as idx:
-        with pytest.raises(mflat.MflatError) as e:
-            idx.search(q, 5, 2)
-        assert e.value.status == mflat.MFLAT_ERR_BAD_ARG
+        check(idx, x, q, 10, 3, L2)
+
+
+def test_large_dim_tiles_compute_identical_keys(gpu_ok, monkeypatch):
+    """At d = 256 the LDS-tiled kernel runs the 128-query items; forcing
+    32-query items (scan_resident, whose tile fits at 32 queries) switches
+    kernels. Integer data keeps every sum exact in any accumulation order, so
+    the two must agree bit for bit."""
+    x, q = int_case(6_000, 140, 256, 16, seed=55)
+    with build(x, 12) as idx:
+        a = idx.search(q, 30, 4)
+        monkeypatch.setenv("MFLAT_IVF_TILES", "32")
+        b = idx.search(q, 30, 4)
+        monkeypatch.delenv("MFLAT_IVF_TILES")
+    parity.exact(a[0], a[1], b[0], b[1])
