@@ -537,14 +537,12 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     const char* Xb = (const char*)p.X + rowBeg * p.dpad * ES;
     const char* Qb = (const char*)p.Q + (int64_t)qb * kBN * p.dpad * ES;
     // IVF: this thread's four query rows (ldRow + 32 i), gathered by entry
-    const char* qrow[4];
+    const char* qrow[IVF ? 4 : 1] = {};
+    if constexpr (IVF) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if constexpr (IVF) {
+        for (int i = 0; i < 4; ++i) {
             const int q = sQi[ldRow + 32 * i];
             qrow[i] = q >= 0 ? (const char*)p.Q + (int64_t)q * p.dpad * ES : nullptr;
-        } else {
-            qrow[i] = Qb + (int64_t)(ldRow + 32 * i) * p.dpad * ES;
         }
     }
     fx4 rx[4], rq[4], rn;
@@ -564,6 +562,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     auto gload = [&](int tile, int kc) {
         const char* xs = Xb + ((int64_t)tile * kBM) * p.dpad * ES + kc * 4096 + tid * 16;
         const int qo = kc * 128 + ldCol * 4;
+        const char* qs = Qb + qo;
         const bool zx = S != kF32 && halfTail && kc == nk - 1 && tid >= 128;
         const bool zq = S != kF32 && halfTail && kc == nk - 1 && (tid & 7) >= 4;
 #pragma unroll
@@ -571,7 +570,11 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
             rx[i] = fx4{0.0f, 0.0f, 0.0f, 0.0f};
             rq[i] = fx4{0.0f, 0.0f, 0.0f, 0.0f};
             if (!zx) rx[i] = *(const fx4*)(xs + (int64_t)i * 32 * p.dpad * ES);
-            if (!zq && qrow[i]) rq[i] = *(const fx4*)(qrow[i] + qo);
+            if constexpr (IVF) {
+                if (!zq && qrow[i]) rq[i] = *(const fx4*)(qrow[i] + qo);
+            } else {
+                if (!zq) rq[i] = *(const fx4*)(qs + (int64_t)(ldRow + 32 * i) * p.dpad * ES);
+            }
         }
         if (METRIC == 0 && kc == 0 && tid < kBM / 4)
             rn = *(const fx4*)(p.xnorm + rowBeg + (int64_t)tile * kBM + tid * 4);
