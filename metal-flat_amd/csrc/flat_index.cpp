@@ -252,11 +252,7 @@ struct FlatIndex::Impl {
         pl.R0 = r;
         pl.stride = (int)(nb / r);
         const double lambda = (double)k * (double)r / (double)nb;
-        // A tighter speculative rank means fewer survivors in the full pass
-        // (each costs an exact test and a store in the scan epilogue) at the
-        // price of more queries re-scanned (a retry batch costs the full pass's
-        // time per query block of kBN); ~1% misses balances the two.
-        pl.j = chooseJ(k, lambda, 0.01);
+        pl.j = chooseSpeculativeRank(k, lambda, mb, nb, r);
         pl.j2 = chooseJ(k, lambda, 1e-9);
         splitPlan(r, (int)mb, dpad, storage, pl.rps0, pl.nsplit0, true, 1, concurrency(kPassSample));
         pl.cap0 = (int)pl.rps0;
@@ -268,6 +264,44 @@ struct FlatIndex::Impl {
         pl.perQuery = std::max({(size_t)pl.nsplit0 * pl.cap0, (size_t)pl.nsplit1 * pl.cap1,
                                 pl.Rb ? (size_t)pl.nsplitb * pl.capb : (size_t)0});
         return pl;
+    }
+
+    // Speculative rank j. A tighter rank means fewer survivors in the full
+    // pass (~j nb / R0 a query, each an exact test and a store in the scan
+    // epilogue); a query whose j-th sample bound admits fewer than k rows
+    // (probability P(Poisson(lambda) >= j), floored at 3e-4: the sample is a
+    // fixed stride, so a few queries miss at every j) is retried, and retries
+    // cost per batch, not per query: a host round trip (~130 us of idle
+    // device) plus a pass over the database per retried block of kBN queries.
+    // j minimises the expected sum, with the measured rates of this part
+    // (C1-C3 shapes): ~0.12 ns a survivor fp32 (0.16 fp16/bf16), ~120 (700)
+    // TFLOP/s a pass; never below the rank of a 1% miss rate (the second
+    // sample level's plan assumes it). Measured sweeps: C1 j = 2 / 3 / 4 / 5
+    // -> 1.61 / 2.13 / 2.11 / 1.51 M QPS (6 / 0 / 0 / 1 queries retried), the
+    // rule picks 3; C3 j = 3 / 4 / 5 -> 122.3 / 122.6 / 123.0 ms, it picks 3.
+    int chooseSpeculativeRank(int k, double lambda, int64_t mb, int64_t nbRows, int64_t r) const {
+        const bool f32 = storage == kF32;
+        const double tSurv = f32 ? 0.12e-9 : 0.16e-9;
+        const double tBlock = (double)nbRows * kBN * dpad * 2.0 / (f32 ? 120e12 : 700e12);
+        const double tTrip = 130e-6;
+        const double perJ = (double)mb * ((double)nbRows / (double)r) * tSurv;
+        int best = k;
+        double bestCost = 1e300;
+        double term = std::exp(-lambda), cdf = term;   // P(X = j - 1), P(X <= j - 1)
+        for (int j = 1; j <= k; ++j) {
+            const double pj = std::min(std::max(3e-4, 1.0 - cdf), 1.0 - 1e-16);   // P(X >= j), floored
+            const double pAny = -std::expm1((double)mb * std::log1p(-pj));
+            const double blocks = std::max(1.0, std::ceil((double)mb * pj / kBN));
+            const double cost = perJ * j + pAny * (tTrip + blocks * tBlock);
+            if (cost < bestCost) {
+                bestCost = cost;
+                best = j;
+            }
+            if (perJ * j > bestCost) break;   // survivors alone exceed the best
+            term *= lambda / j;
+            cdf += term;
+        }
+        return std::max(best, chooseJ(k, lambda, 0.01));
     }
 
     // Second sample level. The full pass's survivors scale with the speculative
