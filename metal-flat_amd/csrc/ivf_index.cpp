@@ -335,17 +335,18 @@ struct IvfIndex::Impl {
     // makes every work item wide / narrow; both compute the same keys, so the
     // results never depend on it.
     // PQ work items: adc_tile_queries(M) queries, wide only.
-    // Large d (a 128-query tile beyond scan_resident's LDS): 128-query items
-    // on the LDS-tiled kernel only, so every pass of a search computes its
-    // keys with the same kernel (MFLAT_IVF_TILES = 32 there picks 32-query
-    // scan_resident items instead, where their tile fits).
+    // Large d (a 128-query tile beyond scan_resident's LDS): the 128-query
+    // items run the LDS-tiled kernel, the 32-query ones scan_resident where
+    // their tile fits (else every item is wide). The two kernels issue the
+    // same MFMA sequence per (query, row) pair, so their keys are
+    // bit-identical and passes may mix them.
     int narrowMax() const {
         if (pq()) return 0;
         if (const char* e = std::getenv("MFLAT_IVF_TILES")) {
             if (std::atoi(e) == 128) return 0;
             if (std::atoi(e) == 32 && ivf_narrow_fits(dpad, storage)) return -1;
         }
-        if (!resident_scan_fits(dpad, storage)) return 0;
+        if (!resident_scan_fits(dpad, storage) && !ivf_narrow_fits(dpad, storage)) return 0;
         return kBN - kIvfNarrow;
     }
     int wideWidth() const { return pq() ? adc_tile_queries(pqM) : kBN; }

@@ -251,15 +251,19 @@ def test_very_large_dim(gpu_ok, d):
         check(idx, x, q, 10, 3, L2)
 
 
-def test_large_dim_tiles_compute_identical_keys(gpu_ok, monkeypatch):
-    """At d = 256 the LDS-tiled kernel runs the 128-query items; forcing
-    32-query items (scan_resident, whose tile fits at 32 queries) switches
-    kernels. Integer data keeps every sum exact in any accumulation order, so
-    the two must agree bit for bit."""
-    x, q = int_case(6_000, 140, 256, 16, seed=55)
-    with build(x, 12) as idx:
-        a = idx.search(q, 30, 4)
-        monkeypatch.setenv("MFLAT_IVF_TILES", "32")
-        b = idx.search(q, 30, 4)
+@pytest.mark.parametrize("d,metric", [(256, L2), (768, IP)])
+def test_large_dim_tiles_compute_identical_keys(gpu_ok, monkeypatch, d, metric):
+    """Above d = 128 the 128-query items run the LDS-tiled kernel and the
+    32-query ones scan_resident, and a search mixes them: their keys must be
+    bit-identical on float data. All-wide (tiled only), all-narrow (resident
+    only) and the default mix must return the same bits."""
+    x, q = datagen.unit_normal(nb=8_000, nq=200, d=d, seed=55 + d)
+    with build(x, 16, metric) as idx:
+        mixed = idx.search(q, 50, 6)
+        out = []
+        for tiles in ("128", "32"):
+            monkeypatch.setenv("MFLAT_IVF_TILES", tiles)
+            out.append(idx.search(q, 50, 6))
         monkeypatch.delenv("MFLAT_IVF_TILES")
-    parity.exact(a[0], a[1], b[0], b[1])
+    for o in out:
+        parity.exact(mixed[0], mixed[1], o[0], o[1])
