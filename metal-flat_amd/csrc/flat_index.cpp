@@ -313,7 +313,10 @@ struct FlatIndex::Impl {
     // fp32 ~60 TMAC/s, fp16/bf16 ~420 TMAC/s resident (~330 tiled), ~0.15 ns
     // per survivor, ~15 ns per query for the extra select.
     void planSecondSample(Plan& pl, int64_t mb, int k, int64_t r) const {
-        if (small_scan_fits((int)std::min<int64_t>(mb, 1 << 30), dpad, storage)) return;
+        if (small_scan_fits((int)std::min<int64_t>(mb, 1 << 30), dpad, storage)) {
+            planSecondSampleSmall(pl, mb, k, r);
+            return;
+        }
         const double tMac = storage == kF32 ? 1.0 / 60e12
                             : resident_scan_fits(dpad, storage) ? 1.0 / 420e12 : 1.0 / 330e12;
         const double tSurv = 0.15e-9, tSelQ = 15e-9;
@@ -331,6 +334,41 @@ struct FlatIndex::Impl {
             }
         }
         if (!pl.Rb) return;
+        finishSecondSample(pl, mb, k, r);
+    }
+
+    // Second sample level of a small batch. Small batches stream the database
+    // once whatever the bound, so the bound only sets how many survivors the
+    // full pass stores for the per-query select: ~j nb / R0 (R0 is capped at
+    // the select's LDS buffer), spread as the j-th order statistic of the
+    // sample, P(count > C) ~ P(Gamma(j, 1) > C R0 / nb). A query above the
+    // select's LDS buffer reads its candidates from global memory on every
+    // select pass (measured ~230 us at 10M x 96, against ~25 us in LDS); a
+    // second sample of Rb = f R0 rows under the first bound (one more small
+    // scan and select, ~30 us) gives ~jb nb / Rb survivors, jb at a 1e-5 miss
+    // rate (a miss costs another pass over the database).
+    void planSecondSampleSmall(Plan& pl, int64_t mb, int k, int64_t r) const {
+        const int buf = pl.nsplit1 <= kSelLargeMaxSplit ? kSelLdsLarge : kSelLds;
+        const double x = (double)buf * (double)r / (double)nb;
+        double term = std::exp(-x), tail = term;
+        for (int i = 1; i < pl.j; ++i) {
+            term *= x / i;
+            tail += term;
+        }
+        const double pAny = -std::expm1((double)mb * std::log1p(-std::min(tail, 1.0 - 1e-16)));
+        if (pAny * 230e-6 <= 30e-6) return;
+        for (int f = 4; f <= 64; f *= 2) {
+            const int64_t Rb = roundUp(f * r, kBM);
+            if (2 * Rb > nb) break;
+            pl.Rb = Rb;
+            pl.jb = chooseJ(k, (double)k * (double)Rb / (double)nb, 1e-5);
+            if ((double)pl.jb * (double)nb / (double)Rb <= kSelLds / 4) break;
+        }
+        if (!pl.Rb) return;
+        finishSecondSample(pl, mb, k, r);
+    }
+
+    void finishSecondSample(Plan& pl, int64_t mb, int k, int64_t r) const {
         pl.strideb = (int)(nb / pl.Rb);
         splitPlan(pl.Rb, (int)mb, dpad, storage, pl.rpsb, pl.nsplitb, true, 1, concurrency(kPassSample));
         const double eb = (double)pl.j * (double)pl.Rb / (double)r;   // expected stored per query

@@ -18,6 +18,7 @@
 #include <cmath>
 #include <cstdio>
 #include <type_traits>
+#include <utility>
 #include <stdexcept>
 #include <string>
 
@@ -1224,7 +1225,13 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
                 for (int e = 0; e < U; ++e) cur[hh][e] = ld(wave, 0, hh, e);
         }
     }
-    for (int b = wave; b < nblk; b += 4) {
+    // One 32-row block of the wave. NEXT: whether block b + 4 exists and is
+    // prefetched. The last block of a wave is a separate instantiation, so
+    // the prefetch of every other block is unconditional: with a branch
+    // around it the compiler's wait for the row norms has to fit both paths
+    // and waits for the prefetch as well.
+    auto block = [&](const int b, auto nextTag) {
+        constexpr bool NEXT = decltype(nextTag)::value;
         // The block's row norms are loaded BEFORE the next block's prefetch:
         // vector-memory loads complete in order, so waiting for norms loaded
         // after the prefetch would wait for the whole prefetch too.
@@ -1259,7 +1266,6 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
                 }
             }
         };
-        const bool hasNext = b + 4 < nblk;
         if constexpr (G > 0) {
 #pragma unroll
             for (int t = 0; t < GB; ++t) {
@@ -1268,12 +1274,15 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
                 for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
                     for (int e = 0; e < U; ++e) x[hh][e] = buf[hh][t][e];
-                if (hasNext) {
+                if constexpr (NEXT) {
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
                         for (int e = 0; e < U; ++e) buf[hh][t][e] = ld(b + 4, t, hh, e);
                 }
+                // Keeps the prefetch of step t issued before step t's MFMAs
+                // (left alone, the scheduler sinks all of it to the block end).
+                __builtin_amdgcn_sched_barrier(0);
                 step(x, t);
             }
         } else {
@@ -1286,12 +1295,13 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
                 for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
                     for (int e = 0; e < U; ++e) nx[hh][e] = cur[hh][e];
-                if (nbk < nblk) {
+                if (NEXT || !lastT) {
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
                         for (int e = 0; e < U; ++e) nx[hh][e] = ld(nbk, nt, hh, e);
                 }
+                __builtin_amdgcn_sched_barrier(0);
                 step(cur, t);
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh)
@@ -1337,7 +1347,10 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
                 }
             }
         }
-    }
+    };
+    int b = wave;
+    for (; b + 4 < nblk; b += 4) block(b, std::true_type{});
+    if (b < nblk) block(b, std::false_type{});
 
     __syncthreads();
     if (tid < 16 * NQB && tid < p.nq) p.cnt[(int64_t)tid * p.nsplit + split] = sCnt[tid];
@@ -1417,15 +1430,27 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
     };
     if (inLds) {
         if (ns >= 256) {
-            // many splits with few candidates each (small batches): every
-            // thread copies its own splits; no offset search per element
-            for (int i = 0; i < per; ++i) {
-                const int sidx = s0 + i;
-                if (sidx >= ns) break;
-                const int n = min(p.cnt[qbase + sidx], p.cap);
-                const int o = sOff[sidx];
-                const uint2* src = p.cand + (qbase + sidx) * p.cap;
-                for (int e = 0; e < n; ++e) sBuf[o + e] = composite(src[e]);
+            // many splits with few candidates each (small batches): thread t's
+            // splits [s0, s0 + per) hold the flat elements [sOff[s0],
+            // sOff[s0 + per]); a split cursor walks them (no offset search per
+            // element), eight loads in flight
+            if (s0 < ns) {
+                const int E1 = sOff[min(s0 + per, ns)];
+                int cur = s0;
+                for (int e0 = sOff[s0]; e0 < E1; e0 += 8) {
+                    uint64_t v[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const int e = e0 + u;
+                        if (e < E1) {
+                            while (sOff[cur + 1] <= e) ++cur;
+                            v[u] = composite(p.cand[(qbase + cur) * p.cap + (e - sOff[cur])]);
+                        }
+                    }
+#pragma unroll
+                    for (int u = 0; u < 8; ++u)
+                        if (e0 + u < E1) sBuf[e0 + u] = v[u];
+                }
             }
         } else {
             // eight offset searches and loads per thread in flight
@@ -2144,9 +2169,13 @@ void launch_select(const SelectParams& p, hipStream_t s) {
     // the split offsets (dynamic LDS) reach (kMaxSplit + 1) ints, above the
     // default dynamic-LDS limit of a launch
     static const bool attr = [] {
-        for (const void* f : {(const void*)select_kernel<kSelLds>, (const void*)select_kernel<kSelLdsSmall>})
-            if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)((kMaxSplit + 1) * sizeof(int))) != hipSuccess)
+        const std::pair<const void*, int> fs[] = {
+            {(const void*)select_kernel<kSelLds>, kMaxSplit},
+            {(const void*)select_kernel<kSelLdsSmall>, kMaxSplit},
+            {(const void*)select_kernel<kSelLdsLarge>, kSelLargeMaxSplit}};
+        for (const auto& f : fs)
+            if (hipFuncSetAttribute(f.first, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)((f.second + 1) * sizeof(int))) != hipSuccess)
                 throw std::runtime_error("select: cannot raise the dynamic LDS limit");
         return true;
     }();
@@ -2156,8 +2185,13 @@ void launch_select(const SelectParams& p, hipStream_t s) {
     // A query's candidates are staged in LDS when they fit (else read from
     // global memory on every pass): the small buffer runs ~2.5x more blocks per
     // CU, for searches that expect few candidates per query.
+    // A batch of at most one block per CU loses nothing to the large buffer's
+    // occupancy (one block per CU): it keeps the ~j nb / R0 survivors of a
+    // small batch's full pass in LDS.
     if (p.expect > 0 && p.expect <= kSelLdsSmall)
         select_kernel<kSelLdsSmall><<<p.nq, 256, (size_t)(p.nsplit + 1) * sizeof(int), s>>>(p);
+    else if (p.nq <= 256 && p.nsplit <= kSelLargeMaxSplit && !(p.expect > 0 && p.expect <= kSelLds))
+        select_kernel<kSelLdsLarge><<<p.nq, 256, (size_t)(p.nsplit + 1) * sizeof(int), s>>>(p);
     else
         select_kernel<kSelLds><<<p.nq, 256, (size_t)(p.nsplit + 1) * sizeof(int), s>>>(p);
     prof_end(tok, s);

@@ -44,6 +44,8 @@ constexpr int kBN = 128;   // queries per scan tile
 constexpr int kBK = 32;    // dpad granularity; fp32 columns per LDS-staged chunk
 constexpr int kSelLds = 4096;   // candidates a select block holds in LDS
 constexpr int kSelLdsSmall = 1024;   // ... in its small-buffer variant (SelectParams::expect)
+constexpr int kSelLdsLarge = 12288;  // ... in its large-buffer variant (batches of <= 256 queries)
+constexpr int kSelLargeMaxSplit = 4096;   // splits the large variant indexes (LDS: 96 + 8 + 16 KB)
 constexpr int kTopMax = 1024;   // largest k (== MFLAT_MAX_K)
 constexpr int kMaxSplit = 16384;  // most database splits one select block indexes
 constexpr int kSmallMaxQ = 64;                 // scan_small serves batches up to this size
