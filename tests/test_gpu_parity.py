@@ -220,6 +220,24 @@ def test_uniform_small_batch(gpu_ok):
         parity.tolerant(gi, gd, oi, od, x, q[:nq], 0)
 
 
+def test_small_batch_second_sample_level(gpu_ok):
+    """Batches of 16 and 64 queries against 10M rows (C4's row count at d=16):
+    the plan adds the second sample level here (a 32,768-row sample scanned
+    under the 4,096-row sample's bound, its 3rd best bounding the full pass);
+    float data within the fp32 tolerance, integer data (exact ties at the
+    bound) bit-exact."""
+    x, q = datagen.uniform_pm1(nb=10_000_000, nq=64, d=16, seed=3)
+    for nq in (16, 64):
+        gi, gd, _ = run(x, q[:nq], 10, L2)
+        oi, od = orc(x, q[:nq], 10, L2)
+        parity.tolerant(gi, gd, oi, od, x, q[:nq], 0)
+    del x
+    x, q = datagen.sift_like(nb=10_000_000, nq=16, d=16, seed=5)
+    gi, gd, _ = run(x, q, 10, L2)
+    oi, od = orc(x, q, 10, L2)
+    parity.exact(gi, gd, oi, od)
+
+
 def test_kmeans_assign_k1(gpu_ok):
     """Reduced C5: nearest centroid (k=1) with exact self-matches."""
     cents, pts = datagen.kmeans_assign(npts=60_000, ncent=4096, seed=4)
