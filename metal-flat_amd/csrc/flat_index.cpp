@@ -167,6 +167,7 @@ struct Plan {
     int nsplitb = 1, capb = 1;
     int64_t rps1 = 0;
     int nsplit1 = 1, cap1 = 1;
+    double e1 = 0.0;      // expected full-pass survivors per query
     size_t perQuery = 0;  // candidate entries per query (max over levels)
 };
 
@@ -258,6 +259,7 @@ struct FlatIndex::Impl {
         pl.cap0 = (int)pl.rps0;
         splitPlan(nb, (int)mb, dpad, storage, pl.rps1, pl.nsplit1, true, 1, concurrency(kPassFull));
         const double e1 = (double)pl.j * (double)nb / (double)r;   // expected survivors
+        pl.e1 = e1;
         const int64_t perSplit = (int64_t)(2.0 * e1 / pl.nsplit1) + 64;
         pl.cap1 = std::max<int>({2 * k, 64, pow2ceil(perSplit)});
         planSecondSample(pl, mb, k, r);
@@ -375,6 +377,7 @@ struct FlatIndex::Impl {
         pl.capb = std::max<int>(32, pow2ceil((int64_t)(4.0 * eb / pl.nsplitb) + 16));
         // the full pass now expects jb nb / Rb survivors
         const double e1 = (double)pl.jb * (double)nb / (double)pl.Rb;
+        pl.e1 = e1;
         pl.cap1 = std::max<int>({2 * k, 64, pow2ceil((int64_t)(2.0 * e1 / pl.nsplit1) + 64)});
     }
 
@@ -557,6 +560,10 @@ struct FlatIndex::Impl {
             sp.out_ids = oIds; sp.out_vals = oVals;
             sp.tau_k_key = tauKk.as<float>(); sp.tau_k_id = tauKi.as<int>();
             sp.status = status.as<int>();
+            // survivors per query spread as the bound's order statistic
+            // (Gamma(j) / R0 of the rows): ~99% of queries stay under 3x the mean
+            // for j >= 3
+            sp.expect = (int)std::min(3.0 * pl.e1 + 64.0, 1e9);
             launch_select(sp, s);
         }
 

@@ -2172,6 +2172,7 @@ void launch_select(const SelectParams& p, hipStream_t s) {
         const std::pair<const void*, int> fs[] = {
             {(const void*)select_kernel<kSelLds>, kMaxSplit},
             {(const void*)select_kernel<kSelLdsSmall>, kMaxSplit},
+            {(const void*)select_kernel<kSelLdsMid>, kMaxSplit},
             {(const void*)select_kernel<kSelLdsLarge>, kSelLargeMaxSplit}};
         for (const auto& f : fs)
             if (hipFuncSetAttribute(f.first, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -2188,12 +2189,15 @@ void launch_select(const SelectParams& p, hipStream_t s) {
     // A batch of at most one block per CU loses nothing to the large buffer's
     // occupancy (one block per CU): it keeps the ~j nb / R0 survivors of a
     // small batch's full pass in LDS.
+    const size_t dyn = (size_t)(p.nsplit + 1) * sizeof(int);
     if (p.expect > 0 && p.expect <= kSelLdsSmall)
-        select_kernel<kSelLdsSmall><<<p.nq, 256, (size_t)(p.nsplit + 1) * sizeof(int), s>>>(p);
+        select_kernel<kSelLdsSmall><<<p.nq, 256, dyn, s>>>(p);
+    else if (p.expect > 0 && p.expect <= kSelLdsMid)
+        select_kernel<kSelLdsMid><<<p.nq, 256, dyn, s>>>(p);
     else if (p.nq <= 256 && p.nsplit <= kSelLargeMaxSplit && !(p.expect > 0 && p.expect <= kSelLds))
-        select_kernel<kSelLdsLarge><<<p.nq, 256, (size_t)(p.nsplit + 1) * sizeof(int), s>>>(p);
+        select_kernel<kSelLdsLarge><<<p.nq, 256, dyn, s>>>(p);
     else
-        select_kernel<kSelLds><<<p.nq, 256, (size_t)(p.nsplit + 1) * sizeof(int), s>>>(p);
+        select_kernel<kSelLds><<<p.nq, 256, dyn, s>>>(p);
     prof_end(tok, s);
     check_launch("select");
 }

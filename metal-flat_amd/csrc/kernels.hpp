@@ -44,6 +44,7 @@ constexpr int kBN = 128;   // queries per scan tile
 constexpr int kBK = 32;    // dpad granularity; fp32 columns per LDS-staged chunk
 constexpr int kSelLds = 4096;   // candidates a select block holds in LDS
 constexpr int kSelLdsSmall = 1024;   // ... in its small-buffer variant (SelectParams::expect)
+constexpr int kSelLdsMid = 2560;     // ... in its mid-size variant (SelectParams::expect)
 constexpr int kSelLdsLarge = 12288;  // ... in its large-buffer variant (batches of <= 256 queries)
 constexpr int kSelLargeMaxSplit = 4096;   // splits the large variant indexes (LDS: 96 + 8 + 16 KB)
 constexpr int kTopMax = 1024;   // largest k (== MFLAT_MAX_K)
@@ -137,8 +138,9 @@ struct SelectParams {
     float* tau_k_key;        // nullable: k-th smallest (key, id), or "no bound"
     int* tau_k_id;
     int* status;             // nullable: bit0 = a region overflowed, bit1 = fewer than k stored
-    int expect;              // expected stored candidates per query (0: unknown); <= kSelLdsSmall picks the
-                             // small-buffer variant
+    int expect;              // stored candidates per query that (nearly) every query stays under (0:
+                             // unknown): picks the smallest LDS buffer variant that holds it (more
+                             // blocks per CU); a query above its buffer reads from global memory
 };
 
 // Launchers (kernels.hip). All are asynchronous on `s` and bracket the launch
