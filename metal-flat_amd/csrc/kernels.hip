@@ -10,8 +10,9 @@
 //                MPS GEMM + per-tile merge pair (src/GemmDistance.mm:15-60,
 //                src/FlatIndex.mm:63-107,375-402).
 //   select       per-query exact top-k of the surviving candidates: radix select
-//                on the 64-bit (key, id) composite, then a bitonic sort of the k
-//                winners in LDS. It is the cross-tile merge.
+//                on the 64-bit (key, id) composite, then the k winners ordered in
+//                LDS (rank placement up to 256 of them, else a bitonic sort). It
+//                is the cross-tile merge.
 //   row norms / normalisation / packing helpers.
 #include "kernels.hpp"
 
@@ -1530,6 +1531,22 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
         }
     };
 
+    // Rank of element i of sTop[0, n) in ascending (composite, position) order:
+    // the elements before it. n <= 256 with one element per thread: a read pass
+    // of broadcast LDS loads and no barriers inside, against the ~28 barrier
+    // stages of a bitonic sort of 128. Composites of one query are distinct
+    // (an id is stored at most once); the position tie-break keeps the ranks a
+    // permutation regardless.
+    auto rankOf = [&](int n, int i, uint64_t x) -> int {
+        int r = 0;
+#pragma unroll 4
+        for (int jj = 0; jj < n; ++jj) {
+            const uint64_t y = sTop[jj];
+            r += (y < x || (y == x && jj < i)) ? 1 : 0;
+        }
+        return r;
+    };
+
     uint64_t T = ~0ull;   // take everything when c <= k
     if (c > k) {
         bool found = false;
@@ -1572,12 +1589,22 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
                     if ((((unsigned)(x >> 32) - omin) >> sh) == b) sTop[atomicAdd(&sN, 1)] = x;
                 });
                 __syncthreads();
-                int P = 1;
-                while (P < (int)hb) P <<= 1;
-                for (int i = (int)hb + tid; i < P; i += 256) sTop[i] = ~0ull;
-                __syncthreads();
-                sortTop(P);
-                T = sTop[kr - 1];
+                if (hb <= 256u) {
+                    // the bucket member of rank kr - 1 is T
+                    if (tid < (int)hb) {
+                        const uint64_t x = sTop[tid];
+                        if (rankOf((int)hb, tid, x) == (int)kr - 1) sT = x;
+                    }
+                    __syncthreads();
+                    T = sT;
+                } else {
+                    int P = 1;
+                    while (P < (int)hb) P <<= 1;
+                    for (int i = (int)hb + tid; i < P; i += 256) sTop[i] = ~0ull;
+                    __syncthreads();
+                    sortTop(P);
+                    T = sTop[kr - 1];
+                }
                 found = true;
                 __syncthreads();
             }
@@ -1621,11 +1648,24 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
     });
     __syncthreads();
     const int nsel = sN < kTopMax ? sN : kTopMax;
-    int P = 1;
-    while (P < nsel) P <<= 1;
-    for (int i = nsel + tid; i < P; i += 256) sTop[i] = ~0ull;
-    __syncthreads();
-    sortTop(P);
+    if (nsel <= 256) {
+        // every thread reads before any writes: one barrier between
+        uint64_t x = 0;
+        int r = 0;
+        if (tid < nsel) {
+            x = sTop[tid];
+            r = rankOf(nsel, tid, x);
+        }
+        __syncthreads();
+        if (tid < nsel) sTop[r] = x;
+        __syncthreads();
+    } else {
+        int P = 1;
+        while (P < nsel) P <<= 1;
+        for (int i = nsel + tid; i < P; i += 256) sTop[i] = ~0ull;
+        __syncthreads();
+        sortTop(P);
+    }
 
     const int orow = p.qmap ? p.qmap[q] : q;
     if (p.out_ids || p.out_vals) {
