@@ -322,12 +322,24 @@ __global__ void max_norm_kernel(const float* __restrict__ xn, int64_t n, unsigne
 // survivor in any of the 64 lanes. Only survivors take the exact
 // lexicographic test; they go to emit(slot, key, id), or, for k = 1, replace
 // the slot's running best.
-template <int METRIC, int PASS, int NB, int NS, class Emit>
+// LQ: the survivor-only state (bound key and id, query norm) is read from the
+// workgroup's LDS tables lq (entry bn * 32 + lq.r32 for slot bn) instead of
+// the register arrays tk / ti / qn, which the caller then leaves dead: in
+// kernels at the register limit this keeps survivor handling free of scratch
+// reloads, whose wait for vector memory also waits for every prefetch load in
+// flight.
+struct QTab {
+    const float* tk;
+    const int* ti;
+    const float* qn;
+    int r32;
+};
+template <int METRIC, int PASS, int NB, int NS, bool LQ = false, class Emit>
 __device__ __forceinline__ void filter_group(const fx16 (&acc)[NB], int g4, int b0, const fx4& xn4, int64_t r0,
                                              int64_t rowLim, int idStride, const int (&idb)[NB],
                                              const ScanParams& p, float (&tk)[NB], int (&ti)[NB],
                                              const float (&qn)[NB], float (&ft)[NB], const bool (&qv)[NB],
-                                             Emit&& emit) {
+                                             const QTab& lq, Emit&& emit) {
     bool f[4][NS];
     bool any = false;
 #pragma unroll
@@ -352,12 +364,13 @@ __device__ __forceinline__ void filter_group(const fx16 (&acc)[NB], int g4, int 
             const float dot = acc[bn][g4 * 4 + i];
             float key;
             if (METRIC == 0) {
-                const float t = fmaf(-2.0f, dot, qn[bn] + xn4[i]);
+                const float qnb = LQ ? lq.qn[bn * 32 + lq.r32] : qn[bn];
+                const float t = fmaf(-2.0f, dot, qnb + xn4[i]);
                 key = (t < 0.0f ? 0.0f : t) + 0.0f;
             } else {
                 key = -dot + 0.0f;
             }
-            if (PASS == kPassArgmin) {
+            if (PASS == kPassArgmin && !LQ) {
                 // k = 1: keep the lexicographically smallest (key, id)
                 if (rv && qv[bn] && (key < tk[bn] || (key == tk[bn] && id < ti[bn]))) {
                     tk[bn] = key;
@@ -367,7 +380,9 @@ __device__ __forceinline__ void filter_group(const fx16 (&acc)[NB], int g4, int 
                 }
                 continue;
             }
-            if (rv && qv[bn] && (key < tk[bn] || (key == tk[bn] && id <= ti[bn]))) emit(bn, key, id);
+            const float tkb = LQ ? lq.tk[bn * 32 + lq.r32] : tk[bn];
+            const int tib = LQ ? lq.ti[bn * 32 + lq.r32] : ti[bn];
+            if (rv && qv[bn] && (key < tkb || (key == tkb && id <= tib))) emit(bn, key, id);
         }
     }
 }
@@ -676,7 +691,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
                     fx4 xn4 = {0.0f, 0.0f, 0.0f, 0.0f};
                     if (METRIC == 0) xn4 = xnr[bm][g4];
                     filter_group<METRIC, PASS, 2, 2>(acc[bm], g4, 0, xn4, r0, rowLim, IVF ? 1 : p.id_stride, idb,
-                                                  p, tk, ti, qn, ft, qv,
+                                                  p, tk, ti, qn, ft, qv, QTab{nullptr, nullptr, nullptr, 0},
                                                   [&](int bn, float key, int id) {
                         const int ql = wn * 64 + bn * 32 + r32;
                         const int slot = atomicAdd(&sCnt[ql], 1);
@@ -788,6 +803,12 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     __shared__ int sRingId[RING ? 4 * kRing : 1];
     __shared__ int sRingQ[RING ? 4 * kRing : 1];
     __shared__ int sRingN[4];
+    // fp16/bf16 (a whole slice of operands in registers): survivor-only query
+    // state in LDS (filter_group's LQ), not registers
+    constexpr bool LQ = S != kF32 && PASS != kPassArgmin;
+    __shared__ float sLTk[LQ ? TQ : 1];
+    __shared__ int sLTi[LQ ? TQ : 1];
+    __shared__ float sLQn[LQ ? TQ : 1];
     __shared__ int sEnt[IVF ? TQ : 1];   // IVF: the tile's entries (-1: empty slot)
     __shared__ int sQi[IVF ? TQ : 1];    // ... their queries
     __shared__ int sReg[IVF ? TQ : 1];   // ... their candidate regions
@@ -898,6 +919,23 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
             ft[bn] = qv[bn] ? -tk[bn] : INFINITY;
         }
     }
+    if constexpr (LQ) {
+        if (tid < TQ) {
+            int q;
+            bool v;
+            if constexpr (IVF) {
+                q = sQi[tid];
+                v = q >= 0;
+            } else {
+                q = qb * kBN + tid;
+                v = q < p.nq;
+            }
+            sLTk[tid] = v ? p.tau_key[q] : 0.0f;
+            sLTi[tid] = v ? p.tau_id[q] : -1;
+            sLQn[tid] = (METRIC == 0 && v) ? p.qnorm[q] : 0.0f;
+        }
+    }
+    const QTab lqt{sLTk, sLTi, sLQn, r32};
     __syncthreads();
 
     // Rows: [rowBeg, rowBeg + 64 nsl) of the database; filter rows count from
@@ -999,8 +1037,8 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
                 if (METRIC == 0) xn4 = *(const fx4*)(sXn + wave * 64 + rl);
 #pragma unroll
                 for (int bp = 0; bp < (NB + 1) / 2; ++bp)
-                    filter_group<METRIC, PASS, NB, NB == 1 ? 1 : 2>(acc[bm], g4, 2 * bp, xn4, r0, rowLim, idStride,
-                                                                     idb, p, tk, ti, qn, ft, qv,
+                    filter_group<METRIC, PASS, NB, NB == 1 ? 1 : 2, LQ>(acc[bm], g4, 2 * bp, xn4, r0, rowLim,
+                                                                         idStride, idb, p, tk, ti, qn, ft, qv, lqt,
                                                   [&](int bn, float key, int id) {
                         const int ql = bn * 32 + r32;
                         const int pos = RING ? atomicAdd(&sRingN[wave], 1) : kRing;
@@ -1016,8 +1054,13 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
         }
     };
 
+    // fp16/bf16: a workgroup-uniform base and a 32-bit lane offset (one
+    // address register, not a 64-bit pair held across the slice loop, which
+    // the G = 4 instantiations would spill and reload in the loop)
+    const float* xnw = p.xnorm + rowBeg;
     auto norm = [&](int sl) -> float {
-        return METRIC == 0 ? p.xnorm[rowBeg + (int64_t)sl * 64 + lane] : 0.0f;
+        if constexpr (S == kF32) return METRIC == 0 ? p.xnorm[rowBeg + (int64_t)sl * 64 + lane] : 0.0f;
+        return METRIC == 0 ? xnw[sl * 64 + lane] : 0.0f;
     };
 
     // Writes the wave's staged survivors to their candidate regions once at
