@@ -49,7 +49,7 @@ PEAK_HBM_GBS = 8000.0
 # roofline.traffic for the configuration it was measured on, null otherwise.
 MEASURED_TRAFFIC_BYTES = {
     ("C2", 10_000, "f32"): 4.76e9,
-    ("C2", 10_000, "f16"): 2.298e9,
+    ("C2", 10_000, "f16"): 1.907e9,
     ("C3", 10_000, "f32"): 287.8e9,
     ("C4", 1, "f32"): 3.880e9,
     ("C4", 1, "f16"): 1.960e9,
