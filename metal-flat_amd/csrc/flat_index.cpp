@@ -250,13 +250,7 @@ struct FlatIndex::Impl {
             return pl;
         }
         pl.direct = false;
-        pl.R0 = r;
-        pl.stride = (int)(nb / r);
-        const double lambda = (double)k * (double)r / (double)nb;
-        pl.j = chooseSpeculativeRank(k, lambda, mb, nb, r);
-        pl.j2 = chooseJ(k, lambda, 1e-9);
-        splitPlan(r, (int)mb, dpad, storage, pl.rps0, pl.nsplit0, true, 1, concurrency(kPassSample));
-        pl.cap0 = (int)pl.rps0;
+        setFirstSample(pl, mb, k, r);
         splitPlan(nb, (int)mb, dpad, storage, pl.rps1, pl.nsplit1, true, 1, concurrency(kPassFull));
         const double e1 = (double)pl.j * (double)nb / (double)r;   // expected survivors
         pl.e1 = e1;
@@ -266,6 +260,18 @@ struct FlatIndex::Impl {
         pl.perQuery = std::max({(size_t)pl.nsplit0 * pl.cap0, (size_t)pl.nsplit1 * pl.cap1,
                                 pl.Rb ? (size_t)pl.nsplitb * pl.capb : (size_t)0});
         return pl;
+    }
+
+    // First sample level of r rows: every row is stored (the select takes the
+    // j-th, j2-th and k-th best of each query).
+    void setFirstSample(Plan& pl, int64_t mb, int k, int64_t r) const {
+        pl.R0 = r;
+        pl.stride = (int)(nb / r);
+        const double lambda = (double)k * (double)r / (double)nb;
+        pl.j = chooseSpeculativeRank(k, lambda, mb, nb, r);
+        pl.j2 = chooseJ(k, lambda, 1e-9);
+        splitPlan(r, (int)mb, dpad, storage, pl.rps0, pl.nsplit0, true, 1, concurrency(kPassSample));
+        pl.cap0 = (int)pl.rps0;
     }
 
     // Speculative rank j. A tighter rank means fewer survivors in the full
@@ -336,6 +342,15 @@ struct FlatIndex::Impl {
             }
         }
         if (!pl.Rb) return;
+        // With a second level, the first one only seeds that level's bound
+        // (~j Rb / R0 candidates a query) and the retries' fallback bounds: a
+        // first sample of max(4 k, 1,024) rows keeps its select, over every
+        // sample row, in the 1,024-entry buffer (~8 blocks per CU, not 3).
+        const int64_t r1 = roundUp(std::max<int64_t>(4LL * k, kSelLdsSmall), kBM);
+        if (r1 < r) {
+            r = r1;
+            setFirstSample(pl, mb, k, r);
+        }
         finishSecondSample(pl, mb, k, r);
     }
 
@@ -549,6 +564,8 @@ struct FlatIndex::Impl {
             tauBk.ensure((size_t)mb * 4); tauBi.ensure((size_t)mb * 4);
             SelectParams sp = selectParams(mb, pl.nsplitb, pl.capb, pl.jb, pl.jb);
             sp.tau_k_key = tauBk.as<float>(); sp.tau_k_id = tauBi.as<int>();
+            // ~j Rb / R0 candidates a query, spread as an order statistic
+            sp.expect = (int)std::min(3.0 * (double)pl.j * (double)pl.Rb / (double)pl.R0 + 64.0, 1e9);
             launch_select(sp, s);
             launch_tau_min(tauSk.as<float>(), tauSi.as<int>(), tauBk.as<float>(), tauBi.as<int>(), mb, s);
         }
