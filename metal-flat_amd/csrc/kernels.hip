@@ -1407,10 +1407,12 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
 // One workgroup (256 threads) per query. The (key, id) composites are distinct
 // (an id appears at most once per query), so the k-th smallest composite T is
 // unique and the winners are exactly the composites <= T.
-template <int NBUF>
+// KT: winners (and k-th bucket members) the block can hold, k <= KT; a
+// smaller KT (k <= 256) leaves LDS for more blocks per CU.
+template <int NBUF, int KT>
 __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
     __shared__ uint64_t sBuf[NBUF];
-    __shared__ uint64_t sTop[kTopMax];
+    __shared__ uint64_t sTop[KT];
     extern __shared__ int sOff[];   // nsplit + 1 entries (dynamic)
     __shared__ unsigned sHist[256];
     __shared__ unsigned sSel[3];
@@ -1625,7 +1627,7 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
             for_each([&](uint64_t x) { atomicAdd(&sHist[((unsigned)(x >> 32) - omin) >> sh], 1u); });
             findBucket((unsigned)k);
             const unsigned b = sSel[0], kr = sSel[1], hb = sSel[2];
-            if (hb <= (unsigned)kTopMax) {
+            if (hb <= (unsigned)KT) {
                 if (tid == 0) sN = 0;
                 __syncthreads();
                 for_each([&](uint64_t x) {
@@ -1686,11 +1688,11 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
     for_each([&](uint64_t x) {
         if (x <= T) {
             const int pos = atomicAdd(&sN, 1);
-            if (pos < kTopMax) sTop[pos] = x;
+            if (pos < KT) sTop[pos] = x;
         }
     });
     __syncthreads();
-    const int nsel = sN < kTopMax ? sN : kTopMax;
+    const int nsel = sN < KT ? sN : KT;
     if (nsel <= 256) {
         // every thread reads before any writes: one barrier between
         uint64_t x = 0;
@@ -2244,6 +2246,23 @@ void launch_fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hip
     check_launch("fill_u64");
 }
 
+// A query's candidates are staged in LDS when they fit (else read from global
+// memory on every pass): the small buffer runs ~2.5x more blocks per CU, for
+// searches that expect few candidates per query. A batch of at most one block
+// per CU loses nothing to the large buffer's occupancy (one block per CU): it
+// keeps the ~j nb / R0 survivors of a small batch's full pass in LDS.
+template <int KT>
+static void launch_select_kt(const SelectParams& p, size_t dyn, hipStream_t s) {
+    if (p.expect > 0 && p.expect <= kSelLdsSmall)
+        select_kernel<kSelLdsSmall, KT><<<p.nq, 256, dyn, s>>>(p);
+    else if (p.expect > 0 && p.expect <= kSelLdsMid)
+        select_kernel<kSelLdsMid, KT><<<p.nq, 256, dyn, s>>>(p);
+    else if (p.nq <= 256 && p.nsplit <= kSelLargeMaxSplit && !(p.expect > 0 && p.expect <= kSelLds))
+        select_kernel<kSelLdsLarge, KT><<<p.nq, 256, dyn, s>>>(p);
+    else
+        select_kernel<kSelLds, KT><<<p.nq, 256, dyn, s>>>(p);
+}
+
 void launch_select(const SelectParams& p, hipStream_t s) {
     if (p.nq <= 0) return;
     if (p.k < 1 || p.k > kTopMax || p.j < 1 || p.j > p.k || p.j2 < 1 || p.j2 > p.k)
@@ -2253,10 +2272,14 @@ void launch_select(const SelectParams& p, hipStream_t s) {
     // default dynamic-LDS limit of a launch
     static const bool attr = [] {
         const std::pair<const void*, int> fs[] = {
-            {(const void*)select_kernel<kSelLds>, kMaxSplit},
-            {(const void*)select_kernel<kSelLdsSmall>, kMaxSplit},
-            {(const void*)select_kernel<kSelLdsMid>, kMaxSplit},
-            {(const void*)select_kernel<kSelLdsLarge>, kSelLargeMaxSplit}};
+            {(const void*)select_kernel<kSelLds, kTopMax>, kMaxSplit},
+            {(const void*)select_kernel<kSelLdsSmall, kTopMax>, kMaxSplit},
+            {(const void*)select_kernel<kSelLdsMid, kTopMax>, kMaxSplit},
+            {(const void*)select_kernel<kSelLdsLarge, kTopMax>, kSelLargeMaxSplit},
+            {(const void*)select_kernel<kSelLds, kTopSmall>, kMaxSplit},
+            {(const void*)select_kernel<kSelLdsSmall, kTopSmall>, kMaxSplit},
+            {(const void*)select_kernel<kSelLdsMid, kTopSmall>, kMaxSplit},
+            {(const void*)select_kernel<kSelLdsLarge, kTopSmall>, kSelLargeMaxSplit}};
         for (const auto& f : fs)
             if (hipFuncSetAttribute(f.first, hipFuncAttributeMaxDynamicSharedMemorySize,
                                     (int)((f.second + 1) * sizeof(int))) != hipSuccess)
@@ -2266,21 +2289,11 @@ void launch_select(const SelectParams& p, hipStream_t s) {
     (void)attr;
     void* tok;
     prof_begin(kFamSelect, s, &tok);
-    // A query's candidates are staged in LDS when they fit (else read from
-    // global memory on every pass): the small buffer runs ~2.5x more blocks per
-    // CU, for searches that expect few candidates per query.
-    // A batch of at most one block per CU loses nothing to the large buffer's
-    // occupancy (one block per CU): it keeps the ~j nb / R0 survivors of a
-    // small batch's full pass in LDS.
     const size_t dyn = (size_t)(p.nsplit + 1) * sizeof(int);
-    if (p.expect > 0 && p.expect <= kSelLdsSmall)
-        select_kernel<kSelLdsSmall><<<p.nq, 256, dyn, s>>>(p);
-    else if (p.expect > 0 && p.expect <= kSelLdsMid)
-        select_kernel<kSelLdsMid><<<p.nq, 256, dyn, s>>>(p);
-    else if (p.nq <= 256 && p.nsplit <= kSelLargeMaxSplit && !(p.expect > 0 && p.expect <= kSelLds))
-        select_kernel<kSelLdsLarge><<<p.nq, 256, dyn, s>>>(p);
-    else
-        select_kernel<kSelLds><<<p.nq, 256, dyn, s>>>(p);
+    // k <= 256: a 2 KB winner buffer instead of 8 KB (select_kernel<1024>:
+    // ~12 KB of LDS a block, ~13 blocks per CU instead of 8)
+    if (p.k <= kTopSmall) launch_select_kt<kTopSmall>(p, dyn, s);
+    else launch_select_kt<kTopMax>(p, dyn, s);
     prof_end(tok, s);
     check_launch("select");
 }

@@ -48,6 +48,7 @@ constexpr int kSelLdsMid = 2560;     // ... in its mid-size variant (SelectParam
 constexpr int kSelLdsLarge = 12288;  // ... in its large-buffer variant (batches of <= 256 queries)
 constexpr int kSelLargeMaxSplit = 4096;   // splits the large variant indexes (LDS: 96 + 8 + 16 KB)
 constexpr int kTopMax = 1024;   // largest k (== MFLAT_MAX_K)
+constexpr int kTopSmall = 256;   // select's winner buffer for k <= kTopSmall
 constexpr int kMaxSplit = 16384;  // most database splits one select block indexes
 constexpr int kSmallMaxQ = 64;                 // scan_small serves batches up to this size
 constexpr size_t kSmallMaxLds = 64 * 1024;     // ... whose query tile fits this much LDS
