@@ -194,6 +194,8 @@ class FlatIndex:
         _check(load().mflat_flat_search(self._h, q.ctypes.data, m, int(k), ids.ctypes.data,
                                          dist.ctypes.data, ctypes.byref(used)), "mflat_flat_search")
         ku = used.value
+        if m > 0 and ku == kk:   # every column produced: the buffers are the result
+            return ids, dist, ku
         flat_i = ids.reshape(-1)[: m * ku].reshape(m, ku)
         flat_d = dist.reshape(-1)[: m * ku].reshape(m, ku)
         return flat_i.copy(), flat_d.copy(), ku
