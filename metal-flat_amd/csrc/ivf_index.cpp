@@ -114,6 +114,12 @@ struct IvfIndex::Impl {
 
     // IVF-PQ (pqM > 0): residual product quantization instead of stored rows
     int pqM = 0, dsub = 0;
+    // Diagnostics knobs, read once when the index is created (never during a
+    // search): MFLAT_IVF_TILES = 128 / 32 makes every work item wide / narrow,
+    // MFLAT_IVF_CAP_B = n overrides the full pass's region capacity. Results
+    // never depend on them, only the work done; 0 = not set.
+    int tilesKnob = 0, capBKnob = 0;
+    bool trace = false;   // MFLAT_TRACE: per-search survivor statistics on stderr
     bool rerankReq = false;    // keep the full rows for exact reranking (set before build)
     bool fullStored = false;   // ... latched at build
     DevBuf dCodes, dPqc, dNorms, dT, dCentD, dFull;
@@ -342,10 +348,8 @@ struct IvfIndex::Impl {
     // bit-identical and passes may mix them.
     int narrowMax() const {
         if (pq()) return 0;
-        if (const char* e = std::getenv("MFLAT_IVF_TILES")) {
-            if (std::atoi(e) == 128) return 0;
-            if (std::atoi(e) == 32 && ivf_narrow_fits(dpad, storage)) return -1;
-        }
+        if (tilesKnob == 128) return 0;
+        if (tilesKnob == 32 && ivf_narrow_fits(dpad, storage)) return -1;
         if (!resident_scan_fits(dpad, storage) && !ivf_narrow_fits(dpad, storage)) return 0;
         return kBN - kIvfNarrow;
     }
@@ -376,10 +380,7 @@ struct IvfIndex::Impl {
     // MFLAT_IVF_CAP_B (diagnostics) overrides capB to exercise the retries;
     // the results never depend on it, only the work done.
     int capB(int k, int nprobe) const {
-        if (const char* e = std::getenv("MFLAT_IVF_CAP_B")) {
-            const int v = std::atoi(e);
-            if (v >= 1) return v;
-        }
+        if (capBKnob >= 1) return capBKnob;
         if (nprobe == 1) return capR();
         // PQ: the bound is the k-th of the whole nearest cell (A covers it, or
         // A2 does), so that cell's region holds at most k survivors and the
@@ -444,7 +445,7 @@ struct IvfIndex::Impl {
         wt.build(probe.as<int>(), mb, nprobe, nprobe, nlist, dCellOrder.as<int>(), narrowMax(), s);
         scanPass(kPassFull, mb, nprobe, nprobe, nprobe + 1, cb, qr, tauAk.as<float>(), tauAi.as<int>(),
                  pos.as<int>(), s, true);
-        if (std::getenv("MFLAT_TRACE")) {
+        if (trace) {
             std::vector<int> c((size_t)mb * (nprobe + 1));
             HIPC(hipMemcpyAsync(c.data(), cnt.p, c.size() * sizeof(int), hipMemcpyDeviceToHost, s));
             HIPC(hipStreamSynchronize(s));
@@ -491,7 +492,7 @@ struct IvfIndex::Impl {
             const int cr = capR();
             const size_t perQ = (size_t)nprobe * cr * sizeof(uint2);
             const int chunk = (int)std::max<size_t>(1, std::min<size_t>(over.size(), kCandBudget / perQ));
-            if (std::getenv("MFLAT_TRACE"))
+            if (trace)
                 std::fprintf(stderr, "[mflat trace] ivf: %d of %d queries overflowed (cap %d), retried with cap %d\n",
                              (int)over.size(), mb, cb, cr);
             for (size_t o = 0; o < over.size(); o += (size_t)chunk) {
@@ -652,6 +653,13 @@ IvfIndex::IvfIndex(int dim, Metric metric, int nlist, Storage storage, int pqM) 
     d_->storage = storage;
     d_->esize = elem_bytes(storage);
     d_->nlistReq = nlist;
+    auto knob = [](const char* name) {
+        const char* v = std::getenv(name);
+        return v ? std::atoi(v) : 0;
+    };
+    d_->tilesKnob = knob("MFLAT_IVF_TILES");
+    d_->capBKnob = knob("MFLAT_IVF_CAP_B");
+    d_->trace = knob("MFLAT_TRACE") != 0;
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
         (void)hipGetLastError();

@@ -1,12 +1,11 @@
 // SPDX-License-Identifier: Apache-2.0
 // mflat_abi.cpp -- the C ABI (include/mflat.h) over the engine.
 //
-// Same shell as the reference's c/mflat.cpp:32-129: an opaque handle wrapping
+// Behaviour of the reference's c/mflat.cpp:32-129: an opaque handle wrapping
 // the engine plus a std::mutex that serialises add / reset / search per handle;
 // every entry point is a try/catch that maps exceptions to status codes;
 // results are copied into caller-owned buffers with row stride k_used.
 #include <algorithm>
-#include <atomic>
 #include <cstring>
 #include <mutex>
 #include <new>
@@ -36,15 +35,6 @@ Metric conv(mflat_metric_t m) {
         case MFLAT_METRIC_COSINE: return Metric::Cosine;
         default: return Metric::L2;
     }
-}
-
-// reference c/mflat.cpp:52-59: the C handler type differs from the C++ one, so
-// calls go through a trampoline (never a function-pointer cast).
-std::atomic<mflat_log_handler_t> gCHandler{nullptr};
-std::atomic<void*> gCUser{nullptr};
-void cLogTrampoline(mflat_amd::LogLevel lvl, const char* msg, void*) {
-    if (auto h = gCHandler.load(std::memory_order_acquire))
-        h(static_cast<mflat_log_level_t>(lvl), msg, gCUser.load(std::memory_order_acquire));
 }
 
 template <class F>
@@ -104,20 +94,10 @@ MFLAT_API const char* mflat_status_str(mflat_status_t s) {
     return "unknown";
 }
 
-MFLAT_API void mflat_set_log_handler(mflat_log_handler_t h, void* user) {
-    gCUser.store(user, std::memory_order_release);
-    gCHandler.store(h, std::memory_order_release);
-    mflat_amd::setLogHandler(h ? &cLogTrampoline : nullptr, nullptr);
-}
-MFLAT_API void mflat_set_log_level(mflat_log_level_t l) {
-    int v = static_cast<int>(l);
-    if (v < 0) v = 0;
-    if (v > 3) v = 3;
-    mflat_amd::setLogLevel(static_cast<mflat_amd::LogLevel>(v));
-}
-MFLAT_API mflat_log_level_t mflat_log_level(void) {
-    return static_cast<mflat_log_level_t>(mflat_amd::logLevel());
-}
+// the engine's router holds the caller's handler and user value as given
+MFLAT_API void mflat_set_log_handler(mflat_log_handler_t h, void* user) { mflat_amd::logRoute(h, user); }
+MFLAT_API void mflat_set_log_level(mflat_log_level_t l) { mflat_amd::logSetThreshold(l); }
+MFLAT_API mflat_log_level_t mflat_log_level(void) { return mflat_amd::logThreshold(); }
 
 MFLAT_API mflat_flat_index_t* mflat_flat_create_ex(int dim, mflat_metric_t metric, mflat_storage_t storage,
                                                    mflat_status_t* st) {

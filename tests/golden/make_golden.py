@@ -7,7 +7,8 @@ reference tree exists and `make -C oracle ref` has built oracle/_ref:
 distance_primitives.npz  inputs and outputs of the reference's own
                          src/Distance.h dot / sqL2 / rowSqNorms / normalizeRows,
                          computed by that code (oracle/_ref).
-flat_small.npz           small flat searches (ties, padding, every metric) whose
+flat_small.npz           small flat searches (ties, padding, NaN and +-inf rows,
+                         every metric) whose
                          expected results are derived from the reference's
                          primitives: every (query, row) score by ref_score
                          (src/Distance.h:67-69), winners in the order strict '>'
@@ -80,6 +81,15 @@ def flat_cases():
     nanx = rng.standard_normal((40, 6)).astype(np.float32)
     nanx[3, 1] = np.nan
     cases["nan_row_l2"] = (nanx, rng.standard_normal((3, 6)).astype(np.float32), 40, 0)
+    # rows holding +inf / -inf: an L2 score of -inf is never inserted; an inner
+    # product of +inf is the best score there is (value +inf), one of -inf is
+    # never inserted. Queries have no zero coordinate (no inf * 0 = NaN).
+    infx = rng.standard_normal((50, 8)).astype(np.float32)
+    infx[7, 2] = np.inf
+    infx[19, 5] = -np.inf
+    infq = rng.standard_normal((4, 8)).astype(np.float32)
+    cases["inf_rows_l2"] = (infx, infq, 50, 0)
+    cases["inf_rows_ip"] = (infx, infq, 50, 1)
     return cases
 
 

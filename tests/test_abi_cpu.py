@@ -30,6 +30,24 @@ def test_loads_and_exports_every_declared_symbol():
     assert set(syms) == set(mflat.SIGNATURES), set(syms) ^ set(mflat.SIGNATURES)
 
 
+def test_dynamic_symbols_are_the_c_abi_only():
+    """Like the reference's C library (hidden visibility, CMakeLists.txt:44-47),
+    libmflat.so's dynamic symbol table holds the C ABI and nothing else: no
+    kernel host stubs, no C++ internals."""
+    import shutil
+    import subprocess
+
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-D", "--defined-only", mflat.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    names = {ln.split()[-1] for ln in out.splitlines() if ln.strip()}
+    extra = sorted(n for n in names if not n.startswith("mflat_"))
+    assert not extra, extra[:10]
+    assert set(header_symbols()) <= names
+
+
 def test_version_status_maxk():
     lib = mflat.load()
     assert lib.mflat_version() == b"0.1.0"
@@ -111,13 +129,18 @@ def test_log_level_roundtrip_and_handler():
 
     @mflat.LOG_HANDLER_T
     def handler(level, msg, user):
-        got.append((level, msg.decode()))
+        got.append((level, msg.decode(), user))
 
     old = lib.mflat_log_level()
     try:
+        # out-of-range thresholds clamp to [INFO, OFF]
+        lib.mflat_set_log_level(7)
+        assert lib.mflat_log_level() == mflat.MFLAT_LOG_OFF
+        lib.mflat_set_log_level(-3)
+        assert lib.mflat_log_level() == mflat.MFLAT_LOG_INFO
         lib.mflat_set_log_level(mflat.MFLAT_LOG_WARN)
         assert lib.mflat_log_level() == mflat.MFLAT_LOG_WARN
-        lib.mflat_set_log_handler(handler, None)
+        lib.mflat_set_log_handler(handler, ctypes.c_void_p(0x5EED))
         idx = mflat.FlatIndex(8)
         if idx.ready():
             pytest.skip("a GPU is present; the no-device message is not emitted")
@@ -127,7 +150,8 @@ def test_log_level_roundtrip_and_handler():
         with pytest.raises(mflat.MflatError) as e:
             idx.search(np.ones((1, 8), np.float32), 2)
         assert e.value.status == mflat.MFLAT_ERR_NOT_READY
-        assert any(lv == mflat.MFLAT_LOG_ERROR and "HIP device" in m for lv, m in got), got
+        assert any(lv == mflat.MFLAT_LOG_ERROR and "HIP device" in m for lv, m, _ in got), got
+        assert all(u == 0x5EED for _, _, u in got), got   # the registered user value, unchanged
         n = len(got)
         lib.mflat_set_log_level(mflat.MFLAT_LOG_OFF)
         with pytest.raises(mflat.MflatError):

@@ -160,16 +160,19 @@ def test_retries_exact_with_tiny_regions(gpu_ok, monkeypatch):
     x, q = datagen.gmm(nb=30_000, nq=500, d=64, ncenters=64, seed=19)
     with build(x, 64) as idx:
         gi, gv, _ = idx.search(q, 30, 12)
-        monkeypatch.setenv("MFLAT_IVF_CAP_B", "4")
+    # the knob is read when an index is created; the build is deterministic,
+    # so the second index holds the same cells
+    monkeypatch.setenv("MFLAT_IVF_CAP_B", "4")
+    with build(x, 64) as idx:
         ri, rv, _ = idx.search(q, 30, 12)
-        monkeypatch.delenv("MFLAT_IVF_CAP_B")
         parity.exact(ri, rv, gi, gv)
         check(idx, x, q, 30, 12, L2)
-        xi, qi = int_case(8_000, 200, 16, 4, seed=20)
+    xi, qi = int_case(8_000, 200, 16, 4, seed=20)
+    monkeypatch.setenv("MFLAT_IVF_CAP_B", "2")
     with build(xi, 16) as idx:
-        monkeypatch.setenv("MFLAT_IVF_CAP_B", "2")
         check(idx, xi, qi, 40, 1, L2, exact=True)
         check(idx, xi, qi, 40, 5, L2, exact=True)
+    monkeypatch.delenv("MFLAT_IVF_CAP_B")
 
 
 @pytest.mark.parametrize("storage", [mflat.MFLAT_STORAGE_F16, mflat.MFLAT_STORAGE_BF16])
@@ -212,12 +215,13 @@ def test_tile_widths_compute_identical_keys(gpu_ok, monkeypatch):
     x, q = datagen.gmm(nb=50_000, nq=900, d=128, ncenters=128, seed=26)
     with build(x, 96) as idx:
         ref = idx.search(q, 100, 10)
-        for tiles in ("128", "32"):
-            monkeypatch.setenv("MFLAT_IVF_TILES", tiles)
-            got = idx.search(q, 100, 10)
-            parity.exact(got[0], got[1], ref[0], ref[1])
-        monkeypatch.delenv("MFLAT_IVF_TILES")
         check(idx, x, q, 100, 10, L2)
+    for tiles in ("128", "32"):
+        monkeypatch.setenv("MFLAT_IVF_TILES", tiles)   # read when the index is created
+        with build(x, 96) as idx:
+            got = idx.search(q, 100, 10)
+        parity.exact(got[0], got[1], ref[0], ref[1])
+    monkeypatch.delenv("MFLAT_IVF_TILES")
 
 
 # ---- dims beyond scan_resident's 128-query tile: the LDS-tiled kernel --------
@@ -260,10 +264,11 @@ def test_large_dim_tiles_compute_identical_keys(gpu_ok, monkeypatch, d, metric):
     x, q = datagen.unit_normal(nb=8_000, nq=200, d=d, seed=55 + d)
     with build(x, 16, metric) as idx:
         mixed = idx.search(q, 50, 6)
-        out = []
-        for tiles in ("128", "32"):
-            monkeypatch.setenv("MFLAT_IVF_TILES", tiles)
+    out = []
+    for tiles in ("128", "32"):
+        monkeypatch.setenv("MFLAT_IVF_TILES", tiles)   # read when the index is created
+        with build(x, 16, metric) as idx:
             out.append(idx.search(q, 50, 6))
-        monkeypatch.delenv("MFLAT_IVF_TILES")
+    monkeypatch.delenv("MFLAT_IVF_TILES")
     for o in out:
         parity.exact(mixed[0], mixed[1], o[0], o[1])
