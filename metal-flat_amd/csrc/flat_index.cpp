@@ -16,9 +16,11 @@
 //                after all k that did).
 //   retry:       queries failing that test rerun L1 alone, with the guaranteed
 //                bound (too few passed) or with the k-th best of what was stored
-//                (a region overflowed; regions hold >= 2k entries, so each
-//                retry admits at least k fewer rows). Exactness never depends on
-//                the estimate, only the amount of work does.
+//                (a region overflowed); a query overflowing again reruns once
+//                more under its new k-th with one region sized by its count,
+//                which cannot overflow. The device builds these work lists, so
+//                a search is a fixed launch sequence (retries()). Exactness
+//                never depends on the estimate, only the amount of work does.
 //
 // Small databases (nb <= max(2*R0, kSelLds)) skip the levels: one unbounded pass.
 #include "flat_index.hpp"
@@ -61,6 +63,7 @@ constexpr int64_t kTargetWGSmall = 4096;        // scan_small workgroups (HBM st
 constexpr size_t kCandBudget = size_t(1536) << 20;  // candidate workspace per batch
 constexpr size_t kStageBytes = size_t(256) << 20;   // host->device staging chunk
 constexpr int64_t kRetryMinTiles = 2;   // tiles per split in the retries of a large batch
+constexpr int kRetryMax = 256;          // queries one device-built retry window takes (large batches)
 
 int64_t roundUp(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
@@ -80,6 +83,42 @@ struct DevBuf {
         bytes = 0;
     }
     template <class T> T* as() const { return static_cast<T*>(p); }
+};
+
+// Two ints of pinned host memory: the counters a batch reads back at its end.
+struct PinnedInts {
+    int* p = nullptr;
+    void ensure() {
+        if (!p) HIPC(hipHostMalloc((void**)&p, 4 * sizeof(int), hipHostMallocDefault));
+    }
+    void release() {
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+    }
+};
+
+// Device storage of the retry work lists (kernels.hpp RetryLists).
+struct RetryStore {
+    DevBuf fail, lvl, idx, tk, ti, qoff, qcap, qcnt, counters;
+    void ensure(int mb, int rmax) {
+        fail.ensure((size_t)mb * 4);
+        lvl.ensure((size_t)mb);
+        for (DevBuf* b : {&idx, &tk, &ti, &qcap}) b->ensure((size_t)rmax * 4);
+        qcnt.ensure((size_t)rmax * kPoolCntStride * 4);
+        qoff.ensure((size_t)rmax * sizeof(int64_t));
+        counters.ensure(4 * sizeof(int));
+    }
+    RetryLists lists() const {
+        RetryLists l;
+        l.fail = fail.as<int>(); l.lvl = lvl.as<unsigned char>();
+        l.idx = idx.as<int>(); l.tk = tk.as<float>(); l.ti = ti.as<int>();
+        l.qoff = qoff.as<int64_t>(); l.qcap = qcap.as<int>(); l.qcnt = qcnt.as<int>();
+        l.counters = counters.as<int>();
+        return l;
+    }
+    void release() {
+        for (DevBuf* b : {&fail, &lvl, &idx, &tk, &ti, &qoff, &qcap, &qcnt, &counters}) b->release();
+    }
 };
 
 // Smallest j in [1, k] with P(Poisson(lambda) >= j) <= tail: the chance that a
@@ -155,7 +194,7 @@ struct Plan {
     int64_t R0 = 0;       // sample rows
     int stride = 1;       // sample row r is database row r*stride
     int j = 1;            // speculative rank
-    int j2 = 1;           // second, looser speculative rank (first retry)
+    int j2 = 1;           // looser speculative rank (first retry of a query with too few rows)
     int64_t rps0 = 0;
     int nsplit0 = 1, cap0 = 1;
     // optional second sample (0 rows: none), scanned with the first one's
@@ -204,8 +243,16 @@ struct FlatIndex::Impl {
     DevBuf stage, inv, qin, outIds, outVals;
     DevBuf qbuf, qh, qnorm, cand, cnt;
     DevBuf tauSk, tauSi, tauS2k, tauS2i, tauGk, tauGi, tauKk, tauKi, tauBk, tauBi, status;
-    DevBuf cQ, cQn, cTk, cTi, cIdx, cSel;
-    DevBuf best;
+    DevBuf cQ, cQn;
+    DevBuf best, total;
+    RetryStore rl;
+    PinnedInts hostCounters;
+    // Diagnostics knobs, read once when the index is created: MFLAT_RETRY_WINDOW
+    // = n limits a device-built retry window to n queries, MFLAT_RETRY_POOL = n
+    // the round-2 pool to n entries (0 = not set). They exercise the host's
+    // fallback windows; results never depend on them, only the work done.
+    int retryWindow = 0;
+    int64_t retryPool = 0;
 
     int kernMetric() const { return metric == Metric::L2 ? 0 : 1; }
     float emptyValue() const { return metric == Metric::L2 ? INFINITY : -INFINITY; }
@@ -474,19 +521,24 @@ struct FlatIndex::Impl {
         sm.stride = stride;
     }
 
-    void scan(const void* Xs, const float* xns, int64_t nrows, int64_t rps, int nsplit, int idStride,
-              const void* Q, const float* qn, int nq, const float* tk, const int* ti, int cap,
-              hipStream_t s, int pass = kPassFull, bool allowSmall = true) {
-        const int nqb = (nq + kBN - 1) / kBN;
-        cand.ensure((size_t)nq * nsplit * cap * sizeof(uint2));
-        cnt.ensure((size_t)nq * nsplit * sizeof(int));
+    ScanParams scanParams(const void* Xs, const float* xns, int64_t nrows, int64_t rps, int nsplit, int idStride,
+                          const void* Q, const float* qn, int nq, const float* tk, const int* ti, int cap) const {
         ScanParams p;
         std::memset(&p, 0, sizeof p);
         p.X = Xs; p.xnorm = xns; p.xnorm_max = xnMax; p.nrows = nrows; p.rows_per_split = rps; p.nsplit = nsplit;
         p.id_stride = idStride;
-        p.Q = Q; p.qnorm = qn; p.nq = nq; p.nqb = nqb; p.dpad = dpad;
+        p.Q = Q; p.qnorm = qn; p.nq = nq; p.nqb = (nq + kBN - 1) / kBN; p.dpad = dpad;
         p.tau_key = tk; p.tau_id = ti;
         p.cand = cand.as<uint2>(); p.cnt = cnt.as<int>(); p.cap = cap;
+        return p;
+    }
+
+    void scan(const void* Xs, const float* xns, int64_t nrows, int64_t rps, int nsplit, int idStride,
+              const void* Q, const float* qn, int nq, const float* tk, const int* ti, int cap,
+              hipStream_t s, int pass = kPassFull, bool allowSmall = true) {
+        cand.ensure((size_t)nq * nsplit * cap * sizeof(uint2));
+        cnt.ensure((size_t)nq * nsplit * sizeof(int));
+        const ScanParams p = scanParams(Xs, xns, nrows, rps, nsplit, idStride, Q, qn, nq, tk, ti, cap);
         launch_scan_filter(p, kernMetric(), pass, storage, s, allowSmall);
     }
 
@@ -522,12 +574,13 @@ struct FlatIndex::Impl {
         }
         tauSk.ensure((size_t)mb * 4); tauSi.ensure((size_t)mb * 4);
         tauS2k.ensure((size_t)mb * 4); tauS2i.ensure((size_t)mb * 4);
+        total.ensure((size_t)mb * 4);
         tauGk.ensure((size_t)mb * 4); tauGi.ensure((size_t)mb * 4);
         tauKk.ensure((size_t)mb * 4); tauKi.ensure((size_t)mb * 4);
         status.ensure((size_t)mb * 4);
 
+        // tauS holds "no bound" from the query preparation
         if (pl.direct) {
-            launch_fill_tau_none(tauSk.as<float>(), tauSi.as<int>(), mb, s);
             scan(X.p, xn.as<float>(), nb, pl.rps1, pl.nsplit1, 1, Q, qn, mb,
                  tauSk.as<float>(), tauSi.as<int>(), pl.cap1, s);
             SelectParams sp = selectParams(mb, pl.nsplit1, pl.cap1, k, 1);
@@ -540,11 +593,10 @@ struct FlatIndex::Impl {
         ensureSample(smp[0], pl.R0, pl.stride, s);
         if (pl.Rb) ensureSample(smp[1], pl.Rb, pl.strideb, s);
         if (traceOn())
-            std::fprintf(stderr, "[mflat trace] mb=%d k=%d nb=%lld R0=%lld stride=%d j=%d j2=%d "
+            std::fprintf(stderr, "[mflat trace] mb=%d k=%d nb=%lld R0=%lld stride=%d j=%d "
                          "L0 %dx%d Rb=%lld jb=%d L1 splits=%d cap=%d\n", mb, k, (long long)nb, (long long)pl.R0,
-                         pl.stride, pl.j, pl.j2, pl.nsplit0, pl.cap0, (long long)pl.Rb, pl.jb, pl.nsplit1, pl.cap1);
+                         pl.stride, pl.j, pl.nsplit0, pl.cap0, (long long)pl.Rb, pl.jb, pl.nsplit1, pl.cap1);
         // L0: sample, no bound -> speculative (j-th) and guaranteed (k-th) bounds
-        launch_fill_tau_none(tauSk.as<float>(), tauSi.as<int>(), mb, s);
         scan(smp[0].X.p, smp[0].xn.as<float>(), pl.R0, pl.rps0, pl.nsplit0, pl.stride, Q, qn, mb,
              tauSk.as<float>(), tauSi.as<int>(), pl.cap0, s, kPassSample);
         {
@@ -577,6 +629,7 @@ struct FlatIndex::Impl {
             sp.out_ids = oIds; sp.out_vals = oVals;
             sp.tau_k_key = tauKk.as<float>(); sp.tau_k_id = tauKi.as<int>();
             sp.status = status.as<int>();
+            sp.total = total.as<int>();
             // survivors per query spread as the bound's order statistic
             // (Gamma(j) / R0 of the rows): ~99% of queries stay under 3x the mean
             // for j >= 3
@@ -584,70 +637,111 @@ struct FlatIndex::Impl {
             launch_select(sp, s);
         }
 
+        retries(mb, k, pl, Q, qn, oIds, oVals, s);
+    }
+
+    // Verification and retries, as a fixed launch sequence whose work list the
+    // device builds (no host round trip): a query is exact unless its
+    // full-pass select reported an overflow or fewer than k stored rows. One
+    // round (retry_plan, gather, pooled scan, select) reruns up to rmax of
+    // them, each with one candidate region of its own:
+    //   overflow: under the k-th best it stored, the region sized by the rows
+    //             it saw under its looser bound -- a subset, so the rerun is
+    //             final;
+    //   too few:  under the sample's j2-th best (rarely still too few), then
+    //             its guaranteed k-th, the region sized for that bound (if it
+    //             overflows, the next round is the final kind above).
+    // Launches with an empty list exit at once. Three counters come back with
+    // the batch's final synchronisation; only if a query is left (more than
+    // rmax failed, a region did not fit the pool, a rerun failed again) does
+    // the host run further rounds before returning. Every rerun either ends a
+    // query or moves it up its bound ladder, so the rounds terminate.
+    void retries(int mb, int k, const Plan& pl, const void* Q, const float* qn, int32_t* oIds, float* oVals,
+                 hipStream_t s) {
         const bool batchSmall = small_scan_fits(mb, dpad, storage);
-        // verification and retries. Per query, the bound used so far:
-        //   0 = speculative (j-th of the sample), 1 = looser speculative (j2-th),
-        //   2 = guaranteed (k-th of the sample or of a stored subset).
-        std::vector<int> st((size_t)mb);
-        HIPC(hipMemcpyAsync(st.data(), status.p, (size_t)mb * 4, hipMemcpyDeviceToHost, s));
-        HIPC(hipStreamSynchronize(s));
-        std::vector<int> level((size_t)mb, pl.j < k ? 0 : 2);
-        std::vector<int> live((size_t)mb);
-        for (int i = 0; i < mb; ++i) live[(size_t)i] = i;
-        for (int round = 0;; ++round) {
-            // sel: 0 -> tau from tauS2 (j2-th), 1 -> tauK (k-th stored), 2 -> tauG (k-th of sample)
-            std::vector<int> idx, sel;
-            for (int i : live) {
-                const int v = st[(size_t)i];
-                int& lv = level[(size_t)i];
-                if (v & 1) {                       // a region overflowed: tighten from stored
-                    idx.push_back(i); sel.push_back(1); lv = 2;
-                } else if ((v & 2) && lv < 2) {    // speculative bound admitted < k rows
-                    const bool useJ2 = lv == 0 && pl.j2 > pl.j;
-                    idx.push_back(i); sel.push_back(useJ2 ? 0 : 2); lv = useJ2 ? 1 : 2;
-                }
-            }
-            if (traceOn()) {
-                int no = 0;
-                for (int t : sel) no += t == 1;
-                std::fprintf(stderr, "[mflat trace] round %d: %d of %d queries refined (%d overflow, %d under)\n",
-                             round, (int)idx.size(), mb, no, (int)idx.size() - no);
-            }
-            if (idx.empty()) break;
-            if (round >= 24) throw std::runtime_error("flat search: bound refinement did not converge");
-            const int nf = (int)idx.size();
-            const int nfPad = (int)roundUp(nf, kBN);
-            cIdx.ensure((size_t)nf * 4); cSel.ensure((size_t)nf * 4);
-            cQ.ensure((size_t)nfPad * dpad * esize); cQn.ensure((size_t)nfPad * 4);
-            cTk.ensure((size_t)nf * 4); cTi.ensure((size_t)nf * 4);
-            HIPC(hipMemcpyAsync(cIdx.p, idx.data(), (size_t)nf * 4, hipMemcpyHostToDevice, s));
-            launch_gather_rows(Q, cIdx.as<int>(), nf, dpad * esize, cQ.p, nfPad, s);
-            launch_gather_f32(qn, cIdx.as<int>(), nf, cQn.as<float>(), s);
-            HIPC(hipMemcpyAsync(cSel.p, sel.data(), (size_t)nf * 4, hipMemcpyHostToDevice, s));
-            TauSources ts;
-            ts.key[0] = tauS2k.as<float>(); ts.id[0] = tauS2i.as<int>();
-            ts.key[1] = tauKk.as<float>();  ts.id[1] = tauKi.as<int>();
-            ts.key[2] = tauGk.as<float>();  ts.id[2] = tauGi.as<int>();
-            launch_gather_tau(ts, cIdx.as<int>(), cSel.as<int>(), nf, cTk.as<float>(), cTi.as<int>(), s);
-            int64_t rps;
-            int nsplit;
-            // Retries run the kernel family of the passes their bounds came
-            // from (the whole batch's), so every bound is compared with keys
-            // computed the same way (a guaranteed bound must admit its own rows).
-            splitPlan(nb, nf, dpad, storage, rps, nsplit, batchSmall, batchSmall ? 1 : kRetryMinTiles,
-                      concurrency(kPassRetry));
-            const int cap = std::max(2 * k, 64);
-            scan(X.p, xn.as<float>(), nb, rps, nsplit, 1, cQ.p, cQn.as<float>(), nf,
-                 cTk.as<float>(), cTi.as<int>(), cap, s, kPassRetry, batchSmall);
-            SelectParams sp = selectParams(nf, nsplit, cap, k, k);
-            sp.qmap = cIdx.as<int>();
+        // pooled capacities of the ladder's bounds: ~rank nb / R0 rows
+        // admitted, three times that (and at least k, so an overflowing rerun
+        // keeps a k-th best) before the final kind of rerun takes over
+        auto capFor = [&](int rank) {
+            const double e = (double)rank * (double)nb / std::max<double>(1.0, (double)pl.R0);
+            return (int)std::min<double>((double)std::max<int64_t>(nb, 1), std::max(3.0 * e + 256.0, (double)k));
+        };
+        RetryLadder lad;
+        std::memset(&lad, 0, sizeof lad);
+        if (pl.j2 > pl.j) {
+            lad.j2_key = tauS2k.as<float>(); lad.j2_id = tauS2i.as<int>();
+            lad.cap_j2 = capFor(pl.j2);
+        }
+        lad.g_key = tauGk.as<float>(); lad.g_id = tauGi.as<int>();
+        lad.cap_g = capFor(k);
+        // a window of rmax queries whose regions fit the candidate budget
+        int rmax = std::max(1, std::min(mb, retryWindow > 0 ? retryWindow : batchSmall ? kSmallMaxQ : kRetryMax));
+        const size_t perQ = (size_t)std::max(lad.cap_g, lad.cap_j2) * sizeof(uint2);
+        while (rmax > 1 && (size_t)rmax * perQ > kCandBudget) rmax = (rmax + 1) / 2;
+        const int rowsPad = (int)roundUp(rmax, kBN);
+        const int rowBytes = dpad * esize;
+        // Retries run the kernel family of the passes their bounds came from
+        // (the whole batch's), so every bound is compared with keys computed
+        // the same way (a guaranteed bound must admit its own rows). Pooled
+        // regions do not depend on the split plan: it only spreads the work.
+        // The split plan is made for one block of queries (a window rarely
+        // holds more): the launch covers rmax, and blocks past the device's
+        // count exit at once.
+        int64_t rps;
+        int nsplit;
+        splitPlan(nb, std::min(rmax, kBN), dpad, storage, rps, nsplit, batchSmall, batchSmall ? 1 : kRetryMinTiles,
+                  concurrency(kPassRetry));
+
+        rl.ensure(mb, rmax);
+        cQ.ensure((size_t)rowsPad * rowBytes);
+        cQn.ensure((size_t)rowsPad * 4);
+        // the pool is the candidate buffer, whose full-pass contents the
+        // full pass's select has consumed: at least one whole region of each
+        // rerun kind for a full window
+        cand.ensure((size_t)rmax * perQ);
+        const RetryLists L = rl.lists();
+
+        auto round = [&](bool first, bool drain) {
+            int64_t pool = (int64_t)(cand.bytes / sizeof(uint2));
+            if (retryPool > 0 && !drain) pool = std::min<int64_t>(pool, retryPool);
+            launch_retry_plan(status.as<int>(), mb, first ? 1 : 0, tauKk.as<float>(), tauKi.as<int>(),
+                              total.as<int>(), lad, pool, rmax, (int)std::max<int64_t>(nb, 1), L, s);
+            launch_gather_rows_dev(Q, qn, L.idx, L.counters + 1, rowBytes, cQ.p, cQn.as<float>(), rowsPad, s);
+            ScanParams p = scanParams(X.p, xn.as<float>(), nb, rps, nsplit, 1, cQ.p, cQn.as<float>(), rmax, L.tk,
+                                      L.ti, 1);
+            p.nq_dev = L.counters + 1;
+            p.qcnt = L.qcnt; p.qoff = L.qoff; p.qcap = L.qcap;
+            launch_scan_filter(p, kernMetric(), kPassRetry, storage, s, batchSmall);
+            SelectParams sp = selectParams(rmax, 1, 1, k, k);
+            sp.cnt = L.qcnt;
+            sp.qoff = L.qoff; sp.qcap = L.qcap;
+            sp.nq_dev = L.counters + 1;
+            sp.qmap = L.idx;
             sp.out_ids = oIds; sp.out_vals = oVals;
             sp.tau_k_key = tauKk.as<float>(); sp.tau_k_id = tauKi.as<int>();
             sp.status = status.as<int>();
+            sp.total = total.as<int>();
+            sp.fail_count = L.counters + 2;
+            // j2 reruns, the usual kind: ~j2 nb / R0 candidates
+            sp.expect = (int)std::min<double>(1.5 * std::max(pl.j2, 2) * (double)nb /
+                                              std::max<double>(1.0, (double)pl.R0) + 2.0 * k, 1e9);
             launch_select(sp, s);
-            HIPC(hipMemcpyAsync(st.data(), status.p, (size_t)mb * 4, hipMemcpyDeviceToHost, s));
+            hostCounters.ensure();
+            HIPC(hipMemcpyAsync(hostCounters.p, L.counters, 3 * sizeof(int), hipMemcpyDeviceToHost, s));
             HIPC(hipStreamSynchronize(s));
-            live = idx;
+            return hostCounters.p[0] - hostCounters.p[1] + hostCounters.p[2];   // queries left
+        };
+        int left = round(true, false);
+        if (traceOn())
+            std::fprintf(stderr, "[mflat trace] retries: %d of %d queries failed the full pass, %d rerun, %d left\n",
+                         hostCounters.p[0], mb, hostCounters.p[1], left);
+        // Host fallback: a pool of nb entries holds any single region, so
+        // every round schedules at least one query.
+        const int64_t limit = 4 * ((int64_t)mb / rmax + 2) + 3LL * mb;
+        for (int64_t r = 0; left > 0; ++r) {
+            if (r > limit) throw std::runtime_error("flat search: retries did not converge");
+            cand.ensure((size_t)std::max<int64_t>(nb, 1) * sizeof(uint2));
+            left = round(false, true);
         }
     }
 
@@ -680,17 +774,19 @@ struct FlatIndex::Impl {
             const int n = (int)std::min<int64_t>(mb, m - b0);
             const Plan pb = (n == mb) ? pl : plan(n, k);
             const int64_t nPad = roundUp(n, kBN);
-            qbuf.ensure((size_t)nPad * dpad * sizeof(float));
+            // queries in the database's element type (Cosine normalised first),
+            // their norms, and every query's first bound, in one launch
+            DevBuf& qs = storage == kF32 ? qbuf : qh;
+            qs.ensure((size_t)nPad * dpad * esize);
             qnorm.ensure((size_t)nPad * sizeof(float));
-            launch_pack_rows(dq + b0 * dim, n, dim, qbuf.as<float>(), nPad, dpad, s);
-            if (metric == Metric::Cosine) launch_normalize_rows(qbuf.as<float>(), n, dpad, s);
-            const void* qs = qbuf.p;
-            if (storage != kF32) {   // queries take the database's element type
-                qh.ensure((size_t)nPad * dpad * esize);
-                launch_round_rows(qbuf.as<float>(), nPad * dpad, storage, qh.p, s);
-                qs = qh.p;
+            const bool bounded = !argminPath(n, k);
+            if (bounded) {
+                tauSk.ensure((size_t)n * 4);
+                tauSi.ensure((size_t)n * 4);
             }
-            if (metric == Metric::L2) launch_row_norms(qs, n, dpad, storage, qnorm.as<float>(), s);
+            launch_prep_queries(dq + b0 * dim, n, dim, nPad, dpad, storage, metric == Metric::Cosine, qs.p,
+                                qnorm.as<float>(), bounded ? tauSk.as<float>() : nullptr,
+                                bounded ? tauSi.as<int>() : nullptr, s);
             searchBatch(n, k, pb, ids ? ids + b0 * k : nullptr, vals ? vals + b0 * k : nullptr, s);
         }
         HIPC(hipStreamSynchronize(s));
@@ -705,6 +801,8 @@ FlatIndex::FlatIndex(int dim, Metric metric, Storage storage) : d_(new Impl) {
     d_->metric = metric;
     d_->storage = storage;
     d_->esize = elem_bytes(storage);
+    if (const char* v = std::getenv("MFLAT_RETRY_WINDOW")) d_->retryWindow = std::max(0, std::atoi(v));
+    if (const char* v = std::getenv("MFLAT_RETRY_POOL")) d_->retryPool = std::max<long long>(0, std::atoll(v));
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
         (void)hipGetLastError();
@@ -735,8 +833,10 @@ FlatIndex::~FlatIndex() {
     for (DevBuf* b : {&d_->X, &d_->xn, &d_->stage, &d_->inv, &d_->qin, &d_->outIds,
                       &d_->outVals, &d_->qbuf, &d_->qh, &d_->qnorm, &d_->cand, &d_->cnt, &d_->tauSk, &d_->tauSi, &d_->tauS2k, &d_->tauS2i, &d_->maxBits,
                       &d_->tauGk, &d_->tauGi, &d_->tauKk, &d_->tauKi, &d_->tauBk, &d_->tauBi, &d_->status, &d_->cQ, &d_->cQn,
-                      &d_->cTk, &d_->cTi, &d_->cIdx, &d_->cSel, &d_->best})
+                      &d_->best, &d_->total})
         b->release();
+    d_->rl.release();
+    d_->hostCounters.release();
     if (d_->stream) (void)hipStreamDestroy(d_->stream);
 }
 

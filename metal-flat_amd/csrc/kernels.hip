@@ -16,6 +16,7 @@
 //   row norms / normalisation / packing helpers.
 #include "kernels.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <type_traits>
@@ -130,6 +131,59 @@ __global__ void row_norms_kernel(const void* __restrict__ v, int64_t n, int dpad
         }
     }
     out[r] = (float)s;
+}
+
+// One search batch's queries in one launch, a thread per row (rows < n_pad):
+// the caller's fp32 row (dim values) -> the zero-padded row of dpad elements
+// in the storage type; Cosine first scales it by float(1 / sqrt(s)), s the
+// sequential double sum of its squares (zero rows unchanged: the reference's
+// normalizeRows, src/Distance.h:50-60); qn = float of the sequential double
+// sum of the stored values' squares (rowSqNorms, src/Distance.h:40-47); the
+// row's bound set to "no bound" (+inf, -1) when tau_key is given. Rows
+// n .. n_pad are zero.
+template <int S>
+__global__ void prep_queries_kernel(const float* __restrict__ src, int64_t n, int dim, int64_t n_pad, int dpad,
+                                    int cosine, void* __restrict__ out, float* __restrict__ qn,
+                                    float* __restrict__ tau_key, int* __restrict__ tau_id) {
+    const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (r >= n_pad) return;
+    constexpr int PE = piece_elems<S>();
+    fx4* dst = (fx4*)out + r * (dpad / PE);
+    const bool live = r < n;
+    const float* row = src + r * dim;
+    float inv = 1.0f;
+    if (live && cosine) {
+        double s = 0.0;
+        for (int c = 0; c < dim; ++c) s += (double)row[c] * row[c];
+        if (s > 0.0) inv = (float)(1.0 / sqrt(s));
+    }
+    double nrm = 0.0;
+    for (int u = 0; u < dpad / PE; ++u) {
+        float v[PE];
+#pragma unroll
+        for (int e = 0; e < PE; ++e) {
+            const int c = u * PE + e;
+            float x = (live && c < dim) ? row[c] : 0.0f;
+            if (cosine) x *= inv;
+            if constexpr (S != kF32) x = from_bits<S>(to_bits<S>(x));
+            v[e] = x;
+            nrm += (double)x * x;
+        }
+        fx4 piece;
+        if constexpr (S == kF32) {
+            piece = fx4{v[0], v[1], v[2], v[3]};
+        } else {
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                piece[w] = __uint_as_float((uint32_t)to_bits<S>(v[2 * w]) | ((uint32_t)to_bits<S>(v[2 * w + 1]) << 16));
+        }
+        dst[u] = piece;
+    }
+    qn[r] = live ? (float)nrm : 0.0f;
+    if (tau_key && live) {
+        tau_key[r] = INFINITY;
+        tau_id[r] = -1;
+    }
 }
 
 // In-place L2 normalisation of fp32 row-major rows (reference
@@ -263,6 +317,108 @@ __global__ void gather_tau_kernel(TauSources src, const int* __restrict__ idx,
     const int w = sel[i];
     ko[i] = src.key[w][q];
     io[i] = src.id[w][q];
+}
+
+// ---------------------------------------------------------------------------
+// device-built retry work lists (flat search)
+// ---------------------------------------------------------------------------
+
+// One 1024-thread block: the plan of a retry round (RetryLists). Failing
+// queries are listed in ascending order (a block prefix count per 1024), then
+// thread 0 walks the list assigning bounds and pooled regions while they fit.
+__global__ void __launch_bounds__(1024) retry_plan_kernel(const int* __restrict__ status, int mb, int first,
+                                                          const float* __restrict__ tkK,
+                                                          const int* __restrict__ tiK,
+                                                          const int* __restrict__ total, RetryLadder lad,
+                                                          int64_t pool_entries, int rmax, int all_rows,
+                                                          RetryLists rl) {
+    __shared__ int sW[16];
+    __shared__ int sBase;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    if (tid == 0) sBase = 0;
+    __syncthreads();
+    for (int q0 = 0; q0 < mb; q0 += 1024) {
+        const int q = q0 + tid;
+        const bool f = q < mb && status[q] != 0;
+        if (first && q < mb) rl.lvl[q] = 0;
+        const unsigned long long bal = __ballot(f);
+        if (lane == 0) sW[wave] = __popcll(bal);
+        __syncthreads();
+        int base = sBase;
+        for (int w = 0; w < wave; ++w) base += sW[w];
+        if (f) rl.fail[base + __popcll(bal & ((1ull << lane) - 1ull))] = q;
+        __syncthreads();
+        if (tid == 0) {
+            int t = sBase;
+            for (int w = 0; w < 16; ++w) t += sW[w];
+            sBase = t;
+        }
+        __syncthreads();
+    }
+    if (tid != 0) return;
+    const int nfail = sBase;
+    int64_t off = 0;
+    int n = 0;
+    for (int i = 0; i < nfail && n < rmax; ++i) {
+        const int q = rl.fail[i];
+        const int st = status[q];
+        float bk = INFINITY;   // "no bound": every row with a finite key
+        int bi = -1;
+        int need = all_rows;
+        int step = rl.lvl[q];
+        if (st & 1) {
+            bk = tkK[q];
+            bi = tiK[q];
+            need = total[q] > 1 ? total[q] : 1;
+        } else {
+            if (step == 0 && lad.j2_key) {
+                bk = lad.j2_key[q];
+                bi = lad.j2_id[q];
+                need = lad.cap_j2;
+                step = 1;
+            } else if (step <= 1 && lad.g_key) {
+                bk = lad.g_key[q];
+                bi = lad.g_id[q];
+                need = lad.cap_g;
+                step = 2;
+            } else {
+                step = 3;
+            }
+        }
+        if (off + need > pool_entries) {
+            if (n == 0 && off == 0) continue;   // too large for this pool: a later round's larger pool
+            break;
+        }
+        rl.lvl[q] = (unsigned char)step;
+        rl.idx[n] = q;
+        rl.tk[n] = bk;
+        rl.ti[n] = bi;
+        rl.qoff[n] = off;
+        rl.qcap[n] = need;
+        rl.qcnt[(int64_t)n * kPoolCntStride] = 0;
+        off += need;
+        ++n;
+    }
+    rl.counters[0] = nfail;
+    rl.counters[1] = n;
+    rl.counters[2] = 0;
+}
+
+// rows idx[i] (i < *n) of src -> dst rows i; rows *n .. rows_pad zeroed; norms likewise
+__global__ void gather_rows_dev_kernel(const fx4* __restrict__ src, const float* __restrict__ qn,
+                                       const int* __restrict__ idx, const int* __restrict__ nptr, int rowP,
+                                       fx4* __restrict__ dst, float* __restrict__ dst_qn, int rows_pad) {
+    const int n = *nptr;
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (dst_qn && t < rows_pad) dst_qn[t] = t < n ? qn[idx[t]] : 0.0f;
+    const int64_t pieces = (int64_t)rows_pad * rowP;
+    for (int64_t i = t; i < pieces; i += (int64_t)gridDim.x * blockDim.x) {
+        const int r = (int)(i / rowP);
+        const int c = (int)(i - (int64_t)r * rowP);
+        dst[i] = r < n ? src[(int64_t)idx[r] * rowP + c] : fx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
 }
 
 // "No bound": (+inf, -1) admits every finite key and rejects +inf and NaN,
@@ -452,15 +608,26 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     } else {
         const int nwg = gridDim.x;
         const int bid = blockIdx.x;
-        const int full = (nwg / 8) * 8;
-        const int v = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
-        const int grpSize = p.nqb < kQGroup ? p.nqb : kQGroup;
-        const int grp = v / (grpSize * p.nsplit);
-        const int r = v - grp * grpSize * p.nsplit;
-        const int inGrp = p.nqb - grp * grpSize < grpSize ? p.nqb - grp * grpSize : grpSize;
-        split = r / inGrp;
-        qb = grp * grpSize + (r - split * inGrp);
+        if (PASS == kPassRetry && p.nq_dev) {
+            // A device-sized retry covers more query blocks than it usually
+            // fills: block-major order dispatches the live blocks' splits
+            // first, over every XCD, and the idle blocks trail.
+            qb = bid / p.nsplit;
+            split = bid - qb * p.nsplit;
+        } else {
+            const int full = (nwg / 8) * 8;
+            const int v = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
+            const int grpSize = p.nqb < kQGroup ? p.nqb : kQGroup;
+            const int grp = v / (grpSize * p.nsplit);
+            const int r = v - grp * grpSize * p.nsplit;
+            const int inGrp = p.nqb - grp * grpSize < grpSize ? p.nqb - grp * grpSize : grpSize;
+            split = r / inGrp;
+            qb = grp * grpSize + (r - split * inGrp);
+        }
     }
+    // A retry whose work list the device built: query blocks beyond it are idle.
+    const int nqv = (PASS == kPassRetry && p.nq_dev) ? *p.nq_dev : p.nq;
+    if (!IVF && qb * kBN >= nqv) return;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -507,7 +674,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
             if (qv[bn]) idb[bn] = p.ivf_pos[sEnt[ql]];
         } else {
             q = qb * kBN + wn * 64 + bn * 32 + r32;
-            qv[bn] = q < p.nq;
+            qv[bn] = q < nqv;
         }
         if (PASS == kPassArgmin) {   // running best of this lane, from "no bound"
             tk[bn] = INFINITY;
@@ -704,6 +871,10 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
                                 const int sp = atomicAdd(&p.cnt[sr], 1);
                                 if (sp < p.cap) p.cand[sr * p.cap + sp] = v;
                             }
+                        } else if (PASS == kPassRetry && p.qcnt) {   // pooled region of the query
+                            const int q = qb * kBN + ql;
+                            const int gs = atomicAdd(&p.qcnt[(int64_t)q * kPoolCntStride], 1);
+                            if (gs < p.qcap[q]) p.cand[p.qoff[q] + gs] = v;
                         } else if (slot < p.cap) {
                             const int64_t q = (int64_t)qb * kBN + ql;
                             p.cand[(q * p.nsplit + split) * p.cap + slot] = v;
@@ -739,7 +910,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
             if (sReg[tid] >= 0) p.cnt[sReg[tid]] = p.ivf_spill && sCnt[tid] > p.cap ? p.cap : sCnt[tid];
         } else {
             const int q = qb * kBN + tid;
-            if (q < p.nq) p.cnt[(int64_t)q * p.nsplit + split] = sCnt[tid];
+            if (q < nqv && !(PASS == kPassRetry && p.qcnt)) p.cnt[(int64_t)q * p.nsplit + split] = sCnt[tid];
         }
     }
 }
@@ -822,15 +993,26 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
         // Workgroup -> (query block, split): the XCD grouping of scan_filter.
         const int nwg = gridDim.x;
         const int bid = blockIdx.x;
-        const int full = (nwg / 8) * 8;
-        const int v = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
-        const int grpSize = p.nqb < kQGroup ? p.nqb : kQGroup;
-        const int grp = v / (grpSize * p.nsplit);
-        const int r = v - grp * grpSize * p.nsplit;
-        const int inGrp = p.nqb - grp * grpSize < grpSize ? p.nqb - grp * grpSize : grpSize;
-        split = r / inGrp;
-        qb = grp * grpSize + (r - split * inGrp);
+        if (PASS == kPassRetry && p.nq_dev) {
+            // A device-sized retry covers more query blocks than it usually
+            // fills: block-major order dispatches the live blocks' splits
+            // first, over every XCD, and the idle blocks trail.
+            qb = bid / p.nsplit;
+            split = bid - qb * p.nsplit;
+        } else {
+            const int full = (nwg / 8) * 8;
+            const int v = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
+            const int grpSize = p.nqb < kQGroup ? p.nqb : kQGroup;
+            const int grp = v / (grpSize * p.nsplit);
+            const int r = v - grp * grpSize * p.nsplit;
+            const int inGrp = p.nqb - grp * grpSize < grpSize ? p.nqb - grp * grpSize : grpSize;
+            split = r / inGrp;
+            qb = grp * grpSize + (r - split * inGrp);
+        }
     }
+    // A retry whose work list the device built: query blocks beyond it are idle.
+    const int nqv = (PASS == kPassRetry && p.nq_dev) ? *p.nq_dev : p.nq;
+    if (!IVF && qb * kBN >= nqv) return;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -902,7 +1084,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
             if (qv[bn]) idb[bn] = p.ivf_pos[sEnt[bn * 32 + r32]];
         } else {
             q = qb * kBN + bn * 32 + r32;
-            qv[bn] = q < p.nq;
+            qv[bn] = q < nqv;
         }
         if (PASS == kPassArgmin) {
             tk[bn] = INFINITY;
@@ -928,7 +1110,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
                 v = q >= 0;
             } else {
                 q = qb * kBN + tid;
-                v = q < p.nq;
+                v = q < nqv;
             }
             sLTk[tid] = v ? p.tau_key[q] : 0.0f;
             sLTi[tid] = v ? p.tau_id[q] : -1;
@@ -967,6 +1149,14 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     // survivors beyond a region's capacity go there, so one crowded cell does
     // not force a retry; the spill's count past cap still flags the overflow.
     auto store = [&](int ql, int slot, uint2 v) {
+        if constexpr (PASS == kPassRetry && !IVF) {
+            if (p.qcnt) {   // pooled region of the query (global slot counter)
+                const int q = qb * kBN + ql;
+                const int gs = atomicAdd(&p.qcnt[(int64_t)q * kPoolCntStride], 1);
+                if (gs < p.qcap[q]) p.cand[p.qoff[q] + gs] = v;
+                return;
+            }
+        }
         if (slot < p.cap) {
             p.cand[region(ql) * p.cap + slot] = v;
         } else if constexpr (IVF) {
@@ -1164,7 +1354,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
         if (tid < wk.z) p.cnt[sReg[tid]] = p.ivf_spill && sCnt[tid] > p.cap ? p.cap : sCnt[tid];
     } else if (tid < TQ) {
         const int q = qb * kBN + tid;
-        if (q < p.nq) p.cnt[(int64_t)q * p.nsplit + split] = sCnt[tid];
+        if (q < nqv && !(PASS == kPassRetry && p.qcnt)) p.cnt[(int64_t)q * p.nsplit + split] = sCnt[tid];
     }
 }
 
@@ -1205,6 +1395,10 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
     const int quarter = lane >> 4;
     const int ldqB = (p.dpad + PAD) * ES;     // LDS query row stride, bytes
     const int rowP = p.dpad * ES / 16;        // 16-byte pieces per query row
+    // a retry whose work list the device built: nothing to do when it is empty
+    const int nqv = (PASS == kPassRetry && p.nq_dev) ? *p.nq_dev : p.nq;
+    if (nqv <= 0) return;
+    constexpr bool kPoolable = PASS == kPassRetry;
 
     for (int i = tid; i < 16 * NQB * rowP; i += 256) {
         const int row = i / rowP;
@@ -1219,7 +1413,7 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
 #pragma unroll
     for (int bq = 0; bq < NQB; ++bq) {
         const int q = bq * 16 + r16;
-        qv[bq] = q < p.nq;
+        qv[bq] = q < nqv;
         tk[bq] = qv[bq] ? p.tau_key[q] : 0.0f;
         ti[bq] = qv[bq] ? p.tau_id[q] : -1;
         qn[bq] = (METRIC == 0 && qv[bq]) ? p.qnorm[q] : 0.0f;
@@ -1381,7 +1575,11 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
                     }
                     const bool pass = row < p.nrows && qv[bq] &&
                                       (key < tk[bq] || (key == tk[bq] && id <= ti[bq]));
-                    if (pass) {
+                    if (pass && kPoolable && p.qcnt) {   // pooled region of the query
+                        const int ql = bq * 16 + r16;
+                        const int gs = atomicAdd(&p.qcnt[ql * kPoolCntStride], 1);
+                        if (gs < p.qcap[ql]) p.cand[p.qoff[ql] + gs] = make_uint2(__float_as_uint(key), (unsigned)id);
+                    } else if (pass) {
                         const int ql = bq * 16 + r16;
                         const int slot = atomicAdd(&sCnt[ql], 1);
                         if (slot < p.cap)
@@ -1397,7 +1595,7 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
     if (b < nblk) block(b, std::false_type{});
 
     __syncthreads();
-    if (tid < 16 * NQB && tid < p.nq) p.cnt[(int64_t)tid * p.nsplit + split] = sCnt[tid];
+    if (tid < 16 * NQB && tid < nqv && !(kPoolable && p.qcnt)) p.cnt[(int64_t)tid * p.nsplit + split] = sCnt[tid];
 }
 
 // ---------------------------------------------------------------------------
@@ -1417,16 +1615,22 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
     __shared__ unsigned sHist[256];
     __shared__ unsigned sSel[3];
     __shared__ int sWave[4];
+    __shared__ int sSeen[4];
     __shared__ uint64_t sT;
     __shared__ int sN;
     __shared__ unsigned sRange[2][4];
 
     const int q = blockIdx.x;
+    if (p.nq_dev && q >= *p.nq_dev) return;   // a device-built work list shorter than the grid
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int ns = p.nsplit;
     const int64_t qbase = (int64_t)q * ns;
+    // region capacity and start: per (query, split) of p.cap entries, or one
+    // pooled region per query (nsplit == 1)
+    const int capq = p.qcap ? p.qcap[q] : p.cap;
+    auto regBase = [&](int sidx) -> int64_t { return p.qoff ? p.qoff[q] : (qbase + sidx) * p.cap; };
 
     // exclusive prefix of the stored (clamped) counts: sOff[s] .. sOff[s+1].
     // Thread t owns the contiguous splits [t per, (t + 1) per), so any split
@@ -1434,14 +1638,19 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
     const int per = (ns + 255) / 256;
     const int s0 = tid * per;
     int local = 0;
+    int seen = 0;   // unclamped
     bool ovfLocal = false;
     for (int i = 0; i < per; ++i) {
         const int sidx = s0 + i;
         if (sidx < ns) {
-            const int n = p.cnt[qbase + sidx];
-            ovfLocal |= n > p.cap;
-            local += n < p.cap ? n : p.cap;
+            const int n = p.cnt[p.qoff ? (int64_t)q * kPoolCntStride : qbase + sidx];
+            ovfLocal |= n > capq;
+            local += n < capq ? n : capq;
+            seen += n;
         }
+    }
+    if (p.total) {
+        for (int off = 32; off > 0; off >>= 1) seen += __shfl_xor(seen, off, 64);
     }
     int x = local;
     for (int off = 1; off < 64; off <<= 1) {
@@ -1449,14 +1658,15 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
         if (lane >= off) x += t;
     }
     if (lane == 63) sWave[wave] = x;
+    if (lane == 0) sSeen[wave] = seen;
     __syncthreads();
     int run = x - local;
     for (int w = 0; w < wave; ++w) run += sWave[w];
     for (int i = 0; i < per; ++i) {
         const int sidx = s0 + i;
         if (sidx < ns) {
-            const int n = p.cnt[qbase + sidx];
-            run += n < p.cap ? n : p.cap;
+            const int n = p.cnt[p.qoff ? (int64_t)q * kPoolCntStride : qbase + sidx];
+            run += n < capq ? n : capq;
             sOff[sidx + 1] = run;
         }
     }
@@ -1472,7 +1682,7 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
             const int mid = (lo + hi) >> 1;
             if (sOff[mid] <= e) lo = mid; else hi = mid;
         }
-        return composite(p.cand[(qbase + lo) * p.cap + (e - sOff[lo])]);
+        return composite(p.cand[regBase(lo) + (e - sOff[lo])]);
     };
     if (inLds) {
         if (ns >= 256) {
@@ -1490,7 +1700,7 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
                         const int e = e0 + u;
                         if (e < E1) {
                             while (sOff[cur + 1] <= e) ++cur;
-                            v[u] = composite(p.cand[(qbase + cur) * p.cap + (e - sOff[cur])]);
+                            v[u] = composite(p.cand[regBase(cur) + (e - sOff[cur])]);
                         }
                     }
 #pragma unroll
@@ -1758,7 +1968,10 @@ __global__ void __launch_bounds__(256) select_kernel(SelectParams p) {
                 p.tau_k_id[orow] = -1;
             }
         }
-        if (p.status) p.status[orow] = (ovf ? 1 : 0) | (c < k ? 2 : 0);
+        const int st = (ovf ? 1 : 0) | (c < k ? 2 : 0);
+        if (p.status) p.status[orow] = st;
+        if (p.fail_count && st) atomicAdd(p.fail_count, 1);
+        if (p.total) p.total[orow] = sSeen[0] + sSeen[1] + sSeen[2] + sSeen[3];
     }
 }
 
@@ -1803,6 +2016,25 @@ void launch_pack_rows(const float* src, int64_t n, int dim, float* dst, int64_t 
     pack_rows_kernel<<<grid_for(n_pad * dpad, 256), 256, 0, s>>>(src, n, dim, dst, n_pad, dpad);
     prof_end(tok, s);
     check_launch("pack_rows");
+}
+
+void launch_prep_queries(const float* src, int64_t n, int dim, int64_t n_pad, int dpad, int storage, bool cosine,
+                         void* out, float* qn, float* tau_key, int* tau_id, hipStream_t s) {
+    if (n_pad <= 0) return;
+    if (dpad % 8 != 0) throw std::runtime_error("prep_queries: dpad must be a multiple of 8");
+    void* tok;
+    prof_begin(kFamPrep, s, &tok);
+    const int g = (int)((n_pad + 63) / 64);
+    if (storage == kF32)
+        prep_queries_kernel<kF32><<<g, 64, 0, s>>>(src, n, dim, n_pad, dpad, cosine ? 1 : 0, out, qn, tau_key, tau_id);
+    else if (storage == kF16)
+        prep_queries_kernel<kF16><<<g, 64, 0, s>>>(src, n, dim, n_pad, dpad, cosine ? 1 : 0, out, qn, tau_key, tau_id);
+    else if (storage == kBF16)
+        prep_queries_kernel<kBF16><<<g, 64, 0, s>>>(src, n, dim, n_pad, dpad, cosine ? 1 : 0, out, qn, tau_key, tau_id);
+    else
+        throw std::runtime_error("prep_queries: unknown storage type");
+    prof_end(tok, s);
+    check_launch("prep_queries");
 }
 
 void launch_normalize_rows(float* v, int64_t n, int dpad, hipStream_t s) {
@@ -1927,6 +2159,32 @@ void launch_gather_tau(const TauSources& src, const int* idx, const int* sel, in
     gather_tau_kernel<<<(n + 255) / 256, 256, 0, s>>>(src, idx, sel, n, ko, io);
     prof_end(tok, s);
     check_launch("gather_tau");
+}
+
+void launch_retry_plan(const int* status, int mb, int first, const float* tau_k_key, const int* tau_k_id,
+                       const int* total, const RetryLadder& ladder, int64_t pool_entries, int rmax, int all_rows,
+                       const RetryLists& rl, hipStream_t s) {
+    if (mb <= 0 || rmax <= 0) throw std::runtime_error("retry_plan: empty batch or window");
+    void* tok;
+    prof_begin(kFamPrep, s, &tok);
+    retry_plan_kernel<<<1, 1024, 0, s>>>(status, mb, first, tau_k_key, tau_k_id, total, ladder, pool_entries, rmax,
+                                         all_rows, rl);
+    prof_end(tok, s);
+    check_launch("retry_plan");
+}
+
+void launch_gather_rows_dev(const void* src, const float* qn, const int* idx, const int* n, int row_bytes,
+                            void* dst, float* dst_qn, int rows_pad, hipStream_t s) {
+    if (rows_pad <= 0) return;
+    if (row_bytes % 16 != 0) throw std::runtime_error("gather_rows_dev: row bytes must be a multiple of 16");
+    const int rowP = row_bytes / 16;
+    const int64_t work = std::max<int64_t>((int64_t)rows_pad * rowP, rows_pad);
+    void* tok;
+    prof_begin(kFamPrep, s, &tok);
+    gather_rows_dev_kernel<<<grid_for(work, 256), 256, 0, s>>>((const fx4*)src, qn, idx, n, rowP, (fx4*)dst, dst_qn,
+                                                             rows_pad);
+    prof_end(tok, s);
+    check_launch("gather_rows_dev");
 }
 
 void launch_fill_tau_none(float* key, int* id, int n, hipStream_t s) {

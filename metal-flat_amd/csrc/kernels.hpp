@@ -55,6 +55,7 @@ constexpr size_t kSmallMaxLds = 64 * 1024;     // ... whose query tile fits this
 constexpr size_t kResidentMaxLds = 68 * 1024;  // scan_resident: largest resident query tile
 constexpr size_t kResidentMaxLdsNarrow = 144 * 1024;  // ... of a 32-query IVF tile (one workgroup a CU)
 constexpr int kRing = 192;                     // scan_resident: staged survivors per wave
+constexpr int kPoolCntStride = 32;             // ints between pooled-region counters (128 bytes)
 
 // Element type of the stored database and of the queries (the ABI's
 // mflat_storage_t values).
@@ -116,6 +117,16 @@ struct ScanParams {
     int ivf_nreg;              // candidate regions per query: query * nreg + rank (1, nprobe or nprobe + 1)
     int ivf_spill;             // 1: region nprobe of each query takes what overflows the others (nreg = nprobe + 1)
     int ivf_row_cap;           // > 0: scan only the first ivf_row_cap rows of each cell
+    // Retry passes (kPassRetry) whose work list the device built:
+    const int* nq_dev;         // nullable: valid queries = *nq_dev (<= nq); query blocks beyond exit
+    // Pooled regions (kPassRetry): one region per query, cand[qoff[q] ..
+    // qoff[q] + qcap[q]), slots taken with global atomics on the query's
+    // counter qcnt[q * kPoolCntStride] (one per 128-byte line: counters of
+    // different queries never share a line), which then holds the unclamped
+    // count; cnt is not written.
+    int* qcnt;
+    const int64_t* qoff;
+    const int* qcap;
 };
 
 struct SelectParams {
@@ -142,10 +153,51 @@ struct SelectParams {
     int expect;              // stored candidates per query that (nearly) every query stays under (0:
                              // unknown): picks the smallest LDS buffer variant that holds it (more
                              // blocks per CU); a query above its buffer reads from global memory
+    const int* nq_dev;       // nullable: blocks at or beyond *nq_dev exit (device-built work lists)
+    const int64_t* qoff;     // nullable (nsplit == 1): pooled regions, query i at cand[qoff[i]],
+    const int* qcap;         //   capacity qcap[i], count cnt[i * kPoolCntStride]
+    int* total;              // nullable: unclamped candidates seen by each query (sum of its counts)
+    int* fail_count;         // nullable: incremented once per query whose status is nonzero
+};
+
+// Device-built retry work lists (flat search). After a full pass's select, a
+// query whose status is nonzero is retried; retry_plan decides each one's
+// bound and pooled region (one per query, cand[qoff .. qoff + qcap)):
+//   overflow (bit 0): the k-th best it stored, capacity = the unclamped count
+//       it saw under the looser bound (total): the rerun cannot overflow, so
+//       it is final;
+//   too few (bit 1): the next looser bound of its ladder (the sample's j2-th,
+//       then its guaranteed k-th, then none), capacity estimated for it.
+// Queries are taken in ascending order while they fit rmax and the pool; the
+// rest wait for the next round. All counts stay on the device.
+struct RetryLists {
+    int* fail;         // [mb] scratch: failing queries in ascending order
+    unsigned char* lvl;   // [mb] ladder step each query has taken
+    int* idx;          // [rmax] queries scheduled this round (original row)
+    float* tk;         // [rmax] their bounds
+    int* ti;
+    int64_t* qoff;     // [rmax] pooled regions
+    int* qcap;
+    int* qcnt;         // [rmax * kPoolCntStride] slot counters, 128 bytes apart (cleared by the plan)
+    int* counters;     // [4]: failing queries, scheduled, failed again (the select adds), spare
+};
+struct RetryLadder {   // per-query bounds of the "too few" ladder (nullable entries are skipped)
+    const float* j2_key;
+    const int* j2_id;
+    const float* g_key;
+    const int* g_id;
+    int cap_j2, cap_g;   // pooled capacities estimated for those bounds
 };
 
 // Launchers (kernels.hip). All are asynchronous on `s` and bracket the launch
 // with the process-wide kernel timer when it is enabled.
+// A search batch's queries in one launch: fp32 rows (dim values, n of them)
+// -> out, n_pad rows of dpad elements of the storage type (zero padded;
+// Cosine rows L2-normalised first, the reference's rule), qn[n_pad] = ||row||^2
+// of the stored values (double sum), and, when tau_key is given, "no bound"
+// (+inf, -1) for the n live rows.
+void launch_prep_queries(const float* src, int64_t n, int dim, int64_t n_pad, int dpad, int storage, bool cosine,
+                         void* out, float* qn, float* tau_key, int* tau_id, hipStream_t s);
 // row-major fp32 (queries)
 void launch_pack_rows(const float* src, int64_t n, int dim, float* dst, int64_t n_pad, int dpad,
                       hipStream_t s);
@@ -200,6 +252,14 @@ void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, 
 void launch_scan_ivf(const ScanParams& p, int metric, int pass, int storage, int tileQueries, int grid,
                      hipStream_t s);
 void launch_select(const SelectParams& p, hipStream_t s);
+// One retry round's plan (one block): see RetryLists. first = 1 on the first
+// round of a batch (every query's ladder step starts at 0).
+void launch_retry_plan(const int* status, int mb, int first, const float* tau_k_key, const int* tau_k_id,
+                       const int* total, const RetryLadder& ladder, int64_t pool_entries, int rmax, int all_rows,
+                       const RetryLists& rl, hipStream_t s);
+// rows idx[i] (i < *n) of src (row_bytes each) -> dst rows i, rows *n .. rows_pad zeroed; norms likewise
+void launch_gather_rows_dev(const void* src, const float* qn, const int* idx, const int* n, int row_bytes,
+                            void* dst, float* dst_qn, int rows_pad, hipStream_t s);
 void launch_argmin_finalize(const unsigned long long* best, int nq, int metric, int32_t* ids, float* vals,
                             hipStream_t s);
 void launch_fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hipStream_t s);
