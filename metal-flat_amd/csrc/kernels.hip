@@ -1379,13 +1379,19 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
 // (the next block's step t is fetched as soon as step t of the current block is
 // consumed), which keeps G pieces per lane in flight. G == 0: any dpad, one
 // step of prefetch.
-template <int S, int METRIC, int NQB, int PASS, int G>
+template <int S, int METRIC, int NQB, int PASS, int G, int KT>
 __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
     constexpr int ES = S == kF32 ? 4 : 2;
     constexpr int U = S == kF32 ? 2 : 1;      // 16-byte pieces per row half per chunk
     constexpr int PAD = 16 / ES;              // LDS row padding (elements)
+    static_assert(KT == 0 || (NQB == 1 && PASS == kPassFull), "top-k mode: one block of 16 queries, full pass");
     extern __shared__ __attribute__((aligned(16))) float sQs[];   // [16*NQB][dpad + PAD] elements
     __shared__ int sCnt[16 * NQB];
+    // Top-k mode (KT > 0): each wave's exact top-k (k = p.cap <= KT) of the
+    // rows it scanned, per query, as ascending composites (ordered key << 32
+    // | id); the list's k-th is the wave's bound for that query.
+    __shared__ uint64_t sList[KT > 0 ? 4 * 16 * KT : 1];
+    __shared__ int sLen[KT > 0 ? 4 * 16 : 1];
 
     const int split = blockIdx.x;
     const int tid = threadIdx.x;
@@ -1406,6 +1412,7 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
         *(fx4*)((char*)sQs + row * ldqB + c * 16) = *((const fx4*)p.Q + (int64_t)row * rowP + c);
     }
     if (tid < 16 * NQB) sCnt[tid] = 0;
+    if (KT > 0 && tid < 4 * 16) sLen[tid] = 0;
 
     float tk[NQB], qn[NQB], ft[NQB];
     int ti[NQB];
@@ -1414,8 +1421,9 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
     for (int bq = 0; bq < NQB; ++bq) {
         const int q = bq * 16 + r16;
         qv[bq] = q < nqv;
-        tk[bq] = qv[bq] ? p.tau_key[q] : 0.0f;
-        ti[bq] = qv[bq] ? p.tau_id[q] : -1;
+        // top-k mode starts from "no bound" (+inf, -1) in every wave
+        tk[bq] = qv[bq] ? (KT > 0 ? INFINITY : p.tau_key[q]) : 0.0f;
+        ti[bq] = qv[bq] ? (KT > 0 ? -1 : p.tau_id[q]) : -1;
         qn[bq] = (METRIC == 0 && qv[bq]) ? p.qnorm[q] : 0.0f;
         if (METRIC == 0) {
             const float m = 0x1p-20f * (tk[bq] + 2.0f * qn[bq] + 2.0f * p.xnorm_max);
@@ -1468,6 +1476,79 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
     // the prefetch of every other block is unconditional: with a branch
     // around it the compiler's wait for the row norms has to fit both paths
     // and waits for the prefetch as well.
+    // Top-k mode: the block's candidates of this lane (rows r0 + i of both
+    // row halves, query r16) go into the wave's list of query r16. The four
+    // lane quarters holding the same query insert one after another, so each
+    // list has one writer at a time; an insertion re-checks against the
+    // list's current k-th. Afterwards every lane re-reads its query's bound.
+    const int kk = p.cap;
+    auto topk_block = [&](const fx4 (&acc)[2][NQB], const fx4 (&xnh)[2], const int b) {
+        uint64_t cc[2][4];
+        bool has = false;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int64_t r0 = rowBeg + (int64_t)b * 32 + hh * 16 + quarter * 4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float dot = acc[hh][0][i];
+                const bool f = METRIC == 0 ? fmaf(-2.0f, dot, xnh[hh][i]) <= ft[0] : dot >= ft[0];
+                cc[hh][i] = ~0ull;
+                if (f) {
+                    const int64_t row = r0 + i;
+                    float key;
+                    if (METRIC == 0) {
+                        const float tt = fmaf(-2.0f, dot, qn[0] + xnh[hh][i]);
+                        key = (tt < 0.0f ? 0.0f : tt) + 0.0f;
+                    } else {
+                        key = -dot + 0.0f;
+                    }
+                    const int id = (int)(row * p.id_stride);
+                    // +inf and NaN keys are never results ("no bound" rejects them)
+                    if (row < p.nrows && qv[0] && key < INFINITY &&
+                        (key < tk[0] || (key == tk[0] && id < ti[0]))) {
+                        cc[hh][i] = ((uint64_t)key_to_ord(__float_as_uint(key)) << 32) | (uint32_t)id;
+                        has = true;
+                    }
+                }
+            }
+        }
+        if (!__any(has)) return;
+        uint64_t* L = sList + (wave * 16 + r16) * KT;
+        int* len = sLen + wave * 16 + r16;
+        for (int qt = 0; qt < 4; ++qt) {
+            if (quarter == qt && has) {
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint64_t c = cc[hh][i];
+                        if (c == ~0ull) continue;
+                        const int n = *len;
+                        if (n == kk && c >= L[kk - 1]) continue;
+                        int j = n == kk ? kk - 1 : n;
+                        while (j > 0 && L[j - 1] > c) {
+                            L[j] = L[j - 1];
+                            --j;
+                        }
+                        L[j] = c;
+                        if (n < kk) *len = n + 1;
+                    }
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+        if (*len == kk && qv[0]) {
+            const uint64_t x = L[kk - 1];
+            tk[0] = ord_to_key((uint32_t)(x >> 32));
+            ti[0] = (int)(uint32_t)(x & 0xFFFFFFFFu);
+            if (METRIC == 0) {
+                const float m = 0x1p-20f * (tk[0] + 2.0f * qn[0] + 2.0f * p.xnorm_max);
+                ft[0] = (tk[0] - qn[0]) + m;
+            } else {
+                ft[0] = -tk[0];
+            }
+        }
+    };
+
     auto block = [&](const int b, auto nextTag) {
         constexpr bool NEXT = decltype(nextTag)::value;
         // The block's row norms are loaded BEFORE the next block's prefetch:
@@ -1548,6 +1629,10 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
             }
         }
 
+        if constexpr (KT > 0) {
+            topk_block(acc, xnh, b);
+            return;
+        }
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const int64_t r0 = rowBeg + (int64_t)b * 32 + hh * 16 + quarter * 4;
@@ -1595,6 +1680,37 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
     if (b < nblk) block(b, std::false_type{});
 
     __syncthreads();
+    if constexpr (KT > 0) {
+        // the split's top-k of query tid: a merge of its four waves' lists
+        if (tid < 16 && tid < nqv) {
+            int h[4] = {0, 0, 0, 0};
+            int n[4];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) n[w] = sLen[w * 16 + tid];
+            uint2* out = p.cand + ((int64_t)tid * p.nsplit + split) * p.cap;
+            int o = 0;
+            for (; o < kk; ++o) {
+                uint64_t best = ~0ull;
+                int bw = -1;
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    if (h[w] < n[w]) {
+                        const uint64_t x = sList[(w * 16 + tid) * KT + h[w]];
+                        if (x < best) {
+                            best = x;
+                            bw = w;
+                        }
+                    }
+                }
+                if (bw < 0) break;
+                ++h[bw];
+                out[o] = make_uint2(__float_as_uint(ord_to_key((uint32_t)(best >> 32))),
+                                    (unsigned)(best & 0xFFFFFFFFu));
+            }
+            p.cnt[(int64_t)tid * p.nsplit + split] = o;
+        }
+        return;
+    }
     if (tid < 16 * NQB && tid < nqv && !(kPoolable && p.qcnt)) p.cnt[(int64_t)tid * p.nsplit + split] = sCnt[tid];
 }
 
@@ -2225,9 +2341,22 @@ void launch_max_norm(const float* xn, int64_t n, unsigned* out, hipStream_t s) {
 
 template <int S, int M, int NQB, int G>
 static void launch_small_g(const ScanParams& p, int pass, int g, size_t lds, hipStream_t s) {
-    if (pass == kPassSample) scan_small_kernel<S, M, NQB, kPassSample, G><<<g, 256, lds, s>>>(p);
-    else if (pass == kPassRetry) scan_small_kernel<S, M, NQB, kPassRetry, G><<<g, 256, lds, s>>>(p);
-    else scan_small_kernel<S, M, NQB, kPassFull, G><<<g, 256, lds, s>>>(p);
+    if (pass == kPassSample) scan_small_kernel<S, M, NQB, kPassSample, G, 0><<<g, 256, lds, s>>>(p);
+    else if (pass == kPassRetry) scan_small_kernel<S, M, NQB, kPassRetry, G, 0><<<g, 256, lds, s>>>(p);
+    else scan_small_kernel<S, M, NQB, kPassFull, G, 0><<<g, 256, lds, s>>>(p);
+}
+template <int S, int M, int G>
+static const void* topk_fn() {
+    return (const void*)scan_small_kernel<S, M, 1, kPassFull, G, kStreamTopK>;
+}
+template <int S, int M>
+static const void* topk_fn_d(int dpad) {
+    return dpad == 96 ? topk_fn<S, M, 3>() : dpad == 128 ? topk_fn<S, M, 4>() : topk_fn<S, M, 0>();
+}
+static const void* topk_kernel(int dpad, int storage, int metric) {
+    if (storage == kF32) return metric == 0 ? topk_fn_d<kF32, 0>(dpad) : topk_fn_d<kF32, 1>(dpad);
+    if (storage == kF16) return metric == 0 ? topk_fn_d<kF16, 0>(dpad) : topk_fn_d<kF16, 1>(dpad);
+    return metric == 0 ? topk_fn_d<kBF16, 0>(dpad) : topk_fn_d<kBF16, 1>(dpad);
 }
 template <int S, int M, int NQB>
 static void launch_small(const ScanParams& p, int pass, int g, size_t lds, hipStream_t s) {
@@ -2352,6 +2481,35 @@ static size_t small_lds_bytes(int nq, int dpad, int storage) {
 
 bool small_scan_fits(int nq, int dpad, int storage) {
     return nq >= 1 && nq <= kSmallMaxQ && small_lds_bytes(nq, dpad, storage) <= kSmallMaxLds;
+}
+
+int topk_concurrency(int dpad, int storage, int metric) {
+    const void* f = topk_kernel(dpad, storage, metric);
+    const size_t lds = small_lds_bytes(1, dpad, storage);
+    int dev = 0, cus = 0, per = 0;
+    if (!f || hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, f, 256, lds) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return per > 0 && cus > 0 ? per * cus : 0;
+}
+
+void launch_scan_topk(const ScanParams& p, int metric, int storage, hipStream_t s) {
+    if (p.nsplit <= 0) return;
+    if (p.nq < 1 || p.nq > kStreamMaxQ || p.cap < 1 || p.cap > kStreamTopK || p.rows_per_split % kBM != 0 ||
+        p.dpad % kBK != 0 || !small_scan_fits(p.nq, p.dpad, storage))
+        throw std::runtime_error("scan_topk: bad parameters");
+    const void* f = topk_kernel(p.dpad, storage, metric);
+    const size_t lds = small_lds_bytes(1, p.dpad, storage);
+    void* tok;
+    prof_begin(kFamScan, s, &tok);
+    void* args[] = {(void*)&p};
+    const hipError_t e = hipLaunchKernel(f, dim3(p.nsplit), dim3(256), args, lds, s);
+    prof_end(tok, s);
+    if (e != hipSuccess) throw std::runtime_error(std::string("scan_topk launch: ") + hipGetErrorString(e));
+    check_launch("scan_topk");
 }
 
 // The function launch_scan_filter starts for a batch too large for scan_small,

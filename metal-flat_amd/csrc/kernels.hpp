@@ -56,6 +56,8 @@ constexpr size_t kResidentMaxLds = 68 * 1024;  // scan_resident: largest residen
 constexpr size_t kResidentMaxLdsNarrow = 144 * 1024;  // ... of a 32-query IVF tile (one workgroup a CU)
 constexpr int kRing = 192;                     // scan_resident: staged survivors per wave
 constexpr int kPoolCntStride = 32;             // ints between pooled-region counters (128 bytes)
+constexpr int kStreamTopK = 32;                // streaming top-k scan: k up to this ...
+constexpr int kStreamMaxQ = 16;                // ... for batches up to this many queries
 
 // Element type of the stored database and of the queries (the ABI's
 // mflat_storage_t values).
@@ -252,6 +254,14 @@ void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, 
 void launch_scan_ivf(const ScanParams& p, int metric, int pass, int storage, int tileQueries, int grid,
                      hipStream_t s);
 void launch_select(const SelectParams& p, hipStream_t s);
+// Streaming top-k scan (batches of <= kStreamMaxQ queries, k = p.cap <=
+// kStreamTopK): one workgroup per split keeps each wave's exact top-k of the
+// rows it reads and writes the split's top-k of every query (cand regions of
+// p.cap entries, cnt = entries written); a select over the splits finishes the
+// search. No bound, sample or retry: exact by construction. The split count
+// wants to be the number of workgroups resident at once (topk_concurrency).
+void launch_scan_topk(const ScanParams& p, int metric, int storage, hipStream_t s);
+int topk_concurrency(int dpad, int storage, int metric);
 // One retry round's plan (one block): see RetryLists. first = 1 on the first
 // round of a batch (every query's ladder step starts at 0).
 void launch_retry_plan(const int* status, int mb, int first, const float* tau_k_key, const int* tau_k_id,

@@ -221,18 +221,19 @@ def test_uniform_small_batch(gpu_ok):
 
 
 def test_small_batch_second_sample_level(gpu_ok):
-    """Batches of 16 and 64 queries against 10M rows (C4's row count at d=16):
-    the plan adds the second sample level here (a 32,768-row sample scanned
-    under the 4,096-row sample's bound, its 3rd best bounding the full pass);
-    float data within the fp32 tolerance, integer data (exact ties at the
-    bound) bit-exact."""
+    """Batches of 17-64 queries against 10M rows (C4's row count at d=16): the
+    plan adds the second sample level here (a 32,768-row sample scanned under
+    the 4,096-row sample's bound, its 3rd best bounding the full pass); float
+    data within the fp32 tolerance, integer data (exact ties at the bound)
+    bit-exact. (Batches of <= 16 queries at k <= 32 take the streaming top-k
+    scan instead; k = 40 keeps 16 queries on this path.)"""
     x, q = datagen.uniform_pm1(nb=10_000_000, nq=64, d=16, seed=3)
-    for nq in (16, 64):
-        gi, gd, _ = run(x, q[:nq], 10, L2)
-        oi, od = orc(x, q[:nq], 10, L2)
+    for nq, k in ((16, 40), (17, 10), (64, 10)):
+        gi, gd, _ = run(x, q[:nq], k, L2)
+        oi, od = orc(x, q[:nq], k, L2)
         parity.tolerant(gi, gd, oi, od, x, q[:nq], 0)
     del x
-    x, q = datagen.sift_like(nb=10_000_000, nq=16, d=16, seed=5)
+    x, q = datagen.sift_like(nb=10_000_000, nq=20, d=16, seed=5)
     gi, gd, _ = run(x, q, 10, L2)
     oi, od = orc(x, q, 10, L2)
     parity.exact(gi, gd, oi, od)

@@ -56,10 +56,13 @@ def check(x, q, k, env, monkeypatch):
 
 
 def test_distance_sorted_10m_small_batches(gpu_ok, monkeypatch):
-    """10M x 16, rank following row order; batches of 1 and 16 queries, k = 10."""
+    """10M x 16, rank following row order; batches of 1 and 16 queries, k = 10
+    and 40 (a single query at k <= 32 takes the streaming top-k scan; the rest
+    the sample, full pass and retries of the streaming kernel family)."""
     x = sorted_db(10_000_000, 16, seed=31, block=2500)
     for nq in (1, 16):
-        check(x, queries(nq, 16, seed=32 + nq), 10, {}, monkeypatch)
+        for k in (10, 40):
+            check(x, queries(nq, 16, seed=32 + nq), k, {}, monkeypatch)
 
 
 def test_distance_sorted_large_batch(gpu_ok, monkeypatch):
