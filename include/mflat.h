@@ -251,6 +251,25 @@ MFLAT_API mflat_status_t mflat_flat_search_device(mflat_flat_index_t*, const flo
 MFLAT_API mflat_status_t mflat_flat_add_device(mflat_flat_index_t*, const float* d_vectors,
         int n, void* stream);
 
+/* ---------------- Additive: allocation-free search ----------------------- */
+/* No counterpart in the reference. For callers that cannot allocate device
+   memory: code under HIP graph capture, tight serving loops, harnesses that
+   forbid hipMalloc. As mflat_flat_search_device, but the call allocates
+   nothing (no hipMalloc / hipFree, no allocating library routine): its
+   workspace is a statically sized device array of 4 MiB that each GPU the
+   library runs on holds until the process ends. The database must already be
+   resident (mflat_flat_add / _add_device allocate as usual). Limits: m <= 16
+   queries, k <= 32, dim <= 992 (fp32 storage) or 2016 (fp16 / bf16); beyond
+   them MFLAT_ERR_BAD_ARG (no clamping).
+   Stream-ordered: returns once the work is enqueued on `stream` (NULL = the
+   index's own stream); results are complete when that stream reaches this
+   point. Every call on one GPU shares that GPU's array: calls that can
+   overlap on one GPU (different streams, or different threads without
+   ordering) race and must be serialised by the caller. Results equal
+   mflat_flat_search_device's (exact top-k, ties to the lower id). */
+MFLAT_API mflat_status_t mflat_flat_search_device_noalloc(mflat_flat_index_t*, const float* d_queries,
+        int m, int k, int32_t* d_out_ids, float* d_out_distances, int* out_k_used, void* stream);
+
 /* ---------------- Additive: IVF extensions ------------------------------- */
 /* No C counterpart in the reference. mflat_ivf_create_ex: as mflat_ivf_create
    with the fine scan's storage type (the rows and the queries of the fine scan

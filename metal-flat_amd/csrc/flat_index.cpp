@@ -37,6 +37,7 @@
 
 #include "kernels.hpp"
 #include "log.hpp"
+#include "noalloc.hpp"
 
 namespace mflat_amd {
 namespace {
@@ -281,6 +282,22 @@ struct FlatIndex::Impl {
         if (device >= 0) HIPC(hipSetDevice(device));
     }
 
+    // The streaming top-k scan's plan: one workgroup per split, as many
+    // splits as run at once; each streams its rows once and hands k candidates
+    // per query to the select, whose LDS buffer holds them all.
+    void setStreamPlan(Plan& pl, int k) const {
+        pl.stream = true;
+        const int64_t ntiles = std::max<int64_t>(1, (nb + kBM - 1) / kBM);
+        int64_t want = streamSplits > 0 ? streamSplits : topkConcurrency();
+        if (want <= 0) want = 1024;
+        want = std::min<int64_t>({want, std::max<int64_t>(256, kSelLdsLarge / k), ntiles, kSelLargeMaxSplit});
+        const int64_t tps = (ntiles + want - 1) / want;
+        pl.nsplit1 = (int)((ntiles + tps - 1) / tps);
+        pl.rps1 = tps * kBM;
+        pl.cap1 = k;
+        pl.perQuery = (size_t)pl.nsplit1 * k;
+    }
+
     // Small batches with a small k: the streaming top-k scan.
     bool streamPath(int64_t mb, int k) const {
         return mb <= std::min(streamMaxQ, kStreamMaxQ) && k <= kStreamTopK && small_scan_fits((int)mb, dpad, storage);
@@ -303,19 +320,7 @@ struct FlatIndex::Impl {
             return pl;
         }
         if (streamPath(mb, k)) {
-            // one workgroup per split, as many splits as run at once: each
-            // streams its rows once and hands k candidates per query to the
-            // select, whose LDS buffer holds them all
-            pl.stream = true;
-            const int64_t ntiles = std::max<int64_t>(1, (nb + kBM - 1) / kBM);
-            int64_t want = streamSplits > 0 ? streamSplits : topkConcurrency();
-            if (want <= 0) want = 1024;
-            want = std::min<int64_t>({want, std::max<int64_t>(256, kSelLdsLarge / k), ntiles, kSelLargeMaxSplit});
-            const int64_t tps = (ntiles + want - 1) / want;
-            pl.nsplit1 = (int)((ntiles + tps - 1) / tps);
-            pl.rps1 = tps * kBM;
-            pl.cap1 = k;
-            pl.perQuery = (size_t)pl.nsplit1 * k;
+            setStreamPlan(pl, k);
             return pl;
         }
         int64_t r = (int64_t)std::ceil(std::sqrt(16.0 * (double)nb));
@@ -794,6 +799,67 @@ struct FlatIndex::Impl {
         }
     }
 
+    // The allocation-free search: the streaming top-k scan with its workspace
+    // (queries, norms, per-split counts and candidates) carved out of the
+    // device's scratch array. Stream-ordered: returns once the work is
+    // enqueued on s. Nothing here allocates: no DevBuf, no timer events.
+    int searchNoAlloc(const float* dq, int m, int k, int32_t* ids, float* vals, hipStream_t s) {
+        if (!ready) throw NotReady("no usable HIP device: flat search needs a gfx950 GPU");
+        if (m > kNoAllocMaxQ)
+            throw BadArg("allocation-free search: at most " + std::to_string(kNoAllocMaxQ) + " queries per call (got " +
+                         std::to_string(m) + ")");
+        if (k > kStreamTopK)
+            throw BadArg("allocation-free search: k at most " + std::to_string(kStreamTopK) + " (got " +
+                         std::to_string(k) + ")");
+        if (dim > kNoAllocMaxDim || !small_scan_fits(kNoAllocMaxQ, dpad, storage))
+            throw BadArg("allocation-free search: dimension " + std::to_string(dim) +
+                         " too large (at most 992 for fp32 storage, 2016 for fp16 / bf16)");
+        if (m <= 0) return 0;
+        if (k < 1) k = 1;
+        setDevice();
+        prof_suppress(true);
+        struct Unsuppress {
+            ~Unsuppress() { prof_suppress(false); }
+        } unsuppress;
+        if (nb == 0) {
+            launch_fill_empty(ids, vals, (int64_t)m * k, emptyValue(), s);
+            return k;
+        }
+        char* base = static_cast<char*>(noalloc_scratch(device));
+        Plan pl;
+        setStreamPlan(pl, k);
+        auto carve = [&](size_t& at, size_t bytes) {
+            const size_t off = at;
+            at = (at + bytes + 255) / 256 * 256;
+            return base + off;
+        };
+        size_t at = 0;
+        void* qs = carve(at, (size_t)kNoAllocMaxQ * dpad * esize);
+        float* qn = reinterpret_cast<float*>(carve(at, (size_t)kNoAllocMaxQ * sizeof(float)));
+        int* cn = reinterpret_cast<int*>(carve(at, (size_t)m * pl.nsplit1 * sizeof(int)));
+        uint2* cd = reinterpret_cast<uint2*>(carve(at, (size_t)m * pl.nsplit1 * k * sizeof(uint2)));
+        if (at > kNoAllocScratchBytes)
+            throw BadArg("allocation-free search: workspace of " + std::to_string(at) + " bytes exceeds the " +
+                         std::to_string(kNoAllocScratchBytes) + "-byte scratch");
+        launch_prep_queries(dq, m, dim, kNoAllocMaxQ, dpad, storage, metric == Metric::Cosine, qs, qn, nullptr,
+                            nullptr, s);
+        ScanParams p;
+        std::memset(&p, 0, sizeof p);
+        p.X = X.p; p.xnorm = xn.as<float>(); p.xnorm_max = xnMax; p.nrows = nb;
+        p.rows_per_split = pl.rps1; p.nsplit = pl.nsplit1; p.id_stride = 1;
+        p.Q = qs; p.qnorm = qn; p.nq = m; p.nqb = 1; p.dpad = dpad;
+        p.cand = cd; p.cnt = cn; p.cap = k;
+        launch_scan_topk(p, kernMetric(), storage, s);
+        SelectParams sp;
+        std::memset(&sp, 0, sizeof sp);
+        sp.cand = cd; sp.cnt = cn; sp.nsplit = pl.nsplit1; sp.cap = k; sp.nq = m; sp.k = k; sp.j = 1; sp.j2 = 1;
+        sp.metric = kernMetric();
+        sp.out_ids = ids; sp.out_vals = vals; sp.out_stride = k;
+        sp.expect = pl.nsplit1 * k;
+        launch_select(sp, s);
+        return k;
+    }
+
     int searchDev(const float* dq, int m, int k, int32_t* ids, float* vals, hipStream_t s) {
         if (!ready) throw NotReady("no usable HIP device: flat search needs a gfx950 GPU");
         if (m <= 0) return 0;
@@ -938,6 +1004,10 @@ int FlatIndex::search(const float* q, int m, int k, int32_t* ids, float* dists) 
 
 int FlatIndex::searchDevice(const float* q, int m, int k, int32_t* ids, float* dists, hipStream_t s) {
     return d_->searchDev(q, m, k, ids, dists, s ? s : d_->stream);
+}
+
+int FlatIndex::searchDeviceNoAlloc(const float* q, int m, int k, int32_t* ids, float* dists, hipStream_t s) {
+    return d_->searchNoAlloc(q, m, k, ids, dists, s ? s : d_->stream);
 }
 
 }  // namespace mflat_amd

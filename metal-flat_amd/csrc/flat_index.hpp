@@ -57,6 +57,12 @@ public:
     int search(const float* host_queries, int m, int k, int32_t* ids, float* dists);
     int searchDevice(const float* dev_queries, int m, int k, int32_t* dev_ids, float* dev_dists,
                      hipStream_t stream);
+    // As searchDevice, allocating nothing: the workspace is the GPU's static
+    // scratch array (noalloc.hpp). m <= kNoAllocMaxQ, k <= kStreamTopK, and a
+    // dimension whose 16-query tile fits the streaming scan's LDS (BadArg
+    // otherwise). Stream-ordered: returns once the work is enqueued.
+    int searchDeviceNoAlloc(const float* dev_queries, int m, int k, int32_t* dev_ids, float* dev_dists,
+                            hipStream_t stream);
 
 private:
     struct Impl;

@@ -277,5 +277,6 @@ void launch_fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hip
 // Kernel timer (profile.cpp).
 void prof_begin(int fam, hipStream_t s, void** token);
 void prof_end(void* token, hipStream_t s);
+void prof_suppress(bool on);   // on: this thread's launches create no timer events (nests)
 
 }  // namespace mflat_amd

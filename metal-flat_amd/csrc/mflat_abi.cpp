@@ -203,6 +203,24 @@ MFLAT_API mflat_status_t mflat_flat_search_device(mflat_flat_index_t* h, const f
     });
 }
 
+// No counterpart in the reference: the allocation-free variant of
+// mflat_flat_search_device (the engine's searchDeviceNoAlloc).
+MFLAT_API mflat_status_t mflat_flat_search_device_noalloc(mflat_flat_index_t* h, const float* q, int m, int k,
+                                                          int32_t* oi, float* od, int* ok, void* stream) {
+    if (!h || !q) return MFLAT_ERR_NULL_ARG;
+    if (m < 0 || k < 1) return MFLAT_ERR_BAD_ARG;
+    if (m == 0) {
+        if (ok) *ok = 0;
+        return MFLAT_OK;
+    }
+    return guarded([&] {
+        std::lock_guard<std::mutex> lk(h->mu);
+        const int used = h->idx.searchDeviceNoAlloc(q, m, k, oi, od, static_cast<hipStream_t>(stream));
+        if (ok) *ok = used;
+        return MFLAT_OK;
+    });
+}
+
 MFLAT_API mflat_status_t mflat_flat_add_device(mflat_flat_index_t* h, const float* v, int n, void* stream) {
     if (!h || !v) return MFLAT_ERR_NULL_ARG;
     if (n < 0) return MFLAT_ERR_BAD_ARG;

@@ -18,6 +18,7 @@ struct Pending { int fam; hipEvent_t a, b; };
 struct Token { int fam; hipEvent_t a; };
 
 std::atomic<int> gOn{0};
+thread_local int tSuppressed = 0;   // > 0: this thread's launches are not timed
 std::mutex gMu;
 std::vector<Pending> gPending;
 double gMs[kFamCount] = {0};
@@ -40,7 +41,7 @@ void resolveLocked() {
 
 void prof_begin(int fam, hipStream_t s, void** token) {
     *token = nullptr;
-    if (!gOn.load(std::memory_order_relaxed)) return;
+    if (!gOn.load(std::memory_order_relaxed) || tSuppressed) return;
     hipEvent_t a;
     if (hipEventCreate(&a) != hipSuccess) return;
     if (hipEventRecord(a, s) != hipSuccess) { (void)hipEventDestroy(a); return; }
@@ -65,6 +66,9 @@ void prof_end(void* token, hipStream_t s) {
 }
 
 void prof_enable(int on) { gOn.store(on ? 1 : 0, std::memory_order_relaxed); }
+
+// The allocation-free entry point's launches create no timer events.
+void prof_suppress(bool on) { tSuppressed += on ? 1 : -1; }
 
 void prof_reset() {
     std::lock_guard<std::mutex> lk(gMu);

@@ -58,6 +58,8 @@ SIGNATURES = {
     "mflat_flat_search_i64": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, POINTER(c_int)]),
     "mflat_flat_search_device": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p,
                                          POINTER(c_int), c_void_p]),
+    "mflat_flat_search_device_noalloc": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p,
+                                                 POINTER(c_int), c_void_p]),
     "mflat_flat_add_device": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
     "mflat_kmeans_train": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
                                    c_void_p, c_void_p, POINTER(c_int)]),
@@ -229,6 +231,18 @@ class FlatIndex:
             out_ids.data_ptr() if out_ids is not None else None,
             out_dist.data_ptr() if out_dist is not None else None,
             ctypes.byref(used), _stream_ptr(stream)), "mflat_flat_search_device")
+        return used.value
+
+    def search_device_noalloc(self, q, k: int, out_ids, out_dist, stream=None) -> int:
+        """mflat_flat_search_device_noalloc: stream-ordered (synchronise the
+        stream before reading the outputs); m <= 16, k <= 32, dim <= 992 (fp32)
+        or 2016 (fp16 / bf16)."""
+        used = c_int(-1)
+        _check(load().mflat_flat_search_device_noalloc(
+            self._h, q.data_ptr(), q.shape[0], int(k),
+            out_ids.data_ptr() if out_ids is not None else None,
+            out_dist.data_ptr() if out_dist is not None else None,
+            ctypes.byref(used), _stream_ptr(stream)), "mflat_flat_search_device_noalloc")
         return used.value
 
 
