@@ -120,9 +120,10 @@ def cpu_baseline(x, q, k, metric, gpu_ids, storage=0, threads=1, seconds_target=
     one = max(time.perf_counter() - t0, 1e-6) / threads
     n = int(max(1, min(q.shape[0], seconds_target / one)))
     t0 = time.perf_counter()
-    oi, _ = oracle.flat_search(x, q[:n], k, metric=metric, threads=threads)
+    oi, od = oracle.flat_search(x, q[:n], k, metric=metric, threads=threads)
     dt = time.perf_counter() - t0
     recall = float(np.mean([len(set(oi[r].tolist()) & set(gpu_ids[r].tolist())) / k for r in range(n)]))
+    swaps, far = near_tie_swaps(x, q[:n], oi, od, gpu_ids[:n], metric)
     where = "one host core" if threads == 1 else f"{threads} host threads (queries split across them)"
     return {
         "value": n / dt,
@@ -130,8 +131,36 @@ def cpu_baseline(x, q, k, metric, gpu_ids, storage=0, threads=1, seconds_target=
         "cores": threads,
         "kind": "port",
         "sample": f"first {n} of the {q.shape[0]} queries against all {nb} rows (d={d}, k={k}), "
-                  f"{dt:.1f} s on {where}; GPU/oracle id agreement on the sample {recall:.5f}",
+                  f"{dt:.1f} s on {where}; GPU/oracle id agreement on the sample {recall:.5f} "
+                  f"({swaps} differing ids, {far} of them outside the 1e-5 near-tie gap of the k-th value)",
     }
+
+
+def near_tie_swaps(x, q, oi, od, gi, metric):
+    """Ids the GPU returned that the oracle did not, and how many of them lie
+    outside the near-tie gap (1e-5 relative of the oracle's k-th value, plus for
+    L2 2^-20 (||q||^2 + ||x||^2)): float64 distances of those rows only."""
+    import numpy as np
+
+    swaps = far = 0
+    k = oi.shape[1]
+    for r in range(oi.shape[0]):
+        extra = set(gi[r].tolist()) - set(oi[r].tolist())
+        swaps += len(extra)
+        if not extra:
+            continue
+        qq = q[r].astype(np.float64)
+        kth = float(od[r, k - 1])
+        for i in extra:
+            if i < 0:
+                far += 1
+                continue
+            xx = x[i].astype(np.float64)
+            v = float(np.sum((xx - qq) ** 2)) if metric == 0 else float(xx @ qq)
+            floor = 2.0 ** -20 * (float(qq @ qq) + float(xx @ xx)) if metric == 0 else 1e-6
+            if not abs(v - kth) <= 1e-5 * abs(kth) + floor:
+                far += 1
+    return swaps, far
 
 
 def kmeans_bench(iters):
@@ -400,6 +429,206 @@ def ivfpq_bench(args):
     print(json.dumps(out), flush=True)
 
 
+def roofline_of(flop, byts, esize, kernel_s_per_launch, step_s, traffic):
+    """Roofline of one search: the bound is whichever of FLOP / dense peak and
+    algorithmic bytes / HBM bandwidth takes longer; frac = that work over the
+    dominant kernel's mean launch, step_frac = over the whole search."""
+    peak = PEAK_FP32_MFMA_TFLOPS if esize == 4 else PEAK_F16_MFMA_TFLOPS
+    if byts / (PEAK_HBM_GBS * 1e9) > flop / (peak * 1e12):
+        ach = byts / kernel_s_per_launch / 1e9
+        return {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": traffic,
+                "step_frac": round(byts / step_s / 1e9 / PEAK_HBM_GBS, 4)}
+    ach = flop / kernel_s_per_launch / 1e12
+    return {"bound": "mfma", "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(ach / peak, 4), "traffic": traffic,
+            "step_frac": round(flop / step_s / 1e12 / peak, 4)}
+
+
+def flat_bench(cfg, nq_override, storage_name, steps, warmup, cpu=True, host_api=True, data=None,
+               cpu_threads=None, cpu_seconds=12.0):
+    """One flat-search workload: K timed searches (device pointers, inputs in
+    HBM, no instrumentation), then K profiled ones for the kernel means.
+    Returns the bench fields of that workload (headline format)."""
+    import numpy as np
+    import hipmem
+    import mflat
+
+    mflat.load()
+    name, metric, k = WORKLOADS[cfg]
+    t0 = time.perf_counter()
+    x, q = data if data is not None else make_data(cfg, nq_override)
+    if nq_override and cfg != "C4":
+        q = q[:nq_override]
+    elif cfg == "C4" and nq_override:
+        q = q[:nq_override]
+    nb, d = x.shape
+    nq = q.shape[0]
+    log(f"[bench] {cfg}: nb={nb} d={d} nq={nq} k={k} storage={storage_name} data in {time.perf_counter() - t0:.1f}s")
+
+    storage = mflat.STORAGE_NAMES[storage_name]
+    esize = 4 if storage == mflat.MFLAT_STORAGE_F32 else 2
+    idx = mflat.FlatIndex(d, metric, storage)
+    if not idx.ready():
+        raise SystemExit("no usable gfx950 device")
+    try:
+        t0 = time.perf_counter()
+        idx.add(x)
+        log(f"[bench] add {time.perf_counter() - t0:.2f}s")
+        qd = hipmem.DeviceArray.from_numpy(q)
+        ids = hipmem.DeviceArray((nq, k), np.int32)
+        dist = hipmem.DeviceArray((nq, k), np.float32)
+
+        for i in range(warmup):
+            idx.search_device(qd, k, ids, dist)
+        hipmem.synchronize()
+
+        # The timed region: K searches, nothing else (no instrumentation).
+        t0 = time.perf_counter()
+        for i in range(steps):
+            idx.search_device(qd, k, ids, dist)
+        hipmem.synchronize()
+        elapsed = time.perf_counter() - t0
+        log(f"[bench] {steps} steps in {elapsed:.3f}s")
+        # Kernel durations from a separate pass of the same searches with the
+        # library's kernel timer on (HIP events around each launch on its stream).
+        mflat.profile_reset()
+        mflat.profile_enable(True)
+        for i in range(steps):
+            idx.search_device(qd, k, ids, dist)
+        hipmem.synchronize()
+        mflat.profile_enable(False)
+
+        kern = {}
+        for fam in ("scan_filter", "scan_sample", "scan_retry", "select", "argmin", "norms", "prep"):
+            ms, n = mflat.profile_read(fam)
+            if n:
+                kern[fam] = {"total_ms": round(ms, 4), "launches": n, "mean_ms": round(ms / n, 4)}
+
+        gpu_ids = ids.numpy()
+        ms_per_step = elapsed * 1000.0 / steps
+        flop = 2.0 * nq * nb * d
+        dominant = "scan_filter" if "scan_filter" in kern else "argmin"
+        # algorithmic work of a search over the dominant kernel's time per search
+        # (a search may be several launches when its batch exceeds the candidate
+        # workspace, e.g. C5)
+        scan_s = kern[dominant]["total_ms"] / 1000.0 / steps
+        # database in its storage type + queries + ids and values out
+        byts = nb * d * esize + nq * d * esize + nq * k * 8
+        roof = roofline_of(flop, byts, esize, scan_s, elapsed / steps,
+                           MEASURED_TRAFFIC_BYTES.get((cfg, nq, storage_name)))
+        out = {
+            "metric": "QPS + % of MFMA/HBM roofline, flat L2 d=128 nb=1M k=100 (1 GPU)",
+            "value": round(nq * steps / elapsed, 2),
+            "unit": "queries/s",
+            "n_gpus": 1,
+            "steps": steps,
+            "warmup": warmup,
+            "ms_per_step": round(ms_per_step, 4),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": {"f32": "fp32", "f16": "fp16 storage, fp32 accumulate",
+                      "bf16": "bf16 storage, fp32 accumulate"}[storage_name],
+            "data": "synthetic",
+            "config": {"workload": name.replace("{nq}", str(nq)), "nb": nb, "d": d, "nq": nq, "k": k,
+                       "metric": "L2" if metric == 0 else "IP", "storage": storage_name,
+                       "parallelism": "single GPU"},
+            "roofline": roof,
+            "kernels": kern,
+        }
+        if host_api:
+            # The reference's own host-pointer entry point on the same batch,
+            # called as a foreign binding calls it (caller-owned output buffers,
+            # allocated once): includes the H2D copy of the queries and the D2H
+            # copy of ids and values (PCIe), not the Python wrapper's per-call
+            # output allocation and copies.
+            import ctypes
+            lib = mflat.load()
+            qh = np.ascontiguousarray(q, dtype=np.float32)
+            ids_h = np.zeros((nq, k), dtype=np.int32)
+            dist_h = np.zeros((nq, k), dtype=np.float32)
+            used = ctypes.c_int(-1)
+
+            def host_call():
+                st = lib.mflat_flat_search(idx._h, qh.ctypes.data, nq, k, ids_h.ctypes.data, dist_h.ctypes.data,
+                                           ctypes.byref(used))
+                if st != mflat.MFLAT_OK:
+                    raise RuntimeError(f"mflat_flat_search status {st}")
+
+            host_call()   # first call sizes the host-entry staging buffers
+            t0 = time.perf_counter()
+            for _ in range(3):
+                host_call()
+            host_ms = (time.perf_counter() - t0) * 1000.0 / 3
+            out["host_api"] = {"entry": "mflat_flat_search (host buffers, PCIe copies included)",
+                               "ms_per_step": round(host_ms, 4), "queries_per_s": round(nq * 1000.0 / host_ms, 2)}
+            log(f"[bench] host entry {host_ms:.3f} ms/step")
+    finally:
+        idx.close()
+    if cpu:
+        nt = host_threads()
+        if cpu_threads is None:
+            log("[bench] cpu baseline (1 core) ...")
+            out["cpu_baseline"] = cpu_baseline(x, q, k, metric, gpu_ids, storage, seconds_target=cpu_seconds)
+            log(f"[bench] cpu baseline ({nt} threads) ...")
+            out["cpu_baseline_all_cores"] = cpu_baseline(x, q, k, metric, gpu_ids, storage, threads=nt,
+                                                         seconds_target=cpu_seconds)
+        else:
+            out["cpu_baseline"] = cpu_baseline(x, q, k, metric, gpu_ids, storage, threads=min(cpu_threads, nt),
+                                               seconds_target=cpu_seconds)
+        log("[bench] cpu baseline done")
+    return out
+
+
+# The other BASELINE.json configurations, measured in the default run beside the
+# C2 headline: (key, config, query count, storage). C4 is measured at each of
+# its batch sizes, with fp32 and fp16 storage.
+EXTRA_CONFIGS = [
+    ("C1", "C1", 0, "f32"),
+    ("C3", "C3", 0, "f32"),
+    ("C4_nq1", "C4", 1, "f32"),
+    ("C4_nq16", "C4", 16, "f32"),
+    ("C4_nq64", "C4", 64, "f32"),
+    ("C4_nq1_f16", "C4", 1, "f16"),
+    ("C4_nq16_f16", "C4", 16, "f16"),
+    ("C4_nq64_f16", "C4", 64, "f16"),
+    ("C5", "C5", 0, "f32"),
+]
+
+
+def extra_configs(args):
+    """Each extra configuration: ms per search, the dominant kernel, its
+    roofline (kernel and whole-search fractions) and a CPU baseline (the
+    oracle on the host threads, ~3 s of work); a failure is recorded in its
+    entry and does not drop the others or the headline."""
+    out = {}
+    cache = {}
+    # steps per workload: about 0.2 s or more of timed searches (C1, C4 run
+    # 0.4-1.3 ms a search; C3 ~120 ms; C5 ~250 ms)
+    steps_of = {"C1": 200, "C3": 5, "C4": 200, "C5": 5}
+    for key, cfg, nq, storage in EXTRA_CONFIGS:
+        steps = steps_of[cfg]
+        try:
+            if cfg not in cache:
+                cache.clear()
+                cache[cfg] = make_data(cfg, 64 if cfg == "C4" else 0)
+            r = flat_bench(cfg, nq, storage, steps, max(1, args.warmup), cpu=not args.no_cpu_baseline,
+                           host_api=False, data=cache[cfg], cpu_threads=host_threads(), cpu_seconds=3.0)
+            ent = {k: r[k] for k in ("value", "unit", "ms_per_step", "steps", "dtype", "config", "roofline")}
+            dom = "scan_filter" if "scan_filter" in r["kernels"] else "argmin"
+            ent["dominant_kernel"] = {"family": dom, "mean_ms": r["kernels"][dom]["mean_ms"]}
+            ent["kernels"] = r["kernels"]
+            if "cpu_baseline" in r:
+                ent["cpu_baseline"] = r["cpu_baseline"]
+            out[key] = ent
+        except Exception as e:   # noqa: BLE001 -- recorded, the others go on
+            out[key] = {"error": f"{type(e).__name__}: {e}"}
+            log(f"[bench] extra {key} failed: {e}")
+    cache.clear()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -410,6 +639,8 @@ def main():
     ap.add_argument("--storage", default="f32", choices=["f32", "f16", "bf16"],
                     help="element type of the stored database and the queries")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="default run: skip the extra_configs (C1, C3, C4 nq 1/16/64 fp32 and fp16, C5)")
     ap.add_argument("--kmeans", type=int, default=0, metavar="ITERS",
                     help="time the device k-means loop (mflat_kmeans_train) on C5's points and centroid "
                          "count instead: one JSON line with ms per training iteration")
@@ -454,142 +685,10 @@ def main():
         ivfpq_bench(args)
         return
 
-    import numpy as np
-    import hipmem
-    import mflat
-
-    mflat.load()
-    name, metric, k = WORKLOADS[args.config]
-    t0 = time.perf_counter()
-    x, q = make_data(args.config, args.nq)
-    if args.nq and args.config != "C4":
-        q = q[: args.nq]
-    nb, d = x.shape
-    nq = q.shape[0]
-    log(f"[bench] {args.config}: nb={nb} d={d} nq={nq} k={k} data in {time.perf_counter() - t0:.1f}s")
-
-    storage = mflat.STORAGE_NAMES[args.storage]
-    esize = 4 if storage == mflat.MFLAT_STORAGE_F32 else 2
-    idx = mflat.FlatIndex(d, metric, storage)
-    if not idx.ready():
-        raise SystemExit("no usable gfx950 device")
-    t0 = time.perf_counter()
-    idx.add(x)
-    log(f"[bench] add {time.perf_counter() - t0:.2f}s")
-    qd = hipmem.DeviceArray.from_numpy(q)
-    ids = hipmem.DeviceArray((nq, k), np.int32)
-    dist = hipmem.DeviceArray((nq, k), np.float32)
-
-    for i in range(args.warmup):
-        idx.search_device(qd, k, ids, dist)
-        log(f"[bench] warmup {i + 1}/{args.warmup} done")
-    hipmem.synchronize()
-
-    # The timed region: K searches, nothing else (no instrumentation).
-    hipmem.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        idx.search_device(qd, k, ids, dist)
-    hipmem.synchronize()
-    elapsed = time.perf_counter() - t0
-    log(f"[bench] {args.steps} steps in {elapsed:.3f}s")
-    # Kernel durations from a separate pass of the same searches with the
-    # library's kernel timer on (HIP events around each launch on its stream).
-    mflat.profile_reset()
-    mflat.profile_enable(True)
-    for i in range(args.steps):
-        idx.search_device(qd, k, ids, dist)
-    hipmem.synchronize()
-    mflat.profile_enable(False)
-
-    kern = {}
-    for fam in ("scan_filter", "scan_sample", "scan_retry", "select", "argmin", "norms", "prep"):
-        ms, n = mflat.profile_read(fam)
-        if n:
-            kern[fam] = {"total_ms": round(ms, 4), "launches": n, "mean_ms": round(ms / n, 4)}
-
-    gpu_ids = ids.numpy()
-    ms_per_step = elapsed * 1000.0 / args.steps
-    flop = 2.0 * nq * nb * d
-    dominant = "scan_filter" if "scan_filter" in kern else "argmin"
-    scan = kern[dominant]
-    # Algorithmic work of the whole timed region over the dominant kernel's total
-    # time (a search may be split into several launches when the query batch is
-    # larger than the candidate workspace, e.g. C5).
-    scan_s = scan["total_ms"] / 1000.0
-    # Bound: whichever of FLOP / peak and algorithmic bytes / HBM bandwidth is
-    # longer (database in its storage type + queries + ids and values out).
-    byts = nb * d * esize + nq * d * esize + nq * k * 8
-    peak = PEAK_FP32_MFMA_TFLOPS if esize == 4 else PEAK_F16_MFMA_TFLOPS
-    traffic = MEASURED_TRAFFIC_BYTES.get((args.config, nq, args.storage))
-    # frac: the dominant kernel's rate (algorithmic work / its mean launch
-    # duration); step_frac: the same work over the whole step (every launch,
-    # gap and synchronisation of a search), the search's own roofline fraction.
-    step_s = elapsed / args.steps
-    if byts / (PEAK_HBM_GBS * 1e9) > flop / (peak * 1e12):
-        ach = byts * args.steps / scan_s / 1e9
-        roof = {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": traffic,
-                "step_frac": round(byts / step_s / 1e9 / PEAK_HBM_GBS, 4)}
-    else:
-        ach = flop * args.steps / scan_s / 1e12
-        roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
-                "frac": round(ach / peak, 4), "traffic": traffic,
-                "step_frac": round(flop / step_s / 1e12 / peak, 4)}
-
-    out = {
-        "metric": "QPS + % of MFMA/HBM roofline, flat L2 d=128 nb=1M k=100 (1 GPU)",
-        "value": round(nq * args.steps / elapsed, 2),
-        "unit": "queries/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": {"f32": "fp32", "f16": "fp16 storage, fp32 accumulate",
-                  "bf16": "bf16 storage, fp32 accumulate"}[args.storage],
-        "data": "synthetic",
-        "config": {"workload": name.replace("{nq}", str(nq)), "nb": nb, "d": d, "nq": nq, "k": k,
-                   "metric": "L2" if metric == 0 else "IP", "storage": args.storage,
-                   "parallelism": "single GPU"},
-        "roofline": roof,
-        "kernels": kern,
-    }
-    # The reference's own host-pointer entry point on the same batch, called as
-    # a foreign binding calls it (caller-owned output buffers, allocated once):
-    # includes the H2D copy of the queries and the D2H copy of ids and values
-    # (PCIe), not the Python wrapper's per-call output allocation and copies.
-    import ctypes
-    lib = mflat.load()
-    qh = np.ascontiguousarray(q, dtype=np.float32)
-    ids_h = np.zeros((nq, k), dtype=np.int32)
-    dist_h = np.zeros((nq, k), dtype=np.float32)
-    used = ctypes.c_int(-1)
-
-    def host_call():
-        st = lib.mflat_flat_search(idx._h, qh.ctypes.data, nq, k, ids_h.ctypes.data, dist_h.ctypes.data,
-                                   ctypes.byref(used))
-        if st != mflat.MFLAT_OK:
-            raise RuntimeError(f"mflat_flat_search status {st}")
-
-    host_call()   # first call sizes the host-entry staging buffers
-    t0 = time.perf_counter()
-    for _ in range(3):
-        host_call()
-    host_ms = (time.perf_counter() - t0) * 1000.0 / 3
-    out["host_api"] = {"entry": "mflat_flat_search (host buffers, PCIe copies included)",
-                       "ms_per_step": round(host_ms, 4), "queries_per_s": round(nq * 1000.0 / host_ms, 2)}
-    log(f"[bench] host entry {host_ms:.3f} ms/step")
-    if not args.no_cpu_baseline:
-        log("[bench] cpu baseline (1 core) ...")
-        out["cpu_baseline"] = cpu_baseline(x, q, k, metric, gpu_ids, storage)
-        nt = host_threads()
-        log(f"[bench] cpu baseline ({nt} threads) ...")
-        out["cpu_baseline_all_cores"] = cpu_baseline(x, q, k, metric, gpu_ids, storage, threads=nt)
-        log("[bench] cpu baseline done")
-    idx.close()
+    out = flat_bench(args.config, args.nq, args.storage, args.steps, args.warmup,
+                     cpu=not args.no_cpu_baseline, host_api=True)
+    if args.config == "C2" and not args.nq and args.storage == "f32" and not args.no_extra:
+        out["extra_configs"] = extra_configs(args)
     print(json.dumps(out), flush=True)
 
 
