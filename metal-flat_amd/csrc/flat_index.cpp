@@ -139,12 +139,14 @@ int chooseJ(int k, double lambda, double tail) {
 // minTiles: fewest kBM-row tiles per split (a scan_resident workgroup needs
 // two tiles to give each of its four waves a 64-row slice).
 // concurrent (> 0): workgroups of the MFMA scan that run at once
-// (scan_concurrency). The launch's nqb x nsplit equal workgroups run in rounds
-// of that many; a last round of a few leaves the chip idle for most of a
-// round (C2: 79 x 26 = 2054 workgroups in rounds of 512 -- 10% of the scan).
-// The split count is then chosen in [want, 3 want] to minimise
-// rounds x (tiles per split + 1), a partial round of fraction f costing
-// 0.5 + 0.5 f of a full one (its workgroups run alone, faster).
+// (scan_concurrency). The launch's nqb x nsplit workgroups run in rounds of
+// that many; a last round of a few leaves the chip idle for most of a round
+// (C1: 8 x 196 = 1,568 workgroups in rounds of 512, a fourth round of 32).
+// Splits share the tiles as evenly as possible (split s starts at tile
+// s * ntiles / nsplit), so any split count is possible: it is chosen in
+// [want / 4, 3 want] to minimise rounds x (tiles of the largest split + 1),
+// a partial round of fraction f costing 0.5 + 0.5 f of a full one (its
+// workgroups run alone, faster). rowsPerSplit is the largest split's rows.
 void splitPlan(int64_t nrows, int nq, int dpad, int storage, int64_t& rowsPerSplit, int& nsplit,
                bool allowSmall = true, int64_t minTiles = 1, int concurrent = 0) {
     const int nqb = (nq + kBN - 1) / kBN;
@@ -154,16 +156,17 @@ void splitPlan(int64_t nrows, int nq, int dpad, int storage, int64_t& rowsPerSpl
     // keep a split's bytes addressable with 32-bit offsets
     const int64_t maxTiles =
         std::max<int64_t>(1, ((int64_t)1 << 31) / ((int64_t)kBM * dpad * elem_bytes(storage)) - 1);
-    want = std::max(want, (ntiles + maxTiles - 1) / maxTiles);
+    const int64_t fewest = std::min<int64_t>(kMaxSplit, (ntiles + maxTiles - 1) / maxTiles);
+    want = std::max(want, fewest);
     want = std::min<int64_t>(want, kMaxSplit);
     want = std::min(want, std::max<int64_t>(1, ntiles / minTiles));
     want = std::min(want, ntiles);
     if (concurrent > 0 && !(allowSmall && small_scan_fits(nq, dpad, storage))) {
-        const int64_t lo = want;   // fewer, longer splits measured slower on short scans (C1, samples)
+        const int64_t lo = std::max<int64_t>({1, fewest, want / 4});
         const int64_t hi = std::min<int64_t>({3 * want, kMaxSplit, std::max<int64_t>(1, ntiles / minTiles), ntiles});
         auto cost = [&](int64_t ns) {
             const int64_t tps = (ntiles + ns - 1) / ns;
-            const int64_t w = (int64_t)nqb * ((ntiles + tps - 1) / tps);
+            const int64_t w = (int64_t)nqb * ns;
             const int64_t full = w / concurrent, rem = w % concurrent;
             const double rounds = (double)full + (rem ? 0.5 + 0.5 * (double)rem / concurrent : 0.0);
             return rounds * ((double)tps + 1.0);
@@ -179,9 +182,8 @@ void splitPlan(int64_t nrows, int nq, int dpad, int storage, int64_t& rowsPerSpl
         }
         want = best;
     }
-    const int64_t tps = (ntiles + want - 1) / want;
-    nsplit = (int)((ntiles + tps - 1) / tps);
-    rowsPerSplit = tps * kBM;
+    nsplit = (int)want;
+    rowsPerSplit = (ntiles + want - 1) / want * kBM;
 }
 
 int pow2ceil(int64_t x) {

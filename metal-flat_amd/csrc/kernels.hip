@@ -62,6 +62,14 @@ __device__ __forceinline__ uint64_t composite(uint2 c) {
     return ((uint64_t)key_to_ord(c.x) << 32) | (uint64_t)c.y;
 }
 
+// First row of split s of a full-database pass: the splits share the kBM-row
+// tiles as evenly as possible (tile counts differ by at most one), so a plan
+// may take any split count; split nsplit starts at the padded row count.
+__device__ __forceinline__ int64_t split_row(const ScanParams& p, int s) {
+    const int64_t tiles = (p.nrows + kBM - 1) / kBM;
+    return tiles * s / p.nsplit * kBM;
+}
+
 static void check_launch(const char* what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
@@ -703,10 +711,8 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
         if (p.ivf_row_cap > 0 && rowLim > p.ivf_row_cap) rowLim = p.ivf_row_cap;   // a cell's first rows only
         ntiles = (int)((rowLim + kBM - 1) / kBM);
     } else {
-        const int64_t rows_pad = (p.nrows + kBM - 1) / kBM * kBM;
-        rowBeg = (int64_t)split * p.rows_per_split;
-        int64_t rowEnd = rowBeg + p.rows_per_split;
-        if (rowEnd > rows_pad) rowEnd = rows_pad;
+        rowBeg = split_row(p, split);
+        const int64_t rowEnd = split_row(p, split + 1);
         ntiles = rowEnd > rowBeg ? (int)((rowEnd - rowBeg) / kBM) : 0;
         rowOrg = rowBeg;
         rowLim = p.nrows;
@@ -1012,7 +1018,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     }
     // A retry whose work list the device built: query blocks beyond it are idle.
     const int nqv = (PASS == kPassRetry && p.nq_dev) ? *p.nq_dev : p.nq;
-    if (!IVF && qb * kBN >= nqv) return;
+    if (!IVF && qb * TQ >= nqv) return;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1033,7 +1039,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     }
     {
         const int rowP = p.dpad * ES / 16;
-        const fx4* qg = (const fx4*)p.Q + (int64_t)qb * kBN * rowP;
+        const fx4* qg = (const fx4*)p.Q + (int64_t)qb * TQ * rowP;
         // eight 16-byte pieces per thread in flight (a work item of the IVF
         // scan is short enough for serial load latencies here to show)
         const int npc = TQ * rowP;
@@ -1083,7 +1089,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
             qv[bn] = q >= 0;
             if (qv[bn]) idb[bn] = p.ivf_pos[sEnt[bn * 32 + r32]];
         } else {
-            q = qb * kBN + bn * 32 + r32;
+            q = qb * TQ + bn * 32 + r32;
             qv[bn] = q < nqv;
         }
         if (PASS == kPassArgmin) {
@@ -1109,7 +1115,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
                 q = sQi[tid];
                 v = q >= 0;
             } else {
-                q = qb * kBN + tid;
+                q = qb * TQ + tid;
                 v = q < nqv;
             }
             sLTk[tid] = v ? p.tau_key[q] : 0.0f;
@@ -1131,10 +1137,8 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
         if (p.ivf_row_cap > 0 && rowLim > p.ivf_row_cap) rowLim = p.ivf_row_cap;   // a cell's first rows only
         nsl = (int)((rowLim + 63) / 64);
     } else {
-        const int64_t rows_pad = (p.nrows + kBM - 1) / kBM * kBM;
-        rowBeg = (int64_t)split * p.rows_per_split;
-        int64_t rowEnd = rowBeg + p.rows_per_split;
-        if (rowEnd > rows_pad) rowEnd = rows_pad;
+        rowBeg = split_row(p, split);
+        const int64_t rowEnd = split_row(p, split + 1);
         nsl = rowEnd > rowBeg ? (int)((rowEnd - rowBeg) / 64) : 0;
         rowOrg = rowBeg;
         rowLim = p.nrows;
@@ -1142,7 +1146,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     const int idStride = IVF ? 1 : p.id_stride;
     auto region = [&](int ql) -> int64_t {
         if constexpr (IVF) return sReg[ql];
-        return ((int64_t)qb * kBN + ql) * p.nsplit + split;
+        return ((int64_t)qb * TQ + ql) * p.nsplit + split;
     };
     // Survivor of slot ql at its region's slot `slot`. IVF with a spill region
     // (region nprobe of each query, filled by global atomics on its count): the
@@ -1151,7 +1155,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     auto store = [&](int ql, int slot, uint2 v) {
         if constexpr (PASS == kPassRetry && !IVF) {
             if (p.qcnt) {   // pooled region of the query (global slot counter)
-                const int q = qb * kBN + ql;
+                const int q = qb * TQ + ql;
                 const int gs = atomicAdd(&p.qcnt[(int64_t)q * kPoolCntStride], 1);
                 if (gs < p.qcap[q]) p.cand[p.qoff[q] + gs] = v;
                 return;
@@ -1344,7 +1348,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
                           ((unsigned long long)key_to_ord(__float_as_uint(tk[bn])) << 32) | (unsigned)ti[bn]);
         __syncthreads();
         if (tid < TQ) {
-            const int q = qb * kBN + tid;
+            const int q = qb * TQ + tid;
             if (q < p.nq && sBest[tid] != ~0ull) atomicMin(&p.best[q], sBest[tid]);
         }
         return;
@@ -1353,7 +1357,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     if constexpr (IVF) {
         if (tid < wk.z) p.cnt[sReg[tid]] = p.ivf_spill && sCnt[tid] > p.cap ? p.cap : sCnt[tid];
     } else if (tid < TQ) {
-        const int q = qb * kBN + tid;
+        const int q = qb * TQ + tid;
         if (q < nqv && !(PASS == kPassRetry && p.qcnt)) p.cnt[(int64_t)q * p.nsplit + split] = sCnt[tid];
     }
 }
@@ -1434,10 +1438,8 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
     }
     __syncthreads();
 
-    const int64_t rows_pad = (p.nrows + kBM - 1) / kBM * kBM;
-    const int64_t rowBeg = (int64_t)split * p.rows_per_split;
-    int64_t rowEnd = rowBeg + p.rows_per_split;
-    if (rowEnd > rows_pad) rowEnd = rows_pad;
+    const int64_t rowBeg = split_row(p, split);
+    const int64_t rowEnd = split_row(p, split + 1);
     // Each wave takes 32-row blocks (two 16-row MFMA sets) round-robin. In the
     // chunked layout, the operand piece e of row half hh for chunk t is one
     // linear 1 KB load per wave: lane l reads piece l of sub-chunk (hh, e),
@@ -2388,9 +2390,18 @@ static void launch_resident_p(const ScanParams& p, int g, size_t lds, hipStream_
     (void)ok;
     scan_resident_kernel<S, M, P, G, IVF, NB><<<g, 256, lds, s>>>(p);
 }
+static size_t resident_lds_bytes(int dpad, int storage, int tileQueries);
+// The row-sample pass runs 32-query tiles (NB = 1): it stores every row it
+// reads, so the survivor stores, not the MFMA work, set its time, and 4x the
+// workgroups spread them; the per-pair MFMA sequence is the same as the
+// 128-query tiles', so its keys are bit-identical to the other passes'.
 template <int S, int M, int G>
 static void launch_resident_g(const ScanParams& p, int pass, int g, size_t lds, hipStream_t s) {
-    if (pass == kPassSample) launch_resident_p<S, M, kPassSample, G>(p, g, lds, s);
+    if (pass == kPassSample) {
+        ScanParams q = p;
+        q.nqb = (p.nq + 31) / 32;
+        launch_resident_p<S, M, kPassSample, G, false, 1>(q, q.nqb * p.nsplit, resident_lds_bytes(p.dpad, S, 32), s);
+    }
     else if (pass == kPassRetry) launch_resident_p<S, M, kPassRetry, G>(p, g, lds, s);
     else launch_resident_p<S, M, kPassFull, G>(p, g, lds, s);
 }
@@ -2437,13 +2448,13 @@ static void launch_ivf_s(const ScanParams& p, int metric, int pass, int nb, int 
     }
 }
 
-static size_t resident_lds_bytes(int dpad, int storage, int tileQueries = kBN) {
+static size_t resident_lds_bytes(int dpad, int storage, int tileQueries) {
     const int es = elem_bytes(storage);
     return (size_t)tileQueries * (dpad + 16 / es) * es;
 }
 
 bool resident_scan_fits(int dpad, int storage) {
-    return resident_lds_bytes(dpad, storage) <= kResidentMaxLds;
+    return resident_lds_bytes(dpad, storage, kBN) <= kResidentMaxLds;
 }
 
 bool ivf_narrow_fits(int dpad, int storage) {
@@ -2530,12 +2541,18 @@ static const void* resident_fn(int pass, int dpad) {
         static const void* k = f((const void*)scan_resident_kernel<S, M, P, GG, false, 4>); \
         return k;                                                                           \
     }
-    MFLAT_RES_FN(kPassSample, 0) MFLAT_RES_FN(kPassRetry, 0) MFLAT_RES_FN(kPassFull, 0)
+#define MFLAT_RES_FN1(GG)                                                                              \
+    if (pass == kPassSample && G == GG) {                                                              \
+        static const void* k = f((const void*)scan_resident_kernel<S, M, kPassSample, GG, false, 1>); \
+        return k;                                                                                      \
+    }
+    MFLAT_RES_FN1(0) MFLAT_RES_FN(kPassRetry, 0) MFLAT_RES_FN(kPassFull, 0)
     if constexpr (S != kF32) {
-        MFLAT_RES_FN(kPassSample, 3) MFLAT_RES_FN(kPassRetry, 3) MFLAT_RES_FN(kPassFull, 3)
-        MFLAT_RES_FN(kPassSample, 4) MFLAT_RES_FN(kPassRetry, 4) MFLAT_RES_FN(kPassFull, 4)
+        MFLAT_RES_FN1(3) MFLAT_RES_FN(kPassRetry, 3) MFLAT_RES_FN(kPassFull, 3)
+        MFLAT_RES_FN1(4) MFLAT_RES_FN(kPassRetry, 4) MFLAT_RES_FN(kPassFull, 4)
     }
 #undef MFLAT_RES_FN
+#undef MFLAT_RES_FN1
     return nullptr;
 }
 template <int S, int M>
@@ -2548,7 +2565,7 @@ static const void* tiled_fn(int pass) {
 template <int S>
 static const void* scan_fn(int dpad, int metric, int pass, size_t& lds) {
     if (resident_scan_fits(dpad, S)) {
-        lds = resident_lds_bytes(dpad, S);
+        lds = resident_lds_bytes(dpad, S, pass == kPassSample ? 32 : kBN);   // the sample pass: 32-query tiles
         return metric == 0 ? resident_fn<S, 0>(pass, dpad) : resident_fn<S, 1>(pass, dpad);
     }
     lds = 0;
@@ -2598,7 +2615,7 @@ void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, 
                : pass == kPassArgmin ? kFamArgmin : kFamScan, s, &tok);
     const int g = (int)grid;
     if (resident_scan_fits(p.dpad, storage)) {
-        const size_t lds = resident_lds_bytes(p.dpad, storage);
+        const size_t lds = resident_lds_bytes(p.dpad, storage, kBN);
         if (storage == kF32) launch_resident_s<kF32>(p, metric, pass, g, lds, s);
         else if (storage == kF16) launch_resident_s<kF16>(p, metric, pass, g, lds, s);
         else launch_resident_s<kBF16>(p, metric, pass, g, lds, s);

@@ -94,7 +94,8 @@ struct ScanParams {
     const float* xnorm;      // per-row ||x||^2 (L2 only)
     float xnorm_max;         // >= every finite ||x||^2 of the pass (L2 fast-reject margin)
     int64_t nrows;           // valid rows; rows >= nrows are padding
-    int64_t rows_per_split;  // multiple of kBM
+    int64_t rows_per_split;  // largest split's rows, a multiple of kBM (split s starts at tile
+                             // s * tiles / nsplit: tile counts differ by at most one)
     int nsplit;              // database splits (grid = nqb * nsplit)
     int id_stride;           // reported id = row * id_stride (sample passes)
     const void* Q;           // queries (storage type, row-major)
