@@ -101,12 +101,13 @@ struct PinnedInts {
 // Device storage of the retry work lists (kernels.hpp RetryLists).
 struct RetryStore {
     DevBuf fail, lvl, idx, tk, ti, qoff, qcap, qcnt, counters;
-    void ensure(int mb, int rmax) {
+    void ensure(int mb, int rmax, hipStream_t s) {
         fail.ensure((size_t)mb * 4);
         lvl.ensure((size_t)mb);
         for (DevBuf* b : {&idx, &tk, &ti, &qcap}) b->ensure((size_t)rmax * 4);
         qcnt.ensure((size_t)rmax * kPoolCntStride * 4);
         qoff.ensure((size_t)rmax * sizeof(int64_t));
+        (void)s;
         counters.ensure(4 * sizeof(int));
     }
     RetryLists lists() const {
@@ -646,6 +647,9 @@ struct FlatIndex::Impl {
             return;
         }
 
+        // the retry round's buffers -- and the candidate pool every pass
+        // shares -- are sized before any pass writes candidates
+        RetryRound rr = retryPrepare(mb, k, pl, Q, qn, s);
         ensureSample(smp[0], pl.R0, pl.stride, s);
         if (pl.Rb) ensureSample(smp[1], pl.Rb, pl.strideb, s);
         if (traceOn())
@@ -693,14 +697,15 @@ struct FlatIndex::Impl {
             launch_select(sp, s);
         }
 
-        retries(mb, k, pl, Q, qn, oIds, oVals, s);
+        retries(mb, k, rr, Q, qn, oIds, oVals, s);
     }
 
     // Verification and retries, as a fixed launch sequence whose work list the
     // device builds (no host round trip): a query is exact unless its
     // full-pass select reported an overflow or fewer than k stored rows. One
-    // round (retry_plan, gather, pooled scan, select) reruns up to rmax of
-    // them, each with one candidate region of its own:
+    // round (retry_plan: bounds, pooled regions and the rerun queries' rows in
+    // one block; pooled scan; select) reruns up to rmax of them, each with
+    // one candidate region of its own:
     //   overflow: under the k-th best it stored, the region sized by the rows
     //             it saw under its looser bound -- a subset, so the rerun is
     //             final;
@@ -710,11 +715,25 @@ struct FlatIndex::Impl {
     // Launches with an empty list exit at once. Three counters come back with
     // the batch's final synchronisation; only if a query is left (more than
     // rmax failed, a region did not fit the pool, a rerun failed again) does
-    // the host run further rounds before returning. Every rerun either ends a
-    // query or moves it up its bound ladder, so the rounds terminate.
-    void retries(int mb, int k, const Plan& pl, const void* Q, const float* qn, int32_t* oIds, float* oVals,
-                 hipStream_t s) {
-        const bool batchSmall = small_scan_fits(mb, dpad, storage);
+    // the host run further rounds before returning.
+    // Every rerun either ends a query or moves it up its bound ladder, so the
+    // rounds terminate.
+    struct RetryRound {
+        bool batchSmall = false;
+        int rmax = 1, rowsPad = kBN, rowBytes = 0;
+        int64_t rps = 0;
+        int nsplit = 1;
+        RetryLadder lad{};
+        int k = 1;
+        double expect = 0.0;
+    };
+
+    RetryRound retryPrepare(int mb, int k, const Plan& pl, const void* Q, const float* qn, hipStream_t s) {
+        (void)Q;
+        (void)qn;
+        RetryRound rr;
+        rr.k = k;
+        rr.batchSmall = small_scan_fits(mb, dpad, storage);
         // pooled capacities of the ladder's bounds: ~rank nb / R0 rows
         // admitted, three times that (and at least k, so an overflowing rerun
         // keeps a k-th best) before the final kind of rerun takes over
@@ -722,53 +741,78 @@ struct FlatIndex::Impl {
             const double e = (double)rank * (double)nb / std::max<double>(1.0, (double)pl.R0);
             return (int)std::min<double>((double)std::max<int64_t>(nb, 1), std::max(3.0 * e + 256.0, (double)k));
         };
-        RetryLadder lad;
-        std::memset(&lad, 0, sizeof lad);
+        std::memset(&rr.lad, 0, sizeof rr.lad);
         if (pl.j2 > pl.j) {
-            lad.j2_key = tauS2k.as<float>(); lad.j2_id = tauS2i.as<int>();
-            lad.cap_j2 = capFor(pl.j2);
+            rr.lad.j2_key = tauS2k.as<float>(); rr.lad.j2_id = tauS2i.as<int>();
+            rr.lad.cap_j2 = capFor(pl.j2);
         }
-        lad.g_key = tauGk.as<float>(); lad.g_id = tauGi.as<int>();
-        lad.cap_g = capFor(k);
+        rr.lad.g_key = tauGk.as<float>(); rr.lad.g_id = tauGi.as<int>();
+        rr.lad.cap_g = capFor(k);
         // a window of rmax queries whose regions fit the candidate budget
-        int rmax = std::max(1, std::min(mb, retryWindow > 0 ? retryWindow : batchSmall ? kSmallMaxQ : kRetryMax));
-        const size_t perQ = (size_t)std::max(lad.cap_g, lad.cap_j2) * sizeof(uint2);
+        int rmax = std::max(1, std::min({mb, retryWindow > 0 ? retryWindow : rr.batchSmall ? kSmallMaxQ : kRetryMax,
+                                         kRetryPlanMax}));
+        const size_t perQ = (size_t)std::max(rr.lad.cap_g, rr.lad.cap_j2) * sizeof(uint2);
         while (rmax > 1 && (size_t)rmax * perQ > kCandBudget) rmax = (rmax + 1) / 2;
-        const int rowsPad = (int)roundUp(rmax, kBN);
-        const int rowBytes = dpad * esize;
+        rr.rmax = rmax;
+        rr.rowsPad = (int)roundUp(rmax, kBN);
+        rr.rowBytes = dpad * esize;
         // Retries run the kernel family of the passes their bounds came from
         // (the whole batch's), so every bound is compared with keys computed
         // the same way (a guaranteed bound must admit its own rows). Pooled
-        // regions do not depend on the split plan: it only spreads the work.
-        // The split plan is made for one block of queries (a window rarely
-        // holds more): the launch covers rmax, and blocks past the device's
-        // count exit at once.
-        int64_t rps;
-        int nsplit;
-        splitPlan(nb, std::min(rmax, kBN), dpad, storage, rps, nsplit, batchSmall, batchSmall ? 1 : kRetryMinTiles,
-                  concurrency(kPassRetry));
+        // regions do not depend on the split plan: it only spreads the work,
+        // made for one block of queries (a window rarely holds more: the
+        // launch covers rmax, and blocks past the device's count exit at once).
+        splitPlan(nb, std::min(rmax, kBN), dpad, storage, rr.rps, rr.nsplit, rr.batchSmall,
+                  rr.batchSmall ? 1 : kRetryMinTiles, concurrency(kPassRetry));
+        // j2 reruns, the usual kind: ~j2 nb / R0 candidates
+        rr.expect = 1.5 * std::max(pl.j2, 2) * (double)nb / std::max<double>(1.0, (double)pl.R0) + 2.0 * k;
 
-        rl.ensure(mb, rmax);
-        cQ.ensure((size_t)rowsPad * rowBytes);
-        cQn.ensure((size_t)rowsPad * 4);
-        // the pool is the candidate buffer, whose full-pass contents the
-        // full pass's select has consumed: at least one whole region of each
-        // rerun kind for a full window
-        cand.ensure((size_t)rmax * perQ);
+        rl.ensure(mb, rmax, s);
+        cQ.ensure((size_t)rr.rowsPad * rr.rowBytes);
+        cQn.ensure((size_t)rr.rowsPad * 4);
+        // one buffer for every pass's candidates and the retry pool, sized now
+        // so no later pass reallocates it under another's candidates
+        cand.ensure(std::max((size_t)rmax * perQ, (size_t)mb * pl.perQuery * sizeof(uint2)));
+        return rr;
+    }
+
+    RetryPlanArgs retryArgs(int mb, const RetryRound& rr, const void* Q, const float* qn, bool first,
+                            bool drain = false) const {
+        RetryPlanArgs a;
+        std::memset(&a, 0, sizeof a);
+        a.status = status.as<int>();
+        a.mb = mb;
+        a.first = first ? 1 : 0;
+        a.tau_k_key = tauKk.as<float>();
+        a.tau_k_id = tauKi.as<int>();
+        a.total = total.as<int>();
+        a.ladder = rr.lad;
+        a.pool_entries = (int64_t)(cand.bytes / sizeof(uint2));
+        // drain: the host's fallback, whose pool always holds one query's region
+        if (retryPool > 0 && !drain) a.pool_entries = std::min<int64_t>(a.pool_entries, retryPool);
+        a.rmax = rr.rmax;
+        a.all_rows = (int)std::max<int64_t>(nb, 1);
+        a.lists = rl.lists();
+        a.Q = Q;
+        a.qn = qn;
+        a.row_bytes = rr.rowBytes;
+        a.dst_q = cQ.p;
+        a.dst_qn = cQn.as<float>();
+        a.rows_pad = rr.rowsPad;
+        return a;
+    }
+
+    void retries(int mb, int k, const RetryRound& rr, const void* Q, const float* qn, int32_t* oIds, float* oVals,
+                 hipStream_t s) {
         const RetryLists L = rl.lists();
-
         auto round = [&](bool first, bool drain) {
-            int64_t pool = (int64_t)(cand.bytes / sizeof(uint2));
-            if (retryPool > 0 && !drain) pool = std::min<int64_t>(pool, retryPool);
-            launch_retry_plan(status.as<int>(), mb, first ? 1 : 0, tauKk.as<float>(), tauKi.as<int>(),
-                              total.as<int>(), lad, pool, rmax, (int)std::max<int64_t>(nb, 1), L, s);
-            launch_gather_rows_dev(Q, qn, L.idx, L.counters + 1, rowBytes, cQ.p, cQn.as<float>(), rowsPad, s);
-            ScanParams p = scanParams(X.p, xn.as<float>(), nb, rps, nsplit, 1, cQ.p, cQn.as<float>(), rmax, L.tk,
-                                      L.ti, 1);
+            launch_retry_plan(retryArgs(mb, rr, Q, qn, first, drain), s);
+            ScanParams p = scanParams(X.p, xn.as<float>(), nb, rr.rps, rr.nsplit, 1, cQ.p, cQn.as<float>(), rr.rmax,
+                                      L.tk, L.ti, 1);
             p.nq_dev = L.counters + 1;
             p.qcnt = L.qcnt; p.qoff = L.qoff; p.qcap = L.qcap;
-            launch_scan_filter(p, kernMetric(), kPassRetry, storage, s, batchSmall);
-            SelectParams sp = selectParams(rmax, 1, 1, k, k);
+            launch_scan_filter(p, kernMetric(), kPassRetry, storage, s, rr.batchSmall);
+            SelectParams sp = selectParams(rr.rmax, 1, 1, k, k);
             sp.cnt = L.qcnt;
             sp.qoff = L.qoff; sp.qcap = L.qcap;
             sp.nq_dev = L.counters + 1;
@@ -778,9 +822,7 @@ struct FlatIndex::Impl {
             sp.status = status.as<int>();
             sp.total = total.as<int>();
             sp.fail_count = L.counters + 2;
-            // j2 reruns, the usual kind: ~j2 nb / R0 candidates
-            sp.expect = (int)std::min<double>(1.5 * std::max(pl.j2, 2) * (double)nb /
-                                              std::max<double>(1.0, (double)pl.R0) + 2.0 * k, 1e9);
+            sp.expect = (int)std::min(rr.expect, 1e9);
             launch_select(sp, s);
             hostCounters.ensure();
             HIPC(hipMemcpyAsync(hostCounters.p, L.counters, 3 * sizeof(int), hipMemcpyDeviceToHost, s));
@@ -793,7 +835,7 @@ struct FlatIndex::Impl {
                          hostCounters.p[0], mb, hostCounters.p[1], left);
         // Host fallback: a pool of nb entries holds any single region, so
         // every round schedules at least one query.
-        const int64_t limit = 4 * ((int64_t)mb / rmax + 2) + 3LL * mb;
+        const int64_t limit = 4 * ((int64_t)mb / rr.rmax + 2) + 3LL * mb;
         for (int64_t r = 0; left > 0; ++r) {
             if (r > limit) throw std::runtime_error("flat search: retries did not converge");
             cand.ensure((size_t)std::max<int64_t>(nb, 1) * sizeof(uint2));

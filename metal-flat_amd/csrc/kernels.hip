@@ -331,102 +331,142 @@ __global__ void gather_tau_kernel(TauSources src, const int* __restrict__ idx,
 // device-built retry work lists (flat search)
 // ---------------------------------------------------------------------------
 
-// One 1024-thread block: the plan of a retry round (RetryLists). Failing
-// queries are listed in ascending order (a block prefix count per 1024), then
-// thread 0 walks the list assigning bounds and pooled regions while they fit.
-__global__ void __launch_bounds__(1024) retry_plan_kernel(const int* __restrict__ status, int mb, int first,
-                                                          const float* __restrict__ tkK,
-                                                          const int* __restrict__ tiK,
-                                                          const int* __restrict__ total, RetryLadder lad,
-                                                          int64_t pool_entries, int rmax, int all_rows,
-                                                          RetryLists rl) {
-    __shared__ int sW[16];
-    __shared__ int sBase;
+// The plan of a retry round (RetryLists), run by one block of NT threads.
+// 1. The failing queries (status nonzero), listed in ascending order: a block
+//    prefix count over NT x 4 queries per step, four status loads in flight.
+// 2. For the first rmax of them, in parallel: bound, ladder step and pooled
+//    capacity (LDS scratch w: two 64-bit words per entry).
+// 3. Thread 0 walks those capacities in LDS assigning pool offsets while they
+//    fit (a query too large for this pool before any fits is left for a
+//    later, larger pool).
+// 4. In parallel: the scheduled queries' lists, rows of Q and norms (rows
+//    past them up to the end of their query block zeroed).
+// sW: NT / 64 ints of LDS; w: 2 * rmax 64-bit words of LDS.
+template <int NT>
+__device__ void retry_plan_block(const RetryPlanArgs& a, int* sW, int* sBase, int* sN, uint64_t* w) {
+    const RetryLists& rl = a.lists;
+    const RetryLadder& lad = a.ladder;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    if (tid == 0) sBase = 0;
+    constexpr int NW = NT / 64;
+    if (tid == 0) *sBase = 0;
     __syncthreads();
-    for (int q0 = 0; q0 < mb; q0 += 1024) {
-        const int q = q0 + tid;
-        const bool f = q < mb && status[q] != 0;
-        if (first && q < mb) rl.lvl[q] = 0;
-        const unsigned long long bal = __ballot(f);
-        if (lane == 0) sW[wave] = __popcll(bal);
-        __syncthreads();
-        int base = sBase;
-        for (int w = 0; w < wave; ++w) base += sW[w];
-        if (f) rl.fail[base + __popcll(bal & ((1ull << lane) - 1ull))] = q;
-        __syncthreads();
-        if (tid == 0) {
-            int t = sBase;
-            for (int w = 0; w < 16; ++w) t += sW[w];
-            sBase = t;
+    for (int q0 = 0; q0 < a.mb; q0 += NT * 4) {
+        int st[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int q = q0 + u * NT + tid;
+            st[u] = q < a.mb ? a.status[q] : 0;
         }
-        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int q = q0 + u * NT + tid;
+            if (a.first && q < a.mb) rl.lvl[q] = 0;
+            const bool f = st[u] != 0;
+            const unsigned long long bal = __ballot(f);
+            if (lane == 0) sW[wave] = __popcll(bal);
+            __syncthreads();
+            int base = *sBase;
+            for (int v = 0; v < wave; ++v) base += sW[v];
+            if (f) rl.fail[base + __popcll(bal & ((1ull << lane) - 1ull))] = q;
+            __syncthreads();
+            if (tid == 0) {
+                int t = *sBase;
+                for (int v = 0; v < NW; ++v) t += sW[v];
+                *sBase = t;
+            }
+            __syncthreads();
+        }
     }
-    if (tid != 0) return;
-    const int nfail = sBase;
-    int64_t off = 0;
-    int n = 0;
-    for (int i = 0; i < nfail && n < rmax; ++i) {
+    const int nfail = *sBase;
+    const int nc = nfail < a.rmax ? nfail : a.rmax;
+    for (int i = tid; i < nc; i += NT) {
         const int q = rl.fail[i];
-        const int st = status[q];
+        const int stq = a.status[q];
         float bk = INFINITY;   // "no bound": every row with a finite key
         int bi = -1;
-        int need = all_rows;
-        int step = rl.lvl[q];
-        if (st & 1) {
-            bk = tkK[q];
-            bi = tiK[q];
-            need = total[q] > 1 ? total[q] : 1;
+        int need = a.all_rows;
+        int step = a.first ? 0 : rl.lvl[q];
+        if (stq & 1) {
+            bk = a.tau_k_key[q];
+            bi = a.tau_k_id[q];
+            need = a.total[q] > 1 ? a.total[q] : 1;
+        } else if (step == 0 && lad.j2_key) {
+            bk = lad.j2_key[q];
+            bi = lad.j2_id[q];
+            need = lad.cap_j2;
+            step = 1;
+        } else if (step <= 1 && lad.g_key) {
+            bk = lad.g_key[q];
+            bi = lad.g_id[q];
+            need = lad.cap_g;
+            step = 2;
         } else {
-            if (step == 0 && lad.j2_key) {
-                bk = lad.j2_key[q];
-                bi = lad.j2_id[q];
-                need = lad.cap_j2;
-                step = 1;
-            } else if (step <= 1 && lad.g_key) {
-                bk = lad.g_key[q];
-                bi = lad.g_id[q];
-                need = lad.cap_g;
-                step = 2;
-            } else {
-                step = 3;
-            }
+            step = 3;
         }
-        if (off + need > pool_entries) {
-            if (n == 0 && off == 0) continue;   // too large for this pool: a later round's larger pool
-            break;
-        }
-        rl.lvl[q] = (unsigned char)step;
-        rl.idx[n] = q;
-        rl.tk[n] = bk;
-        rl.ti[n] = bi;
-        rl.qoff[n] = off;
-        rl.qcap[n] = need;
-        rl.qcnt[(int64_t)n * kPoolCntStride] = 0;
-        off += need;
-        ++n;
+        w[2 * i] = ((uint64_t)(uint32_t)step << 32) | (uint32_t)need;
+        w[2 * i + 1] = ((uint64_t)__float_as_uint(bk) << 32) | (uint32_t)bi;
     }
-    rl.counters[0] = nfail;
-    rl.counters[1] = n;
-    rl.counters[2] = 0;
-}
-
-// rows idx[i] (i < *n) of src -> dst rows i; rows *n .. rows_pad zeroed; norms likewise
-__global__ void gather_rows_dev_kernel(const fx4* __restrict__ src, const float* __restrict__ qn,
-                                       const int* __restrict__ idx, const int* __restrict__ nptr, int rowP,
-                                       fx4* __restrict__ dst, float* __restrict__ dst_qn, int rows_pad) {
-    const int n = *nptr;
-    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (dst_qn && t < rows_pad) dst_qn[t] = t < n ? qn[idx[t]] : 0.0f;
-    const int64_t pieces = (int64_t)rows_pad * rowP;
-    for (int64_t i = t; i < pieces; i += (int64_t)gridDim.x * blockDim.x) {
+    __syncthreads();
+    if (tid == 0) {
+        int64_t off = 0;
+        int n = 0;
+        for (int i = 0; i < nc; ++i) {
+            const int need = (int)(uint32_t)w[2 * i];
+            if (off + need > a.pool_entries) {
+                if (n == 0 && off == 0) {   // too large for this pool: a later round's larger pool
+                    w[2 * i] = ~0ull;
+                    continue;
+                }
+                for (int j = i; j < nc; ++j) w[2 * j] = ~0ull;
+                break;
+            }
+            w[2 * i] = (w[2 * i] & 0xFF00000000ull) | ((uint64_t)n << 40) | (uint32_t)need;
+            rl.qoff[n] = off;
+            off += need;
+            ++n;
+        }
+        rl.counters[0] = nfail;
+        rl.counters[1] = n;
+        rl.counters[2] = 0;
+        *sN = n;
+    }
+    __syncthreads();
+    for (int i = tid; i < nc; i += NT) {
+        const uint64_t w0 = w[2 * i];
+        if (w0 == ~0ull) continue;
+        const int pos = (int)(w0 >> 40);
+        const int q = rl.fail[i];
+        rl.lvl[q] = (unsigned char)((w0 >> 32) & 0xFF);
+        rl.idx[pos] = q;
+        rl.tk[pos] = __uint_as_float((uint32_t)(w[2 * i + 1] >> 32));
+        rl.ti[pos] = (int)(uint32_t)w[2 * i + 1];
+        rl.qcap[pos] = (int)(uint32_t)w0;
+        rl.qcnt[(int64_t)pos * kPoolCntStride] = 0;
+    }
+    __syncthreads();
+    // gather: the scheduled queries' rows, then zeros to the end of the last
+    // live query block (its masked rows)
+    const int n = *sN;
+    const int rowP = a.row_bytes / 16;
+    int fill = (n + kBN - 1) / kBN * kBN;
+    if (fill > a.rows_pad) fill = a.rows_pad;
+    const fx4* src = (const fx4*)a.Q;
+    fx4* dst = (fx4*)a.dst_q;
+    for (int64_t i = tid; i < (int64_t)fill * rowP; i += NT) {
         const int r = (int)(i / rowP);
         const int c = (int)(i - (int64_t)r * rowP);
-        dst[i] = r < n ? src[(int64_t)idx[r] * rowP + c] : fx4{0.0f, 0.0f, 0.0f, 0.0f};
+        dst[i] = r < n ? src[(int64_t)rl.idx[r] * rowP + c] : fx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
+    for (int r = tid; r < fill; r += NT) a.dst_qn[r] = r < n ? a.qn[rl.idx[r]] : 0.0f;
+}
+
+__global__ void __launch_bounds__(1024) retry_plan_kernel(RetryPlanArgs a) {
+    __shared__ int sW[16];
+    __shared__ int sBase, sN;
+    __shared__ uint64_t w[2 * kRetryPlanMax];
+    retry_plan_block<1024>(a, sW, &sBase, &sN, w);
 }
 
 // "No bound": (+inf, -1) admits every finite key and rejects +inf and NaN,
@@ -2279,30 +2319,14 @@ void launch_gather_tau(const TauSources& src, const int* idx, const int* sel, in
     check_launch("gather_tau");
 }
 
-void launch_retry_plan(const int* status, int mb, int first, const float* tau_k_key, const int* tau_k_id,
-                       const int* total, const RetryLadder& ladder, int64_t pool_entries, int rmax, int all_rows,
-                       const RetryLists& rl, hipStream_t s) {
-    if (mb <= 0 || rmax <= 0) throw std::runtime_error("retry_plan: empty batch or window");
+void launch_retry_plan(const RetryPlanArgs& a, hipStream_t s) {
+    if (a.mb <= 0 || a.rmax <= 0 || a.rmax > kRetryPlanMax || a.rows_pad < a.rmax || a.row_bytes % 16 != 0)
+        throw std::runtime_error("retry_plan: bad sizes");
     void* tok;
     prof_begin(kFamPrep, s, &tok);
-    retry_plan_kernel<<<1, 1024, 0, s>>>(status, mb, first, tau_k_key, tau_k_id, total, ladder, pool_entries, rmax,
-                                         all_rows, rl);
+    retry_plan_kernel<<<1, 1024, 0, s>>>(a);
     prof_end(tok, s);
     check_launch("retry_plan");
-}
-
-void launch_gather_rows_dev(const void* src, const float* qn, const int* idx, const int* n, int row_bytes,
-                            void* dst, float* dst_qn, int rows_pad, hipStream_t s) {
-    if (rows_pad <= 0) return;
-    if (row_bytes % 16 != 0) throw std::runtime_error("gather_rows_dev: row bytes must be a multiple of 16");
-    const int rowP = row_bytes / 16;
-    const int64_t work = std::max<int64_t>((int64_t)rows_pad * rowP, rows_pad);
-    void* tok;
-    prof_begin(kFamPrep, s, &tok);
-    gather_rows_dev_kernel<<<grid_for(work, 256), 256, 0, s>>>((const fx4*)src, qn, idx, n, rowP, (fx4*)dst, dst_qn,
-                                                             rows_pad);
-    prof_end(tok, s);
-    check_launch("gather_rows_dev");
 }
 
 void launch_fill_tau_none(float* key, int* id, int n, hipStream_t s) {

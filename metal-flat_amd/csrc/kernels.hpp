@@ -56,6 +56,7 @@ constexpr size_t kResidentMaxLds = 68 * 1024;  // scan_resident: largest residen
 constexpr size_t kResidentMaxLdsNarrow = 144 * 1024;  // ... of a 32-query IVF tile (one workgroup a CU)
 constexpr int kRing = 192;                     // scan_resident: staged survivors per wave
 constexpr int kPoolCntStride = 32;             // ints between pooled-region counters (128 bytes)
+constexpr int kRetryPlanMax = 512;             // largest retry window (the plan's LDS: 2 words a query)
 constexpr int kStreamTopK = 32;                // streaming top-k scan: k up to this ...
 constexpr int kStreamMaxQ = 16;                // ... for batches up to this many queries
 
@@ -132,6 +133,59 @@ struct ScanParams {
     const int* qcap;
 };
 
+// Device-built retry work lists (flat search). After a full pass's select, a
+// query whose status is nonzero is retried; retry_plan decides each one's
+// bound and pooled region (one per query, cand[qoff .. qoff + qcap)):
+//   overflow (bit 0): the k-th best it stored, capacity = the unclamped count
+//       it saw under the looser bound (total): the rerun cannot overflow, so
+//       it is final;
+//   too few (bit 1): the next looser bound of its ladder (the sample's j2-th,
+//       then its guaranteed k-th, then none), capacity estimated for it.
+// Queries are taken in ascending order while they fit rmax and the pool; the
+// rest wait for the next round. All counts stay on the device.
+struct RetryLists {
+    int* fail;         // [mb] scratch: failing queries in ascending order
+    unsigned char* lvl;   // [mb] ladder step each query has taken
+    int* idx;          // [rmax] queries scheduled this round (original row)
+    float* tk;         // [rmax] their bounds
+    int* ti;
+    int64_t* qoff;     // [rmax] pooled regions
+    int* qcap;
+    int* qcnt;         // [rmax * kPoolCntStride] slot counters, 128 bytes apart (cleared by the plan)
+    int* counters;     // [4]: failing queries, scheduled, failed again (the select adds), spare
+};
+struct RetryLadder {   // per-query bounds of the "too few" ladder (nullable entries are skipped)
+    const float* j2_key;
+    const int* j2_id;
+    const float* g_key;
+    const int* g_id;
+    int cap_j2, cap_g;   // pooled capacities estimated for those bounds
+};
+
+// One retry round's plan and gather (see RetryLists), run by one block
+// (launch_retry_plan). Scheduled queries' rows of Q (row_bytes each) and norms
+// go to dst_q / dst_qn, rows past them up to the end of their query block
+// zeroed.
+struct RetryPlanArgs {
+    const int* status;
+    int mb;
+    int first;                 // 1: every query's ladder step starts at 0
+    const float* tau_k_key;
+    const int* tau_k_id;
+    const int* total;
+    RetryLadder ladder;
+    int64_t pool_entries;
+    int rmax;
+    int all_rows;
+    RetryLists lists;
+    const void* Q;
+    const float* qn;
+    int row_bytes;
+    void* dst_q;
+    float* dst_qn;
+    int rows_pad;
+};
+
 struct SelectParams {
     const uint2* cand;
     const int* cnt;
@@ -161,35 +215,6 @@ struct SelectParams {
     const int* qcap;         //   capacity qcap[i], count cnt[i * kPoolCntStride]
     int* total;              // nullable: unclamped candidates seen by each query (sum of its counts)
     int* fail_count;         // nullable: incremented once per query whose status is nonzero
-};
-
-// Device-built retry work lists (flat search). After a full pass's select, a
-// query whose status is nonzero is retried; retry_plan decides each one's
-// bound and pooled region (one per query, cand[qoff .. qoff + qcap)):
-//   overflow (bit 0): the k-th best it stored, capacity = the unclamped count
-//       it saw under the looser bound (total): the rerun cannot overflow, so
-//       it is final;
-//   too few (bit 1): the next looser bound of its ladder (the sample's j2-th,
-//       then its guaranteed k-th, then none), capacity estimated for it.
-// Queries are taken in ascending order while they fit rmax and the pool; the
-// rest wait for the next round. All counts stay on the device.
-struct RetryLists {
-    int* fail;         // [mb] scratch: failing queries in ascending order
-    unsigned char* lvl;   // [mb] ladder step each query has taken
-    int* idx;          // [rmax] queries scheduled this round (original row)
-    float* tk;         // [rmax] their bounds
-    int* ti;
-    int64_t* qoff;     // [rmax] pooled regions
-    int* qcap;
-    int* qcnt;         // [rmax * kPoolCntStride] slot counters, 128 bytes apart (cleared by the plan)
-    int* counters;     // [4]: failing queries, scheduled, failed again (the select adds), spare
-};
-struct RetryLadder {   // per-query bounds of the "too few" ladder (nullable entries are skipped)
-    const float* j2_key;
-    const int* j2_id;
-    const float* g_key;
-    const int* g_id;
-    int cap_j2, cap_g;   // pooled capacities estimated for those bounds
 };
 
 // Launchers (kernels.hip). All are asynchronous on `s` and bracket the launch
@@ -263,14 +288,8 @@ void launch_select(const SelectParams& p, hipStream_t s);
 // wants to be the number of workgroups resident at once (topk_concurrency).
 void launch_scan_topk(const ScanParams& p, int metric, int storage, hipStream_t s);
 int topk_concurrency(int dpad, int storage, int metric);
-// One retry round's plan (one block): see RetryLists. first = 1 on the first
-// round of a batch (every query's ladder step starts at 0).
-void launch_retry_plan(const int* status, int mb, int first, const float* tau_k_key, const int* tau_k_id,
-                       const int* total, const RetryLadder& ladder, int64_t pool_entries, int rmax, int all_rows,
-                       const RetryLists& rl, hipStream_t s);
-// rows idx[i] (i < *n) of src (row_bytes each) -> dst rows i, rows *n .. rows_pad zeroed; norms likewise
-void launch_gather_rows_dev(const void* src, const float* qn, const int* idx, const int* n, int row_bytes,
-                            void* dst, float* dst_qn, int rows_pad, hipStream_t s);
+// One retry round's plan and gather in one block (RetryPlanArgs).
+void launch_retry_plan(const RetryPlanArgs& a, hipStream_t s);
 void launch_argmin_finalize(const unsigned long long* best, int nq, int metric, int32_t* ids, float* vals,
                             hipStream_t s);
 void launch_fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hipStream_t s);
