@@ -9,8 +9,8 @@
 // entry is grouped with the other entries of its cell, and each run of up to
 // 128 entries of one cell is one work item of the scan.
 #include "ivf_kernels.hpp"
+#include "primitives.hpp"
 
-#include <hipcub/hipcub.hpp>
 
 #include <algorithm>
 #include <stdexcept>
@@ -422,10 +422,7 @@ void IvfWorkTable::build(const int* probe, int m, int np, int ranks, int nlist, 
             for (int** p : {&hist, &histOff}) check(hipMalloc((void**)p, (size_t)nh * sizeof(int)), "hipMalloc(hist)");
             capHist = nh;
         }
-        size_t need = 0;
-        check(hipcub::DeviceScan::ExclusiveSum(nullptr, need, (const int*)hist, histOff, (int)nh, s),
-              "ExclusiveSum (size)");
-        need = std::max(need, (size_t)16);
+        const size_t need = std::max(scan_temp_bytes(nh), (size_t)16);
         if (need > tempBytes) {
             if (temp) (void)hipFree(temp);
             temp = nullptr;
@@ -444,8 +441,7 @@ void IvfWorkTable::build(const int* probe, int m, int np, int ranks, int nlist, 
         prof_begin(kFamPrep, s, &tok);
         ivf_hist_kernel<<<G, kHistBlock, lds, s>>>(probe, m, np, ranks, nlist, pos, posLimit, chunk, G, hist);
         check(hipGetLastError(), "ivf_hist");
-        size_t t = tempBytes;
-        check(hipcub::DeviceScan::ExclusiveSum(temp, t, (const int*)hist, histOff, (int)nh, s), "ExclusiveSum");
+        launch_scan_i32(hist, histOff, nh, false, temp, s);
         ivf_scatter_kernel<<<G, kHistBlock, lds, s>>>(probe, m, np, ranks, nlist, pos, posLimit, chunk, G, hist,
                                                       histOff, ent, eStart, eEnd);
         check(hipGetLastError(), "ivf_scatter");
@@ -460,12 +456,7 @@ void IvfWorkTable::build(const int* probe, int m, int np, int ranks, int nlist, 
 
     int bits = 1;
     while ((1 << bits) <= nlist) ++bits;   // keys 0 .. nlist
-    size_t needSort = 0, needIn = 0;
-    check(hipcub::DeviceRadixSort::SortPairs(nullptr, needSort, (const int*)keysIn, keysOut, (const int*)valsIn,
-                                             ent, ne, 0, bits, s),
-          "SortPairs (size)");
-    check(hipcub::DeviceScan::InclusiveSum(nullptr, needIn, (const int*)tiles, tEnd, nlist, s), "InclusiveSum (size)");
-    const size_t need = std::max({needSort, needIn, (size_t)16});
+    const size_t need = std::max({radix_sort_temp_bytes(ne, bits), scan_temp_bytes(nlist), (size_t)16});
     if (need > tempBytes) {
         if (temp) (void)hipFree(temp);
         temp = nullptr;
@@ -480,19 +471,14 @@ void IvfWorkTable::build(const int* probe, int m, int np, int ranks, int nlist, 
     ivf_entries_kernel<<<(int)((ne + 255) / 256), 256, 0, s>>>(probe, m, np, ranks, nlist, pos, posLimit, keysIn,
                                                                 valsIn);
     check(hipGetLastError(), "ivf_entries");
-    size_t t = tempBytes;
-    check(hipcub::DeviceRadixSort::SortPairs(temp, t, (const int*)keysIn, keysOut, (const int*)valsIn, ent, ne, 0,
-                                             bits, s),
-          "SortPairs");
+    launch_radix_sort_pairs(keysIn, keysOut, valsIn, ent, ne, bits, temp, s);
     ivf_runs_kernel<<<(ne + 255) / 256, 256, 0, s>>>(keysOut, ne, nlist, eStart, eEnd);
     check(hipGetLastError(), "ivf_runs");
     ivf_tiles_kernel<<<(nlist + 255) / 256, 256, 0, s>>>(cellOrder, eStart, eEnd, nlist, wideW, narrowMax, tiles,
                                                           tilesN);
     check(hipGetLastError(), "ivf_tiles");
-    t = tempBytes;
-    check(hipcub::DeviceScan::InclusiveSum(temp, t, (const int*)tiles, tEnd, nlist, s), "InclusiveSum");
-    t = tempBytes;
-    check(hipcub::DeviceScan::InclusiveSum(temp, t, (const int*)tilesN, tEndN, nlist, s), "InclusiveSum");
+    launch_scan_i32(tiles, tEnd, nlist, true, temp, s);
+    launch_scan_i32(tilesN, tEndN, nlist, true, temp, s);
     ivf_work_kernel<<<(nlist + 3) / 4, 256, 0, s>>>(cellOrder, eEnd, eStart, tEnd, tEndN, nlist, wideW, narrowMax,
                                                      work, workN, nwork);
     check(hipGetLastError(), "ivf_work");

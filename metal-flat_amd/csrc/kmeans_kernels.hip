@@ -2,7 +2,7 @@
 // kmeans_kernels.hip -- device side of the k-means training loop (the
 // centroid update after the fused k = 1 assignment).
 //
-//   group_by_cell     stable radix sort of (cell, point) pairs (hipCUB), so the
+//   group_by_cell     stable radix sort of (cell, point) pairs (primitives.hip), so the
 //                     points of every cell come out in ascending point order
 //   cell_counts       points per cell
 //   gather_points     training subsample rows
@@ -13,8 +13,8 @@
 //                     assignment yields bit-identical centroids; an empty cell
 //                     takes a copy of its reseed row (:63-66)
 #include "kmeans_kernels.hpp"
+#include "primitives.hpp"
 
-#include <hipcub/hipcub.hpp>
 
 #include <stdexcept>
 #include <string>
@@ -100,10 +100,7 @@ void CellGrouping::group(const int* cell, int n, int nlist, int* orderOut, int* 
     }
     int bits = 1;
     while ((1 << bits) < nlist) ++bits;
-    size_t need = 0;
-    check(hipcub::DeviceRadixSort::SortPairs(nullptr, need, cell, (int*)keysOut, (const int*)iota, orderOut, n,
-                                             0, bits, s),
-          "SortPairs (size)");
+    const size_t need = radix_sort_temp_bytes(n, bits);
     if (need > tempBytes) {
         if (temp) (void)hipFree(temp);
         temp = nullptr;
@@ -112,9 +109,7 @@ void CellGrouping::group(const int* cell, int n, int nlist, int* orderOut, int* 
     }
     iota_kernel<<<(n + 255) / 256, 256, 0, s>>>((int*)iota, n);
     check(hipGetLastError(), "iota");
-    check(hipcub::DeviceRadixSort::SortPairs(temp, need, cell, (int*)keysOut, (const int*)iota, orderOut, n, 0,
-                                             bits, s),
-          "SortPairs");
+    launch_radix_sort_pairs(cell, (int*)keysOut, (const int*)iota, orderOut, n, bits, temp, s);
     check(hipMemsetAsync(countsOut, 0, (size_t)nlist * sizeof(int), s), "hipMemsetAsync(counts)");
     cell_counts_kernel<<<(n + 255) / 256, 256, 0, s>>>(cell, n, countsOut);
     check(hipGetLastError(), "cell_counts");

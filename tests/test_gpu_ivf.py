@@ -175,6 +175,17 @@ def test_retries_exact_with_tiny_regions(gpu_ok, monkeypatch):
     monkeypatch.delenv("MFLAT_IVF_CAP_B")
 
 
+def test_many_cells_radix_path(gpu_ok):
+    """More than 32,768 cells: the work tables group entries with the radix
+    sort and scans of primitives.hip instead of the per-block LDS histograms
+    (and k-means groups its points with the same sort). Integer data: exact."""
+    xi, qi = int_case(120_000, 300, 16, 6, seed=27)
+    with build(xi, 40_000) as idx:
+        assert mflat.load().mflat_ivf_nlist(idx.handle) == 40_000
+        check(idx, xi, qi, 10, 64, L2, exact=True)
+        check(idx, xi, qi, 50, 300, L2, exact=True)
+
+
 @pytest.mark.parametrize("storage", [mflat.MFLAT_STORAGE_F16, mflat.MFLAT_STORAGE_BF16])
 def test_reduced_precision_storage(gpu_ok, storage):
     x, q = datagen.gmm(nb=40_000, nq=600, d=128, ncenters=128, seed=21)
