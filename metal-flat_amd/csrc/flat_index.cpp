@@ -269,6 +269,9 @@ struct FlatIndex::Impl {
     // fp32, 0.363 / 0.372 ms fp16).
     int streamMaxQ = 1;
     int streamSplits = 0;
+    // MFLAT_QGROUP = n: query blocks co-scheduled per XCD by the MFMA scans
+    // (0: each kernel's default).
+    int qgroupKnob = 0;
 
     int kernMetric() const { return metric == Metric::L2 ? 0 : 1; }
     float emptyValue() const { return metric == Metric::L2 ? INFINITY : -INFINITY; }
@@ -576,6 +579,7 @@ struct FlatIndex::Impl {
         p.Q = Q; p.qnorm = qn; p.nq = nq; p.nqb = (nq + kBN - 1) / kBN; p.dpad = dpad;
         p.tau_key = tk; p.tau_id = ti;
         p.cand = cand.as<uint2>(); p.cnt = cnt.as<int>(); p.cap = cap;
+        p.qgroup = qgroupKnob;
         return p;
     }
 
@@ -964,6 +968,7 @@ FlatIndex::FlatIndex(int dim, Metric metric, Storage storage) : d_(new Impl) {
     if (const char* v = std::getenv("MFLAT_RETRY_POOL")) d_->retryPool = std::max<long long>(0, std::atoll(v));
     if (const char* v = std::getenv("MFLAT_STREAM_MAXQ")) d_->streamMaxQ = std::max(0, std::atoi(v));
     if (const char* v = std::getenv("MFLAT_STREAM_SPLITS")) d_->streamSplits = std::max(0, std::atoi(v));
+    if (const char* v = std::getenv("MFLAT_QGROUP")) d_->qgroupKnob = std::max(0, std::atoi(v));
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
         (void)hipGetLastError();

@@ -665,7 +665,8 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
         } else {
             const int full = (nwg / 8) * 8;
             const int v = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
-            const int grpSize = p.nqb < kQGroup ? p.nqb : kQGroup;
+            const int qgrp = p.qgroup > 0 ? p.qgroup : kQGroup;
+            const int grpSize = p.nqb < qgrp ? p.nqb : qgrp;
             const int grp = v / (grpSize * p.nsplit);
             const int r = v - grp * grpSize * p.nsplit;
             const int inGrp = p.nqb - grp * grpSize < grpSize ? p.nqb - grp * grpSize : grpSize;
@@ -1048,7 +1049,8 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
         } else {
             const int full = (nwg / 8) * 8;
             const int v = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
-            const int grpSize = p.nqb < kQGroup ? p.nqb : kQGroup;
+            const int qgrp = p.qgroup > 0 ? p.qgroup : kQGroup;
+            const int grpSize = p.nqb < qgrp ? p.nqb : qgrp;
             const int grp = v / (grpSize * p.nsplit);
             const int r = v - grp * grpSize * p.nsplit;
             const int inGrp = p.nqb - grp * grpSize < grpSize ? p.nqb - grp * grpSize : grpSize;
@@ -2647,9 +2649,17 @@ void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, 
         check_launch("scan_resident");
         return;
     }
-    if (storage == kF32) launch_tiled_s<kF32>(p, metric, pass, g, s);
-    else if (storage == kF16) launch_tiled_s<kF16>(p, metric, pass, g, s);
-    else launch_tiled_s<kBF16>(p, metric, pass, g, s);
+    // LDS-tiled kernel: every database tile re-reads the group's query tiles
+    // through L2, so the group is as many query blocks as ~2.5 MB of query
+    // tiles (the XCD's L2 is 4 MB and also streams the database tiles).
+    ScanParams pt = p;
+    if (pt.qgroup <= 0) {
+        const int64_t tileBytes = (int64_t)kBN * p.dpad * elem_bytes(storage);
+        pt.qgroup = (int)std::max<int64_t>(1, std::min<int64_t>(kQGroup, ((int64_t)5 << 19) / tileBytes));
+    }
+    if (storage == kF32) launch_tiled_s<kF32>(pt, metric, pass, g, s);
+    else if (storage == kF16) launch_tiled_s<kF16>(pt, metric, pass, g, s);
+    else launch_tiled_s<kBF16>(pt, metric, pass, g, s);
     prof_end(tok, s);
     check_launch("scan_filter");
 }

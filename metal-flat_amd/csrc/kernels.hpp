@@ -103,6 +103,7 @@ struct ScanParams {
     const float* qnorm;      // per-query ||q||^2 (L2 only)
     int nq;                  // valid queries
     int nqb;                 // query blocks of kBN
+    int qgroup;              // query blocks co-scheduled per XCD (0: the launcher's choice for the kernel)
     int dpad;                // padded dimension, multiple of kBK
     const float* tau_key;    // per-query threshold key
     const int* tau_id;       // per-query threshold id (lexicographic bound)
