@@ -296,7 +296,7 @@ struct FlatIndex::Impl {
         const int64_t ntiles = std::max<int64_t>(1, (nb + kBM - 1) / kBM);
         int64_t want = streamSplits > 0 ? streamSplits : topkConcurrency();
         if (want <= 0) want = 1024;
-        want = std::min<int64_t>({want, std::max<int64_t>(256, kSelLdsLarge / k), ntiles, kSelLargeMaxSplit});
+        want = std::min<int64_t>({want, ntiles, kMergeMaxSplit});
         const int64_t tps = (ntiles + want - 1) / want;
         pl.nsplit1 = (int)((ntiles + tps - 1) / tps);
         pl.rps1 = tps * kBM;
@@ -636,8 +636,7 @@ struct FlatIndex::Impl {
             launch_scan_topk(p, kernMetric(), storage, s);
             SelectParams sp = selectParams(mb, pl.nsplit1, k, k, 1);
             sp.out_ids = oIds; sp.out_vals = oVals;
-            sp.expect = pl.nsplit1 * k;
-            launch_select(sp, s);
+            launch_merge_lists(sp, s);
             return;
         }
         // tauS holds "no bound" from the query preparation
@@ -903,8 +902,7 @@ struct FlatIndex::Impl {
         sp.cand = cd; sp.cnt = cn; sp.nsplit = pl.nsplit1; sp.cap = k; sp.nq = m; sp.k = k; sp.j = 1; sp.j2 = 1;
         sp.metric = kernMetric();
         sp.out_ids = ids; sp.out_vals = vals; sp.out_stride = k;
-        sp.expect = pl.nsplit1 * k;
-        launch_select(sp, s);
+        launch_merge_lists(sp, s);
         return k;
     }
 

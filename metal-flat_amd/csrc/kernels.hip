@@ -141,7 +141,7 @@ __global__ void row_norms_kernel(const void* __restrict__ v, int64_t n, int dpad
     out[r] = (float)s;
 }
 
-// One search batch's queries in one launch, a thread per row (rows < n_pad):
+// One search batch's queries in one launch, a wave per row (rows < n_pad):
 // the caller's fp32 row (dim values) -> the zero-padded row of dpad elements
 // in the storage type; Cosine first scales it by float(1 / sqrt(s)), s the
 // sequential double sum of its squares (zero rows unchanged: the reference's
@@ -149,48 +149,81 @@ __global__ void row_norms_kernel(const void* __restrict__ v, int64_t n, int dpad
 // sum of the stored values' squares (rowSqNorms, src/Distance.h:40-47); the
 // row's bound set to "no bound" (+inf, -1) when tau_key is given. Rows
 // n .. n_pad are zero.
+// The row goes in chunks of 64 pieces (16 bytes of output each, one a lane,
+// coalesced); each chunk's values are staged in LDS, where lane 0 adds their
+// squares in column order, so both sums keep the sequential order.
 template <int S>
-__global__ void prep_queries_kernel(const float* __restrict__ src, int64_t n, int dim, int64_t n_pad, int dpad,
-                                    int cosine, void* __restrict__ out, float* __restrict__ qn,
-                                    float* __restrict__ tau_key, int* __restrict__ tau_id) {
-    const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (r >= n_pad) return;
+__global__ void __launch_bounds__(256) prep_queries_kernel(const float* __restrict__ src, int64_t n, int dim,
+                                                           int64_t n_pad, int dpad, int cosine,
+                                                           void* __restrict__ out, float* __restrict__ qn,
+                                                           float* __restrict__ tau_key, int* __restrict__ tau_id) {
     constexpr int PE = piece_elems<S>();
+    __shared__ float sRow[4][64 * PE];
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int64_t r = blockIdx.x * (int64_t)4 + wave;
+    if (r >= n_pad) return;
     fx4* dst = (fx4*)out + r * (dpad / PE);
     const bool live = r < n;
     const float* row = src + r * dim;
+    float* st = sRow[wave];
+    const int npc = dpad / PE;
+
+    // lane 0 adds the squares of the chunk staged in st (cols values)
+    auto addChunk = [&](double acc, int cols) {
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0)
+            for (int c = 0; c < cols; ++c) acc += (double)st[c] * st[c];
+        __builtin_amdgcn_wave_barrier();
+        return acc;
+    };
+
     float inv = 1.0f;
     if (live && cosine) {
         double s = 0.0;
-        for (int c = 0; c < dim; ++c) s += (double)row[c] * row[c];
-        if (s > 0.0) inv = (float)(1.0 / sqrt(s));
+        for (int u0 = 0; u0 < npc; u0 += 64) {
+            const int c0 = (u0 + lane) * PE;
+#pragma unroll
+            for (int e = 0; e < PE; ++e) st[lane * PE + e] = c0 + e < dim ? row[c0 + e] : 0.0f;
+            const int cols = min(64 * PE, dim - u0 * PE);
+            if (cols > 0) s = addChunk(s, cols);
+        }
+        if (lane == 0 && s > 0.0) inv = (float)(1.0 / sqrt(s));
+        inv = __shfl(inv, 0);
     }
     double nrm = 0.0;
-    for (int u = 0; u < dpad / PE; ++u) {
+    for (int u0 = 0; u0 < npc; u0 += 64) {
+        const int u = u0 + lane;
         float v[PE];
 #pragma unroll
         for (int e = 0; e < PE; ++e) {
             const int c = u * PE + e;
-            float x = (live && c < dim) ? row[c] : 0.0f;
+            float x = (live && u < npc && c < dim) ? row[c] : 0.0f;
             if (cosine) x *= inv;
             if constexpr (S != kF32) x = from_bits<S>(to_bits<S>(x));
             v[e] = x;
-            nrm += (double)x * x;
+            st[lane * PE + e] = x;
         }
-        fx4 piece;
-        if constexpr (S == kF32) {
-            piece = fx4{v[0], v[1], v[2], v[3]};
-        } else {
+        if (u < npc) {
+            fx4 piece;
+            if constexpr (S == kF32) {
+                piece = fx4{v[0], v[1], v[2], v[3]};
+            } else {
 #pragma unroll
-            for (int w = 0; w < 4; ++w)
-                piece[w] = __uint_as_float((uint32_t)to_bits<S>(v[2 * w]) | ((uint32_t)to_bits<S>(v[2 * w + 1]) << 16));
+                for (int w = 0; w < 4; ++w)
+                    piece[w] = __uint_as_float((uint32_t)to_bits<S>(v[2 * w]) | ((uint32_t)to_bits<S>(v[2 * w + 1]) << 16));
+            }
+            dst[u] = piece;
         }
-        dst[u] = piece;
+        const int cols = min(64 * PE, dim - u0 * PE);
+        if (live && cols > 0) nrm = addChunk(nrm, cols);
     }
-    qn[r] = live ? (float)nrm : 0.0f;
-    if (tau_key && live) {
-        tau_key[r] = INFINITY;
-        tau_id[r] = -1;
+    if (lane == 0) {
+        qn[r] = (float)nrm;
+        if (tau_key && live) {
+            tau_key[r] = INFINITY;
+            tau_id[r] = -1;
+        }
     }
 }
 
@@ -2184,13 +2217,13 @@ void launch_prep_queries(const float* src, int64_t n, int dim, int64_t n_pad, in
     if (dpad % 8 != 0) throw std::runtime_error("prep_queries: dpad must be a multiple of 8");
     void* tok;
     prof_begin(kFamPrep, s, &tok);
-    const int g = (int)((n_pad + 63) / 64);
+    const int g = (int)((n_pad + 3) / 4);   // a wave per row
     if (storage == kF32)
-        prep_queries_kernel<kF32><<<g, 64, 0, s>>>(src, n, dim, n_pad, dpad, cosine ? 1 : 0, out, qn, tau_key, tau_id);
+        prep_queries_kernel<kF32><<<g, 256, 0, s>>>(src, n, dim, n_pad, dpad, cosine ? 1 : 0, out, qn, tau_key, tau_id);
     else if (storage == kF16)
-        prep_queries_kernel<kF16><<<g, 64, 0, s>>>(src, n, dim, n_pad, dpad, cosine ? 1 : 0, out, qn, tau_key, tau_id);
+        prep_queries_kernel<kF16><<<g, 256, 0, s>>>(src, n, dim, n_pad, dpad, cosine ? 1 : 0, out, qn, tau_key, tau_id);
     else if (storage == kBF16)
-        prep_queries_kernel<kBF16><<<g, 64, 0, s>>>(src, n, dim, n_pad, dpad, cosine ? 1 : 0, out, qn, tau_key, tau_id);
+        prep_queries_kernel<kBF16><<<g, 256, 0, s>>>(src, n, dim, n_pad, dpad, cosine ? 1 : 0, out, qn, tau_key, tau_id);
     else
         throw std::runtime_error("prep_queries: unknown storage type");
     prof_end(tok, s);
@@ -2728,6 +2761,124 @@ static void launch_select_kt(const SelectParams& p, size_t dyn, hipStream_t s) {
         select_kernel<kSelLdsLarge, KT><<<p.nq, 256, dyn, s>>>(p);
     else
         select_kernel<kSelLds, KT><<<p.nq, 256, dyn, s>>>(p);
+}
+
+// ---------------------------------------------------------------------------
+// merge_lists: exact top-k of the streaming scan's per-split lists
+// ---------------------------------------------------------------------------
+//
+// One workgroup per query; region (q, s) holds cnt[q, s] <= cap <=
+// kStreamTopK composites in ascending order (the streaming scan's per-split
+// top-k). A k-way merge in two levels: lane s holds region s in registers;
+// each wave takes k rounds of "smallest head of its 64 lanes" (composites are
+// distinct: a row is in one split, so exactly one lane owns the minimum and
+// shifts its list), leaving the wave's ascending top-k in LDS; wave 0 then
+// merges the 16 wave lists the same way into the query's output.
+constexpr int kMergeThreads = kMergeMaxSplit;   // a list per thread
+
+// Minimum of x over the wave: DPP steps within each 16-lane row (swap
+// neighbours, swap pairs, reverse 8, reverse 16), then the four rows' results
+// read from lanes 0, 16, 32, 48.
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_min_step(uint64_t x) {
+    const uint32_t lo = (uint32_t)x, hi = (uint32_t)(x >> 32);
+    const uint32_t lo2 = (uint32_t)__builtin_amdgcn_update_dpp((int)lo, (int)lo, CTRL, 0xf, 0xf, false);
+    const uint32_t hi2 = (uint32_t)__builtin_amdgcn_update_dpp((int)hi, (int)hi, CTRL, 0xf, 0xf, false);
+    const uint64_t y = ((uint64_t)hi2 << 32) | lo2;
+    return y < x ? y : x;
+}
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t x) {
+    x = dpp_min_step<0xB1>(x);    // quad_perm [1, 0, 3, 2]
+    x = dpp_min_step<0x4E>(x);    // quad_perm [2, 3, 0, 1]
+    x = dpp_min_step<0x141>(x);   // row_half_mirror
+    x = dpp_min_step<0x140>(x);   // row_mirror
+    uint64_t m = ~0ull;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint64_t y = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), 16 * r) << 32) |
+                           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, 16 * r);
+        m = y < m ? y : m;
+    }
+    return m;
+}
+
+// k rounds over the lanes' ascending lists v (KT entries, ~0 past the end):
+// round r's minimum goes to emit(r, m); stops early once every list is empty.
+template <int KT, class Emit>
+__device__ __forceinline__ void wave_merge(uint64_t (&v)[KT], int k, Emit&& emit) {
+    for (int r = 0; r < k; ++r) {
+        const uint64_t m = wave_min_u64(v[0]);
+        if (m == ~0ull) return;
+        if (v[0] == m) {   // this lane's head: shift its list
+#pragma unroll
+            for (int e = 0; e + 1 < KT; ++e) v[e] = v[e + 1];
+            v[KT - 1] = ~0ull;
+        }
+        emit(r, m);
+    }
+}
+
+// KT: entries a lane holds (cap <= KT): 16 for k <= 16, else kStreamTopK.
+template <int KT>
+__global__ void __launch_bounds__(kMergeThreads) merge_lists_kernel(SelectParams p) {
+    constexpr int NW = kMergeThreads / 64;
+    __shared__ uint64_t sWave[NW][KT];
+
+    const int q = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int k = p.k;
+
+    uint64_t v[KT];
+    {
+        int c = 0;
+        const uint2* reg = p.cand + ((int64_t)q * p.nsplit + tid) * p.cap;
+        if (tid < p.nsplit) {
+            c = p.cnt[(int64_t)q * p.nsplit + tid];
+            c = c < p.cap ? c : p.cap;
+        }
+#pragma unroll
+        for (int e = 0; e < KT; ++e) v[e] = e < c ? composite(reg[e]) : ~0ull;
+    }
+#pragma unroll
+    for (int e = 0; e < KT; ++e) sWave[wave][e] = ~0ull;   // lane-uniform stores: same value
+    wave_merge(v, k, [&](int r, uint64_t m) {
+        if (lane == 0) sWave[wave][r] = m;
+    });
+    __syncthreads();
+    if (wave != 0) return;
+
+    uint64_t w[KT];
+#pragma unroll
+    for (int e = 0; e < KT; ++e) w[e] = lane < NW ? sWave[lane][e] : ~0ull;
+    const int orow = p.qmap ? p.qmap[q] : q;
+    int got = 0;
+    wave_merge(w, k, [&](int r, uint64_t m) {
+        got = r + 1;
+        if (lane == 0) {
+            const float key = ord_to_key((uint32_t)(m >> 32));
+            if (p.out_ids) p.out_ids[(int64_t)orow * p.out_stride + r] = (int32_t)(uint32_t)(m & 0xFFFFFFFFu);
+            if (p.out_vals) p.out_vals[(int64_t)orow * p.out_stride + r] = p.metric == 0 ? key : -key;
+        }
+    });
+    // fewer than k rows in the whole database: padding
+    for (int i = got + lane; i < k; i += 64) {
+        if (p.out_ids) p.out_ids[(int64_t)orow * p.out_stride + i] = -1;
+        if (p.out_vals) p.out_vals[(int64_t)orow * p.out_stride + i] = p.metric == 0 ? INFINITY : -INFINITY;
+    }
+}
+
+void launch_merge_lists(const SelectParams& p, hipStream_t s) {
+    if (p.nq <= 0) return;
+    if (p.k < 1 || p.k > p.cap || p.cap > kStreamTopK || p.nsplit < 1 || p.nsplit > kMergeThreads)
+        throw std::runtime_error("merge_lists: bad k/cap/nsplit");
+    void* tok;
+    prof_begin(kFamSelect, s, &tok);
+    if (p.cap <= 16) merge_lists_kernel<16><<<p.nq, kMergeThreads, 0, s>>>(p);
+    else merge_lists_kernel<kStreamTopK><<<p.nq, kMergeThreads, 0, s>>>(p);
+    prof_end(tok, s);
+    check_launch("merge_lists");
 }
 
 void launch_select(const SelectParams& p, hipStream_t s) {

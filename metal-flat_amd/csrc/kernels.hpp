@@ -57,6 +57,7 @@ constexpr size_t kResidentMaxLdsNarrow = 144 * 1024;  // ... of a 32-query IVF t
 constexpr int kRing = 192;                     // scan_resident: staged survivors per wave
 constexpr int kPoolCntStride = 32;             // ints between pooled-region counters (128 bytes)
 constexpr int kRetryPlanMax = 512;             // largest retry window (the plan's LDS: 2 words a query)
+constexpr int kMergeMaxSplit = 1024;   // lists merge_lists takes (one per thread)
 constexpr int kStreamTopK = 32;                // streaming top-k scan: k up to this ...
 constexpr int kStreamMaxQ = 16;                // ... for batches up to this many queries
 
@@ -289,6 +290,12 @@ void launch_select(const SelectParams& p, hipStream_t s);
 // wants to be the number of workgroups resident at once (topk_concurrency).
 void launch_scan_topk(const ScanParams& p, int metric, int storage, hipStream_t s);
 int topk_concurrency(int dpad, int storage, int metric);
+// The streaming scan's exact top-k per query from its ascending per-split
+// lists (cand / cnt / nsplit <= kMergeMaxSplit / cap of launch_scan_topk;
+// k <= cap; out_ids / out_vals / out_stride / metric / qmap as for
+// launch_select). Rows missing when the database holds fewer than k: id -1
+// and the empty value.
+void launch_merge_lists(const SelectParams& p, hipStream_t s);
 // One retry round's plan and gather in one block (RetryPlanArgs).
 void launch_retry_plan(const RetryPlanArgs& a, hipStream_t s);
 void launch_argmin_finalize(const unsigned long long* best, int nq, int metric, int32_t* ids, float* vals,

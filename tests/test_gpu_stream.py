@@ -107,3 +107,21 @@ def test_rank_follows_row_order(gpu_ok):
     gi, gd = run(x, q, 32, L2)
     oi, od = oracle.flat_search(x, q, 32, threads=oracle_threads())
     parity.exact(gi, gd, oi, od)
+
+
+@pytest.mark.parametrize("nq,k", [(1, 32), (3, 20)])
+def test_merge_many_close_rows(gpu_ok, nq, k):
+    """Every split holds fewer than k rows at distance 0 (one every 500 rows)
+    and there are thousands of them: the per-split lists' k-th entries bound
+    nothing useful, so the merge takes its radix descent to the exact k-th."""
+    rng = np.random.default_rng(65 + nq)
+    nb = 2_000_000
+    q = rng.integers(0, 4, size=(nq, 16)).astype(np.float32)
+    x = rng.integers(0, 4, size=(nb, 16)).astype(np.float32)
+    for i in range(nq):
+        x[i::500] = q[i]   # distance 0 for query i, one row in 500 (by query)
+    print(f"[stream] close rows nq={nq} k={k}", flush=True)
+    gi, gd = run(x, q, k, L2)
+    oi, od = oracle.flat_search(x, q, k, threads=oracle_threads())
+    parity.exact(gi, gd, oi, od)
+    assert np.all(gd[:, :k] == 0.0)
