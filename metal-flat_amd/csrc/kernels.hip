@@ -1471,6 +1471,10 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
     // | id); the list's k-th is the wave's bound for that query.
     __shared__ uint64_t sList[KT > 0 ? 4 * 16 * KT : 1];
     __shared__ int sLen[KT > 0 ? 4 * 16 : 1];
+    // ... and the workgroup's best bound per query: the smallest k-th entry of
+    // a full wave list (k rows at or below it exist, so no row above it is a
+    // result); every wave filters with it once it beats the wave's own.
+    __shared__ unsigned long long sBound[KT > 0 ? 16 : 1];
 
     const int split = blockIdx.x;
     const int tid = threadIdx.x;
@@ -1492,6 +1496,7 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
     }
     if (tid < 16 * NQB) sCnt[tid] = 0;
     if (KT > 0 && tid < 4 * 16) sLen[tid] = 0;
+    if (KT > 0 && tid < 16) sBound[tid] = ~0ull;
 
     float tk[NQB], qn[NQB], ft[NQB];
     int ti[NQB];
@@ -1559,7 +1564,22 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
     // list has one writer at a time; an insertion re-checks against the
     // list's current k-th. Afterwards every lane re-reads its query's bound.
     const int kk = p.cap;
+    // Bound of query slot 0 from a composite (ordered key << 32 | id).
+    auto setBound = [&](uint64_t x) {
+        tk[0] = ord_to_key((uint32_t)(x >> 32));
+        ti[0] = (int)(uint32_t)(x & 0xFFFFFFFFu);
+        if (METRIC == 0) {
+            const float m = 0x1p-20f * (tk[0] + 2.0f * qn[0] + 2.0f * p.xnorm_max);
+            ft[0] = (tk[0] - qn[0]) + m;
+        } else {
+            ft[0] = -tk[0];
+        }
+    };
     auto topk_block = [&](const fx4 (&acc)[2][NQB], const fx4 (&xnh)[2], const int b) {
+        if (qv[0]) {   // another wave's tighter bound
+            const uint64_t sb = sBound[r16];
+            if (sb < ((uint64_t)key_to_ord(__float_as_uint(tk[0])) << 32 | (uint32_t)ti[0])) setBound(sb);
+        }
         uint64_t cc[2][4];
         bool has = false;
 #pragma unroll
@@ -1615,13 +1635,12 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
         }
         if (*len == kk && qv[0]) {
             const uint64_t x = L[kk - 1];
-            tk[0] = ord_to_key((uint32_t)(x >> 32));
-            ti[0] = (int)(uint32_t)(x & 0xFFFFFFFFu);
-            if (METRIC == 0) {
-                const float m = 0x1p-20f * (tk[0] + 2.0f * qn[0] + 2.0f * p.xnorm_max);
-                ft[0] = (tk[0] - qn[0]) + m;
+            const uint64_t sb = sBound[r16];
+            if (x < sb) {
+                if (quarter == 0) atomicMin(&sBound[r16], (unsigned long long)x);
+                setBound(x);
             } else {
-                ft[0] = -tk[0];
+                setBound(sb);
             }
         }
     };
@@ -2802,26 +2821,28 @@ __device__ __forceinline__ uint64_t wave_min_u64(uint64_t x) {
     return m;
 }
 
-// k rounds over the lanes' ascending lists v (KT entries, ~0 past the end):
-// round r's minimum goes to emit(r, m); stops early once every list is empty.
-template <int KT, class Emit>
-__device__ __forceinline__ void wave_merge(uint64_t (&v)[KT], int k, Emit&& emit) {
+// k rounds over the lanes' ascending lists, each lane holding its list's
+// head (~0: empty): round r's smallest head goes to emit(r, m) and its lane
+// replaces the head with pop(); stops early once every list is empty.
+template <class Pop, class Emit>
+__device__ __forceinline__ void wave_merge(uint64_t head, int k, Pop&& pop, Emit&& emit) {
     for (int r = 0; r < k; ++r) {
-        const uint64_t m = wave_min_u64(v[0]);
+        const uint64_t m = wave_min_u64(head);
         if (m == ~0ull) return;
-        if (v[0] == m) {   // this lane's head: shift its list
-#pragma unroll
-            for (int e = 0; e + 1 < KT; ++e) v[e] = v[e + 1];
-            v[KT - 1] = ~0ull;
-        }
+        if (head == m) head = pop();
         emit(r, m);
     }
 }
 
-// KT: entries a lane holds (cap <= KT): 16 for k <= 16, else kStreamTopK.
+// KT: entries a region holds at most (cap <= KT): 16 for k <= 16, else
+// kStreamTopK. With KT = 16 a lane's entries past the head wait in LDS
+// (entry e of lane t at sTail[(e - 1) * kMergeThreads + t]: 120 KB); with 32
+// they stay in registers and a pop shifts them.
 template <int KT>
 __global__ void __launch_bounds__(kMergeThreads) merge_lists_kernel(SelectParams p) {
     constexpr int NW = kMergeThreads / 64;
+    constexpr bool TAIL_LDS = KT <= 16;
+    __shared__ uint64_t sTail[TAIL_LDS ? (KT - 1) * kMergeThreads : 1];
     __shared__ uint64_t sWave[NW][KT];
 
     const int q = blockIdx.x;
@@ -2831,30 +2852,56 @@ __global__ void __launch_bounds__(kMergeThreads) merge_lists_kernel(SelectParams
     const int k = p.k;
 
     uint64_t v[KT];
+    int c;
     {
-        int c = 0;
-        const uint2* reg = p.cand + ((int64_t)q * p.nsplit + tid) * p.cap;
-        if (tid < p.nsplit) {
-            c = p.cnt[(int64_t)q * p.nsplit + tid];
-            c = c < p.cap ? c : p.cap;
-        }
+        // every lane loads from a valid address (lanes past the last region
+        // re-read it, entries past cap re-read the last one) so that the
+        // loads issue back to back, unpredicated; masks apply afterwards
+        const int sidx = tid < p.nsplit ? tid : p.nsplit - 1;
+        const uint2* reg = p.cand + ((int64_t)q * p.nsplit + sidx) * p.cap;
+        c = p.cnt[(int64_t)q * p.nsplit + sidx];
+        uint2 raw[KT];
 #pragma unroll
-        for (int e = 0; e < KT; ++e) v[e] = e < c ? composite(reg[e]) : ~0ull;
+        for (int e = 0; e < KT; ++e) raw[e] = reg[e < p.cap ? e : p.cap - 1];
+        c = tid < p.nsplit ? (c < p.cap ? c : p.cap) : 0;
+#pragma unroll
+        for (int e = 0; e < KT; ++e) v[e] = e < c ? composite(raw[e]) : ~0ull;
     }
+    if constexpr (TAIL_LDS) {
 #pragma unroll
-    for (int e = 0; e < KT; ++e) sWave[wave][e] = ~0ull;   // lane-uniform stores: same value
-    wave_merge(v, k, [&](int r, uint64_t m) {
+        for (int e = 1; e < KT; ++e) sTail[(e - 1) * kMergeThreads + tid] = v[e];
+    }
+    if (lane < KT) sWave[wave][lane] = ~0ull;
+    __builtin_amdgcn_wave_barrier();
+    int h = 0;
+    auto pop1 = [&]() -> uint64_t {
+        ++h;
+        if constexpr (TAIL_LDS) {
+            return h < c ? sTail[(h - 1) * kMergeThreads + tid] : ~0ull;
+        } else {
+#pragma unroll
+            for (int e = 0; e + 1 < KT; ++e) v[e] = v[e + 1];
+            v[KT - 1] = ~0ull;
+            return v[0];
+        }
+    };
+    wave_merge(v[0], k, pop1, [&](int r, uint64_t m) {
         if (lane == 0) sWave[wave][r] = m;
     });
     __syncthreads();
     if (wave != 0) return;
 
-    uint64_t w[KT];
-#pragma unroll
-    for (int e = 0; e < KT; ++e) w[e] = lane < NW ? sWave[lane][e] : ~0ull;
+    // wave 0: lane l < NW merges wave l's ascending list
+    int h2 = 0;
+    const int src = lane < NW ? lane : 0;
+    auto pop2 = [&]() -> uint64_t {
+        ++h2;
+        return h2 < KT ? sWave[src][h2] : ~0ull;
+    };
+    const uint64_t head2 = lane < NW ? sWave[src][0] : ~0ull;
     const int orow = p.qmap ? p.qmap[q] : q;
     int got = 0;
-    wave_merge(w, k, [&](int r, uint64_t m) {
+    wave_merge(head2, k, pop2, [&](int r, uint64_t m) {
         got = r + 1;
         if (lane == 0) {
             const float key = ord_to_key((uint32_t)(m >> 32));
