@@ -602,6 +602,22 @@ struct FlatIndex::Impl {
         return sp;
     }
 
+    // The streaming top-k search of mb raw fp32 queries (device rows of dim
+    // values; the scan prepares them itself): two launches, no staging.
+    // cd / cn: mb * nsplit1 * k entries and mb * nsplit1 counts.
+    void streamBatch(const float* dq, int mb, int k, const Plan& pl, uint2* cd, int* cn, int32_t* oIds,
+                     float* oVals, hipStream_t s) {
+        ScanParams p = scanParams(X.p, xn.as<float>(), nb, pl.rps1, pl.nsplit1, 1, nullptr, nullptr, mb, nullptr,
+                                  nullptr, k);
+        p.cand = cd; p.cnt = cn;
+        p.qraw = dq; p.qdim = dim; p.qcos = metric == Metric::Cosine ? 1 : 0;
+        launch_scan_topk(p, kernMetric(), storage, s);
+        SelectParams sp = selectParams(mb, pl.nsplit1, k, k, 1);
+        sp.cand = cd; sp.cnt = cn;
+        sp.out_ids = oIds; sp.out_vals = oVals;
+        launch_merge_lists(sp, s);
+    }
+
     // Search mb staged queries (storage type, qh or qbuf; norms in qnorm) and
     // write rows [0, mb) of the outputs.
     void searchBatch(int mb, int k, const Plan& pl, int32_t* oIds, float* oVals, hipStream_t s) {
@@ -629,16 +645,6 @@ struct FlatIndex::Impl {
         tauKk.ensure((size_t)mb * 4); tauKi.ensure((size_t)mb * 4);
         status.ensure((size_t)mb * 4);
 
-        if (pl.stream) {
-            cand.ensure((size_t)mb * pl.nsplit1 * k * sizeof(uint2));
-            cnt.ensure((size_t)mb * pl.nsplit1 * sizeof(int));
-            ScanParams p = scanParams(X.p, xn.as<float>(), nb, pl.rps1, pl.nsplit1, 1, Q, qn, mb, nullptr, nullptr, k);
-            launch_scan_topk(p, kernMetric(), storage, s);
-            SelectParams sp = selectParams(mb, pl.nsplit1, k, k, 1);
-            sp.out_ids = oIds; sp.out_vals = oVals;
-            launch_merge_lists(sp, s);
-            return;
-        }
         // tauS holds "no bound" from the query preparation
         if (pl.direct) {
             scan(X.p, xn.as<float>(), nb, pl.rps1, pl.nsplit1, 1, Q, qn, mb,
@@ -881,28 +887,12 @@ struct FlatIndex::Impl {
             return base + off;
         };
         size_t at = 0;
-        void* qs = carve(at, (size_t)kNoAllocMaxQ * dpad * esize);
-        float* qn = reinterpret_cast<float*>(carve(at, (size_t)kNoAllocMaxQ * sizeof(float)));
         int* cn = reinterpret_cast<int*>(carve(at, (size_t)m * pl.nsplit1 * sizeof(int)));
         uint2* cd = reinterpret_cast<uint2*>(carve(at, (size_t)m * pl.nsplit1 * k * sizeof(uint2)));
         if (at > kNoAllocScratchBytes)
             throw BadArg("allocation-free search: workspace of " + std::to_string(at) + " bytes exceeds the " +
                          std::to_string(kNoAllocScratchBytes) + "-byte scratch");
-        launch_prep_queries(dq, m, dim, kNoAllocMaxQ, dpad, storage, metric == Metric::Cosine, qs, qn, nullptr,
-                            nullptr, s);
-        ScanParams p;
-        std::memset(&p, 0, sizeof p);
-        p.X = X.p; p.xnorm = xn.as<float>(); p.xnorm_max = xnMax; p.nrows = nb;
-        p.rows_per_split = pl.rps1; p.nsplit = pl.nsplit1; p.id_stride = 1;
-        p.Q = qs; p.qnorm = qn; p.nq = m; p.nqb = 1; p.dpad = dpad;
-        p.cand = cd; p.cnt = cn; p.cap = k;
-        launch_scan_topk(p, kernMetric(), storage, s);
-        SelectParams sp;
-        std::memset(&sp, 0, sizeof sp);
-        sp.cand = cd; sp.cnt = cn; sp.nsplit = pl.nsplit1; sp.cap = k; sp.nq = m; sp.k = k; sp.j = 1; sp.j2 = 1;
-        sp.metric = kernMetric();
-        sp.out_ids = ids; sp.out_vals = vals; sp.out_stride = k;
-        launch_merge_lists(sp, s);
+        streamBatch(dq, m, k, pl, cd, cn, ids, vals, s);
         return k;
     }
 
@@ -934,6 +924,13 @@ struct FlatIndex::Impl {
         for (int64_t b0 = 0; b0 < m; b0 += mb) {
             const int n = (int)std::min<int64_t>(mb, m - b0);
             const Plan pb = (n == mb) ? pl : plan(n, k);
+            if (pb.stream) {
+                cand.ensure((size_t)n * pb.nsplit1 * k * sizeof(uint2));
+                cnt.ensure((size_t)n * pb.nsplit1 * sizeof(int));
+                streamBatch(dq + b0 * dim, n, k, pb, cand.as<uint2>(), cnt.as<int>(), ids ? ids + b0 * k : nullptr,
+                            vals ? vals + b0 * k : nullptr, s);
+                continue;
+            }
             const int64_t nPad = roundUp(n, kBN);
             // queries in the database's element type (Cosine normalised first),
             // their norms, and every query's first bound, in one launch

@@ -1475,6 +1475,8 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
     // a full wave list (k rows at or below it exist, so no row above it is a
     // result); every wave filters with it once it beats the wave's own.
     __shared__ unsigned long long sBound[KT > 0 ? 16 : 1];
+    __shared__ float sQn[KT > 0 ? 16 : 1];    // fused preparation: query norms ...
+    __shared__ float sInv[KT > 0 ? 16 : 1];   // ... and Cosine scale factors
 
     const int split = blockIdx.x;
     const int tid = threadIdx.x;
@@ -1489,10 +1491,74 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
     if (nqv <= 0) return;
     constexpr bool kPoolable = PASS == kPassRetry;
 
-    for (int i = tid; i < 16 * NQB * rowP; i += 256) {
-        const int row = i / rowP;
-        const int c = i - row * rowP;
-        *(fx4*)((char*)sQs + row * ldqB + c * 16) = *((const fx4*)p.Q + (int64_t)row * rowP + c);
+    // Top-k mode with raw queries: prep_queries' rules, per workgroup: Cosine
+    // rows scaled by float(1 / sqrt(s)) (s: sequential double sum of the
+    // squares), values rounded to the storage type, L2 norms the sequential
+    // double sum of the stored values' squares. The sums run on lanes 0..15,
+    // one query each.
+    const bool fused = KT > 0 && p.qraw != nullptr;
+    if (fused) {
+        constexpr int PE = S == kF32 ? 4 : 8;
+        if (p.qcos) {
+            if (tid < 16) {
+                float inv = 1.0f;
+                if (tid < p.nq) {
+                    const float* row = p.qraw + (int64_t)tid * p.qdim;
+                    double sum = 0.0;
+                    for (int c = 0; c < p.qdim; ++c) sum += (double)row[c] * row[c];
+                    if (sum > 0.0) inv = (float)(1.0 / sqrt(sum));
+                }
+                sInv[tid] = inv;
+            }
+            __syncthreads();
+        }
+        for (int i = tid; i < 16 * rowP; i += 256) {
+            const int row = i / rowP;
+            const int u = i - row * rowP;
+            const bool live = row < p.nq;
+            const float* src = p.qraw + (int64_t)(live ? row : 0) * p.qdim;
+            float v[PE];
+#pragma unroll
+            for (int e = 0; e < PE; ++e) {
+                const int c = u * PE + e;
+                float x = live && c < p.qdim ? src[c] : 0.0f;
+                if (p.qcos) x *= sInv[row];
+                if constexpr (S != kF32) x = from_bits<S>(to_bits<S>(x));
+                v[e] = x;
+            }
+            fx4 piece;
+            if constexpr (S == kF32) {
+                piece = fx4{v[0], v[1], v[2], v[3]};
+            } else {
+#pragma unroll
+                for (int w = 0; w < 4; ++w)
+                    piece[w] = __uint_as_float((uint32_t)to_bits<S>(v[2 * w]) | ((uint32_t)to_bits<S>(v[2 * w + 1]) << 16));
+            }
+            *(fx4*)((char*)sQs + row * ldqB + u * 16) = piece;
+        }
+        if (METRIC == 0) {
+            __syncthreads();
+            if (tid < 16) {
+                double nrm = 0.0;
+                if (tid < p.nq) {
+                    const char* rb = (const char*)sQs + tid * ldqB;
+                    for (int c = 0; c < p.qdim; ++c) {
+                        float x;
+                        if constexpr (S == kF32) x = ((const float*)rb)[c];
+                        else x = from_bits<S>(((const uint16_t*)rb)[c]);
+                        nrm += (double)x * x;
+                    }
+                }
+                sQn[tid] = (float)nrm;
+            }
+        }
+        __syncthreads();
+    } else {
+        for (int i = tid; i < 16 * NQB * rowP; i += 256) {
+            const int row = i / rowP;
+            const int c = i - row * rowP;
+            *(fx4*)((char*)sQs + row * ldqB + c * 16) = *((const fx4*)p.Q + (int64_t)row * rowP + c);
+        }
     }
     if (tid < 16 * NQB) sCnt[tid] = 0;
     if (KT > 0 && tid < 4 * 16) sLen[tid] = 0;
@@ -1508,7 +1574,7 @@ __global__ void __launch_bounds__(256) scan_small_kernel(ScanParams p) {
         // top-k mode starts from "no bound" (+inf, -1) in every wave
         tk[bq] = qv[bq] ? (KT > 0 ? INFINITY : p.tau_key[q]) : 0.0f;
         ti[bq] = qv[bq] ? (KT > 0 ? -1 : p.tau_id[q]) : -1;
-        qn[bq] = (METRIC == 0 && qv[bq]) ? p.qnorm[q] : 0.0f;
+        qn[bq] = (METRIC == 0 && qv[bq]) ? (fused ? sQn[q] : p.qnorm[q]) : 0.0f;
         if (METRIC == 0) {
             const float m = 0x1p-20f * (tk[bq] + 2.0f * qn[bq] + 2.0f * p.xnorm_max);
             ft[bq] = qv[bq] ? (tk[bq] - qn[bq]) + m : -INFINITY;
@@ -2588,7 +2654,8 @@ int topk_concurrency(int dpad, int storage, int metric) {
 void launch_scan_topk(const ScanParams& p, int metric, int storage, hipStream_t s) {
     if (p.nsplit <= 0) return;
     if (p.nq < 1 || p.nq > kStreamMaxQ || p.cap < 1 || p.cap > kStreamTopK || p.rows_per_split % kBM != 0 ||
-        p.dpad % kBK != 0 || !small_scan_fits(p.nq, p.dpad, storage))
+        p.dpad % kBK != 0 || !small_scan_fits(p.nq, p.dpad, storage) ||
+        (p.qraw ? (p.qdim < 1 || p.qdim > p.dpad) : p.Q == nullptr))
         throw std::runtime_error("scan_topk: bad parameters");
     const void* f = topk_kernel(p.dpad, storage, metric);
     const size_t lds = small_lds_bytes(1, p.dpad, storage);

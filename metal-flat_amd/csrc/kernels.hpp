@@ -133,6 +133,12 @@ struct ScanParams {
     int* qcnt;
     const int64_t* qoff;
     const int* qcap;
+    // Streaming top-k scan only: the caller's fp32 queries (qdim values a
+    // row, nq rows), prepared by every workgroup in LDS as prep_queries would
+    // (qcos: Cosine scaling first); Q and qnorm are then unused.
+    const float* qraw;
+    int qdim;
+    int qcos;
 };
 
 // Device-built retry work lists (flat search). After a full pass's select, a
@@ -285,9 +291,11 @@ void launch_select(const SelectParams& p, hipStream_t s);
 // Streaming top-k scan (batches of <= kStreamMaxQ queries, k = p.cap <=
 // kStreamTopK): one workgroup per split keeps each wave's exact top-k of the
 // rows it reads and writes the split's top-k of every query (cand regions of
-// p.cap entries, cnt = entries written); a select over the splits finishes the
+// p.cap entries, cnt = entries written); launch_merge_lists finishes the
 // search. No bound, sample or retry: exact by construction. The split count
 // wants to be the number of workgroups resident at once (topk_concurrency).
+// Queries: prepared rows (Q, qnorm) or the caller's fp32 rows (qraw), which
+// every workgroup prepares itself (no separate preparation launch).
 void launch_scan_topk(const ScanParams& p, int metric, int storage, hipStream_t s);
 int topk_concurrency(int dpad, int storage, int metric);
 // The streaming scan's exact top-k per query from its ascending per-split
