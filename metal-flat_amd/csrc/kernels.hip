@@ -565,29 +565,54 @@ __global__ void max_norm_kernel(const float* __restrict__ xn, int64_t n, unsigne
 // kernels at the register limit this keeps survivor handling free of scratch
 // reloads, whose wait for vector memory also waits for every prefetch load in
 // flight.
+// MAXT: the group test compares each slot's largest accumulator with its
+// bound (larger = nearer), 2 operations a row pair instead of 2 a value; the
+// slow path then tests every value. It needs accumulators ordered like the
+// key: IP (the dot) or PRE.
+// PRE (L2): the accumulators hold dot - ||x||^2 / 2 (the MFMA chain started
+// from -||x||^2 / 2 instead of 0), so xn4 is unused, ft holds -ft / 2 (the
+// bound on dot - ||x||^2 / 2) and key = fma(-2, acc, ||q||^2).
 struct QTab {
     const float* tk;
     const int* ti;
     const float* qn;
     int r32;
 };
-template <int METRIC, int PASS, int NB, int NS, bool LQ = false, class Emit>
+template <int METRIC, int PASS, int NB, int NS, bool LQ = false, bool MAXT = false, bool PRE = false, class Emit>
 __device__ __forceinline__ void filter_group(const fx16 (&acc)[NB], int g4, int b0, const fx4& xn4, int64_t r0,
                                              int64_t rowLim, int idStride, const int (&idb)[NB],
                                              const ScanParams& p, float (&tk)[NB], int (&ti)[NB],
                                              const float (&qn)[NB], float (&ft)[NB], const bool (&qv)[NB],
                                              const QTab& lq, Emit&& emit) {
+    static_assert(!MAXT || METRIC != 0 || PRE, "MAXT needs accumulators ordered like the key");
+    static_assert(!PRE || METRIC == 0, "PRE is an L2 form");
     bool f[4][NS];
     bool any = false;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
+    if constexpr (MAXT) {
+        // fmaxf drops a NaN value (never a survivor); the slow path's tests
+        // below reject it on their own
 #pragma unroll
         for (int b = 0; b < NS; ++b) {
-            const float dot = acc[b0 + b][g4 * 4 + i];
-            f[i][b] = METRIC == 0 ? fmaf(-2.0f, dot, xn4[i]) <= ft[b0 + b] : dot >= ft[b0 + b];
-            any |= f[i][b];
+            const fx16& a = acc[b0 + b];
+            const float m = fmaxf(fmaxf(a[g4 * 4 + 0], a[g4 * 4 + 1]), fmaxf(a[g4 * 4 + 2], a[g4 * 4 + 3]));
+            any |= m >= ft[b0 + b];
         }
-    if (!any) return;
+        if (!any) return;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int b = 0; b < NS; ++b) f[i][b] = acc[b0 + b][g4 * 4 + i] >= ft[b0 + b];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int b = 0; b < NS; ++b) {
+                const float dot = acc[b0 + b][g4 * 4 + i];
+                f[i][b] = METRIC == 0 ? fmaf(-2.0f, dot, xn4[i]) <= ft[b0 + b] : dot >= ft[b0 + b];
+                any |= f[i][b];
+            }
+        if (!any) return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int64_t row = r0 + i;
@@ -602,7 +627,7 @@ __device__ __forceinline__ void filter_group(const fx16 (&acc)[NB], int g4, int 
             float key;
             if (METRIC == 0) {
                 const float qnb = LQ ? lq.qn[bn * 32 + lq.r32] : qn[bn];
-                const float t = fmaf(-2.0f, dot, qnb + xn4[i]);
+                const float t = PRE ? fmaf(-2.0f, dot, qnb) : fmaf(-2.0f, dot, qnb + xn4[i]);
                 key = (t < 0.0f ? 0.0f : t) + 0.0f;
             } else {
                 key = -dot + 0.0f;
@@ -614,6 +639,7 @@ __device__ __forceinline__ void filter_group(const fx16 (&acc)[NB], int g4, int 
                     ti[bn] = id;
                     ft[bn] = METRIC == 0 ? (key - qn[bn]) + 0x1p-20f * (key + 2.0f * qn[bn] + 2.0f * p.xnorm_max)
                                          : -key;
+                    if (PRE) ft[bn] *= -0.5f;
                 }
                 continue;
             }
@@ -665,6 +691,10 @@ __device__ __forceinline__ void filter_group(const fx16 (&acc)[NB], int g4, int 
 template <int S, int METRIC, int PASS, bool IVF = false>
 __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     constexpr int ES = S == kF32 ? 4 : 2;   // element bytes
+    // fp16/bf16: the filter's group test through maxima (MAXT) and, for L2,
+    // accumulators started from -||x||^2 / 2 (PRE); see filter_group
+    constexpr bool MAXT = S != kF32;
+    constexpr bool PRE = S != kF32 && METRIC == 0;
     __shared__ __attribute__((aligned(16))) float sX[2 * kBM * kLds];
     __shared__ __attribute__((aligned(16))) float sQ[2 * kBN * kLds];
     __shared__ __attribute__((aligned(16))) float sXn[2 * kBM];   // tile row norms, by tile parity
@@ -769,6 +799,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
         if (METRIC == 0) {
             const float m = 0x1p-20f * (tk[bn] + 2.0f * qn[bn] + 2.0f * p.xnorm_max);
             ft[bn] = qv[bn] ? (tk[bn] - qn[bn]) + m : -INFINITY;
+            if (PRE) ft[bn] *= -0.5f;
         } else {
             ft[bn] = qv[bn] ? -tk[bn] : INFINITY;
         }
@@ -852,7 +883,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
             *(fx4*)(dq + (ldRow + 32 * i) * kLds + ldCol) = rq[i];
         }
         if (METRIC == 0 && kc == 0 && tid < kBM / 4)
-            *(fx4*)(sXn + (tile & 1) * kBM + tid * 4) = rn;
+            *(fx4*)(sXn + (tile & 1) * kBM + tid * 4) = PRE ? rn * -0.5f : rn;
     };
 
     fx16 acc[2][2];
@@ -878,7 +909,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
         const float* sq = sQ + buf * (kBN * kLds);
         // the epilogue's row norms, read before the last chunk's MFMAs
         fx4 xnr[2][4];
-        if (METRIC == 0 && kc == nk - 1) {
+        if (METRIC == 0 && !PRE && kc == nk - 1) {
 #pragma unroll
             for (int bm = 0; bm < 2; ++bm)
 #pragma unroll
@@ -897,7 +928,16 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
                 fx4 a1 = *(const fx4*)(sx + aOff + 32 * kLds + g * 8);
                 fx4 b0 = *(const fx4*)(sq + bOff + g * 8);
                 fx4 b1 = *(const fx4*)(sq + bOff + 32 * kLds + g * 8);
-                if constexpr (S != kF32) {
+                if constexpr (PRE) {
+                    // a tile's first MFMAs start from acc[bm][0] (set below to
+                    // the rows' -||x||^2 / 2), which is overwritten last
+                    const bool zc = ZERO && g == 0;
+                    acc[0][1] = mfma32x32x16<S>(a0, b1, zc ? acc[0][0] : acc[0][1]);
+                    acc[0][0] = mfma32x32x16<S>(a0, b0, acc[0][0]);
+                    acc[1][1] = mfma32x32x16<S>(a1, b1, zc ? acc[1][0] : acc[1][1]);
+                    acc[1][0] = mfma32x32x16<S>(a1, b0, acc[1][0]);
+                    continue;
+                } else if constexpr (S != kF32) {
                     const bool zc = ZERO && g == 0;
                     acc[0][0] = mfma32x32x16<S>(a0, b0, zc ? z : acc[0][0]);
                     acc[0][1] = mfma32x32x16<S>(a0, b1, zc ? z : acc[0][1]);
@@ -921,6 +961,19 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
                 }
             }
         };
+        if (PRE && kc == 0) {
+            // the tile's -||x||^2 / 2 (sXn, staged with its first chunk) for
+            // the rows of this lane's accumulator registers: row wm * 64 +
+            // bm * 32 + 8 g4 + 4 h + i at register 4 g4 + i
+#pragma unroll
+            for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const fx4 v = *(const fx4*)(sXn + (tile & 1) * kBM + wm * 64 + bm * 32 + g4 * 8 + h * 4);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[bm][0][g4 * 4 + i] = v[i];
+                }
+        }
         if (kc == 0)
             mma(std::true_type{});
         else
@@ -936,8 +989,9 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
                     const int rl = wm * 64 + bm * 32 + g4 * 8 + h * 4;
                     const int64_t r0 = tileRow0 + rl;
                     fx4 xn4 = {0.0f, 0.0f, 0.0f, 0.0f};
-                    if (METRIC == 0) xn4 = xnr[bm][g4];
-                    filter_group<METRIC, PASS, 2, 2>(acc[bm], g4, 0, xn4, r0, rowLim, IVF ? 1 : p.id_stride, idb,
+                    if (METRIC == 0 && !PRE) xn4 = xnr[bm][g4];
+                    filter_group<METRIC, PASS, 2, 2, false, MAXT, PRE>(acc[bm], g4, 0, xn4, r0, rowLim,
+                                                                       IVF ? 1 : p.id_stride, idb,
                                                   p, tk, ti, qn, ft, qv, QTab{nullptr, nullptr, nullptr, 0},
                                                   [&](int bn, float key, int id) {
                         const int ql = wn * 64 + bn * 32 + r32;
@@ -1040,6 +1094,10 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     constexpr int NK = S == kF32 ? 4 : 2;          // operand pieces per row block per chunk
     constexpr int KSTEP = S == kF32 ? 256 : 512;   // byte step between a lane's pieces in a chunk
     constexpr int CB = 32 * 32 * ES;               // bytes per 32 x 32 chunk
+    // fp16/bf16: the filter's group test through maxima (MAXT) and, for L2,
+    // accumulators started from -||x||^2 / 2 (PRE); see filter_group
+    constexpr bool MAXT = S != kF32;
+    constexpr bool PRE = S != kF32 && METRIC == 0;
     extern __shared__ __attribute__((aligned(16))) float sQr[];   // [TQ][dpad + 16 / ES] elements
     __shared__ __attribute__((aligned(16))) float sXn[4 * 64];    // per wave: its slice's row norms
     __shared__ int sCnt[TQ];
@@ -1178,6 +1236,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
         if (METRIC == 0) {
             const float m = 0x1p-20f * (tk[bn] + 2.0f * qn[bn] + 2.0f * p.xnorm_max);
             ft[bn] = qv[bn] ? (tk[bn] - qn[bn]) + m : -INFINITY;
+            if (PRE) ft[bn] *= -0.5f;
         } else {
             ft[bn] = qv[bn] ? -tk[bn] : INFINITY;
         }
@@ -1280,19 +1339,40 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
                             acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(
                                 a[bm][k][j], b[bn][j], (ZERO && k == 0 && j == 0) ? z : acc[bm][bn], 0, 0, 0);
             } else {
+                // PRE: a slice's first MFMAs all start from acc[bm][0] (the
+                // rows' -||x||^2 / 2, set by preInit), which is overwritten last
 #pragma unroll
                 for (int bm = 0; bm < 2; ++bm)
 #pragma unroll
-                    for (int bn = 0; bn < NB; ++bn)
-                        acc[bm][bn] = mfma32x32x16<S>(a[bm][k], b[bn], (ZERO && k == 0) ? z : acc[bm][bn]);
+                    for (int bn = NB - 1; bn >= 0; --bn)
+                        acc[bm][bn] = mfma32x32x16<S>(a[bm][k], b[bn],
+                                                      (ZERO && k == 0) ? (PRE ? acc[bm][0] : z) : acc[bm][bn]);
             }
+        }
+    };
+    // PRE: acc[bm][0] = -||x||^2 / 2 of the rows this lane's accumulator
+    // registers hold in block bm (register 4 g4 + i: row 32 bm + 8 g4 + 4 h + i
+    // of the slice), staged through the wave's sXn entries.
+    auto preInit = [&](float xnv) {
+        if constexpr (PRE) {
+            sXn[wave * 64 + lane] = -0.5f * xnv;
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const fx4 v = *(const fx4*)(sXn + wave * 64 + bm * 32 + g4 * 8 + h * 4);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[bm][0][g4 * 4 + i] = v[i];
+                }
+            __builtin_amdgcn_wave_barrier();
         }
     };
 
     // Filter epilogue of slice sl (rows rowBeg + 64 sl ..), whose row norms
     // this lane holds for row `lane` in xnv.
     auto epilogue = [&](int sl, float xnv) {
-        if (METRIC == 0) {
+        if (METRIC == 0 && !PRE) {
             sXn[wave * 64 + lane] = xnv;
             __builtin_amdgcn_wave_barrier();
         }
@@ -1303,10 +1383,10 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
                 const int rl = bm * 32 + g4 * 8 + h * 4;
                 const int64_t r0 = rowOrg + (int64_t)sl * 64 + rl;
                 fx4 xn4 = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (METRIC == 0) xn4 = *(const fx4*)(sXn + wave * 64 + rl);
+                if (METRIC == 0 && !PRE) xn4 = *(const fx4*)(sXn + wave * 64 + rl);
 #pragma unroll
                 for (int bp = 0; bp < (NB + 1) / 2; ++bp)
-                    filter_group<METRIC, PASS, NB, NB == 1 ? 1 : 2, LQ>(acc[bm], g4, 2 * bp, xn4, r0, rowLim,
+                    filter_group<METRIC, PASS, NB, NB == 1 ? 1 : 2, LQ, MAXT, PRE>(acc[bm], g4, 2 * bp, xn4, r0, rowLim,
                                                                          idStride, idb, p, tk, ti, qn, ft, qv, lqt,
                                                   [&](int bn, float key, int id) {
                         const int ql = bn * 32 + r32;
@@ -1366,6 +1446,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
         for (int sl = wave; sl < nsl; sl += 4) {
             const int nx = sl + 4 < nsl ? sl + 4 : sl;
             const float xnNext = norm(nx);
+            preInit(xnv);
 #pragma unroll
             for (int t = 0; t < G; ++t) {
                 if (t == 0) mma(buf[t], t, std::true_type{});
@@ -1374,6 +1455,10 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
                 for (int bm = 0; bm < 2; ++bm)
 #pragma unroll
                     for (int k = 0; k < NK; ++k) buf[t][bm][k] = lda(nx, bm, t, k);
+                // issue the refill here, not after the last chunk's MFMAs
+                // (where the scheduler otherwise sinks it to reuse buf[t]'s
+                // registers for the next chunk's query fragments)
+                __builtin_amdgcn_sched_barrier(0);
             }
             epilogue(sl, xnv);
             flush(kRing / 2);
@@ -1392,6 +1477,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
         for (int sl = wave; sl < nsl; sl += 4) {
             const int nxs = sl + 4 < nsl ? sl + 4 : sl;
             const float xnNext = norm(nxs);
+            preInit(xnv);
             for (int t = 0; t < nchunk; ++t) {
                 const bool lastT = t + 1 == nchunk;
                 const int ns = lastT ? nxs : sl;
