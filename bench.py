@@ -51,13 +51,15 @@ PEAK_HBM_GBS = 8000.0
 # committed under profiles/. Keyed by (config, nq, storage); reported as
 # roofline.traffic for the configuration it was measured on, null otherwise.
 MEASURED_TRAFFIC_BYTES = {
-    ("C2", 10_000, "f32"): 4.76e9,
-    ("C2", 10_000, "f16"): 1.907e9,
-    ("C3", 10_000, "f32"): 287.8e9,
-    ("C4", 1, "f32"): 3.880e9,
-    ("C4", 1, "f16"): 1.960e9,
-    ("C4", 64, "f16"): 1.972e9,
-    ("C5", 2_000_000, "f32"): 34.27e9,
+    ("C1", 1_000, "f32"): 61.9e6,
+    ("C2", 10_000, "f32"): 4.636e9,
+    ("C2", 10_000, "f16"): 2.090e9,
+    ("C3", 10_000, "f32"): 239.84e9,
+    ("C3", 10_000, "bf16"): 58.74e9,
+    ("C4", 1, "f32"): 3.881e9,
+    ("C4", 1, "f16"): 1.961e9,
+    ("C4", 64, "f16"): 1.970e9,
+    ("C5", 2_000_000, "f32"): 30.7e9,
     # IVF fine scan (both launches of a search), C2's data, nlist 1000, nprobe 62
     ("IVF", 1000, 62, "f32"): 4.66e9,
     # IVF-PQ ADC full pass, C2's data, nlist 1000, nprobe 62, m_sub 16 (lookup tables, codes, cross tables)
