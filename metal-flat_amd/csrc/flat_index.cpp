@@ -291,12 +291,13 @@ struct FlatIndex::Impl {
     // The streaming top-k scan's plan: one workgroup per split, as many
     // splits as run at once; each streams its rows once and hands k candidates
     // per query to the select, whose LDS buffer holds them all.
-    void setStreamPlan(Plan& pl, int k) const {
+    // maxSplits: a workspace bound (the allocation-free path's scratch).
+    void setStreamPlan(Plan& pl, int k, int64_t maxSplits = kMergeMaxSplit) const {
         pl.stream = true;
         const int64_t ntiles = std::max<int64_t>(1, (nb + kBM - 1) / kBM);
         int64_t want = streamSplits > 0 ? streamSplits : topkConcurrency();
         if (want <= 0) want = 1024;
-        want = std::min<int64_t>({want, ntiles, kMergeMaxSplit});
+        want = std::max<int64_t>(1, std::min<int64_t>({want, ntiles, kMergeMaxSplit, maxSplits}));
         const int64_t tps = (ntiles + want - 1) / want;
         pl.nsplit1 = (int)((ntiles + tps - 1) / tps);
         pl.rps1 = tps * kBM;
@@ -880,7 +881,9 @@ struct FlatIndex::Impl {
         }
         char* base = static_cast<char*>(noalloc_scratch(device));
         Plan pl;
-        setStreamPlan(pl, k);
+        // the split lists and counts of m queries must fit the scratch (with
+        // 256-byte alignment slack for both carves)
+        setStreamPlan(pl, k, (int64_t)((kNoAllocScratchBytes - 512) / ((size_t)m * ((size_t)k * sizeof(uint2) + sizeof(int)))));
         auto carve = [&](size_t& at, size_t bytes) {
             const size_t off = at;
             at = (at + bytes + 255) / 256 * 256;

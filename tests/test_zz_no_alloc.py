@@ -31,16 +31,19 @@ def dev_search(idx, q, k, noalloc, st):
     return ids.numpy(), dist.numpy(), ku
 
 
-def test_noalloc_matches_device_entry_integer(gpu_ok):
+@pytest.mark.parametrize("nb,d", [(300_000, 96), (2_000_000, 16)])
+def test_noalloc_matches_device_entry_integer(gpu_ok, nb, d):
+    """d = 16 runs the most streaming workgroups at once: at 16 queries and
+    k = 32 their lists would outgrow the scratch, so the split count is capped."""
     rng = np.random.default_rng(71)
-    x = rng.integers(0, 8, size=(300_000, 96)).astype(np.float32)
-    q = rng.integers(0, 8, size=(16, 96)).astype(np.float32)
+    x = rng.integers(0, 8, size=(nb, d)).astype(np.float32)
+    q = rng.integers(0, 8, size=(16, d)).astype(np.float32)
     st = hipmem.Stream()
     try:
-        with mflat.FlatIndex(96, L2) as idx:
+        with mflat.FlatIndex(d, L2) as idx:
             idx.add(x)
             for m, k in ((16, 32), (3, 7)):   # the second call smaller than the first
-                print(f"[noalloc] integer m={m} k={k}", flush=True)
+                print(f"[noalloc] integer nb={nb} d={d} m={m} k={k}", flush=True)
                 ni, nd, nku = dev_search(idx, q[:m], k, True, st)
                 di, dd, dku = dev_search(idx, q[:m], k, False, st)
                 assert nku == dku == k
