@@ -700,6 +700,14 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     __shared__ __attribute__((aligned(16))) float sXn[2 * kBM];   // tile row norms, by tile parity
     __shared__ int sCnt[kBN];
     __shared__ unsigned long long sBest[kBN];   // argmin: per-query (ordered key, id)
+    // Flat retry pass: survivors staged in LDS and written in one block of
+    // slots per (workgroup, query), as in scan_resident (there: why); the
+    // stage fits the LDS two workgroups per CU leave.
+    constexpr bool STAGE = PASS == kPassRetry && !IVF;
+    constexpr int kStage = 480;
+    __shared__ uint2 sStage[STAGE ? kStage : 1];
+    __shared__ uint32_t sStageTag[STAGE ? kStage : 1];
+    __shared__ int sStageN;
     __shared__ int sEnt[IVF ? kBN : 1];   // IVF: the item's entries (-1: empty slot)
     __shared__ int sQi[IVF ? kBN : 1];    // ... their queries
     __shared__ int sReg[IVF ? kBN : 1];   // ... their candidate regions
@@ -749,6 +757,7 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
     const int r32 = lane & 31;
     const int h = lane >> 5;
 
+    if (tid == 0) sStageN = 0;
     if (tid < kBN) {
         sCnt[tid] = 0;
         sBest[tid] = ~0ull;
@@ -995,8 +1004,22 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
                                                   p, tk, ti, qn, ft, qv, QTab{nullptr, nullptr, nullptr, 0},
                                                   [&](int bn, float key, int id) {
                         const int ql = wn * 64 + bn * 32 + r32;
-                        const int slot = atomicAdd(&sCnt[ql], 1);
                         const uint2 v = make_uint2(__float_as_uint(key), (unsigned)id);
+                        if constexpr (STAGE) {
+                            if (p.qcnt) {
+                                const int e = atomicAdd(&sStageN, 1);
+                                if (e < kStage) {
+                                    sStage[e] = v;
+                                    sStageTag[e] = ((uint32_t)atomicAdd(&sCnt[ql], 1) << 8) | (uint32_t)ql;
+                                } else {   // a global slot of its own
+                                    const int q = qb * kBN + ql;
+                                    const int gs = atomicAdd(&p.qcnt[(int64_t)q * kPoolCntStride], 1);
+                                    if (gs < p.qcap[q]) p.cand[p.qoff[q] + gs] = v;
+                                }
+                                return;
+                            }
+                        }
+                        const int slot = atomicAdd(&sCnt[ql], 1);
                         if constexpr (IVF) {
                             if (slot < p.cap) {
                                 p.cand[(int64_t)sReg[ql] * p.cap + slot] = v;
@@ -1039,6 +1062,25 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
         return;
     }
     __syncthreads();
+    if constexpr (STAGE) {
+        if (p.qcnt) {
+            int* sBase = reinterpret_cast<int*>(sBest);
+            if (tid < kBN) {
+                const int q = qb * kBN + tid;
+                sBase[tid] = sCnt[tid] > 0 ? atomicAdd(&p.qcnt[(int64_t)q * kPoolCntStride], sCnt[tid]) : 0;
+            }
+            __syncthreads();
+            const int n = sStageN < kStage ? sStageN : kStage;
+            for (int e = tid; e < n; e += 256) {
+                const uint32_t tag = sStageTag[e];
+                const int ql = (int)(tag & 255u);
+                const int q = qb * kBN + ql;
+                const int gs = sBase[ql] + (int)(tag >> 8);
+                if (gs < p.qcap[q]) p.cand[p.qoff[q] + gs] = sStage[e];
+            }
+            return;
+        }
+    }
     if (tid < kBN) {
         if constexpr (IVF) {
             if (sReg[tid] >= 0) p.cnt[sReg[tid]] = p.ivf_spill && sCnt[tid] > p.cap ? p.cap : sCnt[tid];
@@ -1102,16 +1144,29 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
     __shared__ __attribute__((aligned(16))) float sXn[4 * 64];    // per wave: its slice's row norms
     __shared__ int sCnt[TQ];
     __shared__ unsigned long long sBest[TQ];
-    // Per-wave survivor ring (fp32 full and retry passes): (key, id, query)
-    // staged in LDS and written to the candidate regions half a ring at a
-    // time, so the next slices' prefetch waits rarely wait on survivor stores
-    // (1.4% at C2). The fp16/bf16 instantiations hold a whole slice of
-    // operands in registers and lose more to the extra register pressure.
-    constexpr bool RING = S == kF32 && (PASS == kPassFull || PASS == kPassRetry);
+    // Per-wave survivor ring (fp32 full pass): (key, id, query) staged in LDS
+    // and written to the candidate regions half a ring at a time, so the next
+    // slices' prefetch waits rarely wait on survivor stores (1.4% at C2). The
+    // fp16/bf16 instantiations hold a whole slice of operands in registers
+    // and lose more to the extra register pressure.
+    constexpr bool RING = S == kF32 && PASS == kPassFull;
     __shared__ uint32_t sRingKey[RING ? 4 * kRing : 1];
     __shared__ int sRingId[RING ? 4 * kRing : 1];
     __shared__ int sRingQ[RING ? 4 * kRing : 1];
     __shared__ int sRingN[4];
+    // Flat retry pass (pooled regions, one global slot counter per query):
+    // survivors staged in LDS with a slot among the workgroup's own for their
+    // query (sCnt); at the end one global atomic per query reserves the
+    // workgroup's block of slots (in sBest's storage) and the staged entries
+    // are written there (one atomic per survivor on counters shared by every
+    // workgroup: C2 fp16's retry pass 250 -> 193 us); beyond kStage a
+    // survivor takes a slot of its own. (Entry: key bits and id; tag: slot
+    // << 8 | query slot.)
+    constexpr bool STAGE = PASS == kPassRetry && !IVF;
+    constexpr int kStage = 768;   // 9 KB, the ring's LDS in the other passes
+    __shared__ uint2 sStage[STAGE ? kStage : 1];
+    __shared__ uint32_t sStageTag[STAGE ? kStage : 1];
+    __shared__ int sStageN;
     // fp16/bf16 (a whole slice of operands in registers): survivor-only query
     // state in LDS (filter_group's LQ), not registers
     constexpr bool LQ = S != kF32 && PASS != kPassArgmin;
@@ -1208,6 +1263,7 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
         sBest[tid] = ~0ull;
     }
     if (tid < 4) sRingN[tid] = 0;
+    if (tid == 0) sStageN = 0;
 
     // Per-lane query state for its NB query blocks; bounds as in scan_filter.
     float tk[NB], qn[NB], ft[NB];
@@ -1390,6 +1446,19 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
                                                                          idStride, idb, p, tk, ti, qn, ft, qv, lqt,
                                                   [&](int bn, float key, int id) {
                         const int ql = bn * 32 + r32;
+                        if constexpr (STAGE) {
+                            if (p.qcnt) {
+                                const uint2 v = make_uint2(__float_as_uint(key), (unsigned)id);
+                                const int e = atomicAdd(&sStageN, 1);
+                                if (e < kStage) {
+                                    sStage[e] = v;
+                                    sStageTag[e] = ((uint32_t)atomicAdd(&sCnt[ql], 1) << 8) | (uint32_t)ql;
+                                } else {
+                                    store(ql, 0, v);   // a global slot of its own
+                                }
+                                return;
+                            }
+                        }
                         const int pos = RING ? atomicAdd(&sRingN[wave], 1) : kRing;
                         if (pos < kRing) {
                             sRingKey[wave * kRing + pos] = __float_as_uint(key);
@@ -1515,6 +1584,25 @@ __global__ void __launch_bounds__(256, 2) scan_resident_kernel(ScanParams p) {
         return;
     }
     __syncthreads();
+    if constexpr (STAGE) {
+        if (p.qcnt) {
+            int* sBase = reinterpret_cast<int*>(sBest);
+            if (tid < TQ) {
+                const int q = qb * TQ + tid;
+                sBase[tid] = sCnt[tid] > 0 ? atomicAdd(&p.qcnt[(int64_t)q * kPoolCntStride], sCnt[tid]) : 0;
+            }
+            __syncthreads();
+            const int n = sStageN < kStage ? sStageN : kStage;
+            for (int e = tid; e < n; e += 256) {
+                const uint32_t tag = sStageTag[e];
+                const int ql = (int)(tag & 255u);
+                const int q = qb * TQ + ql;
+                const int gs = sBase[ql] + (int)(tag >> 8);
+                if (gs < p.qcap[q]) p.cand[p.qoff[q] + gs] = sStage[e];
+            }
+            return;
+        }
+    }
     if constexpr (IVF) {
         if (tid < wk.z) p.cnt[sReg[tid]] = p.ivf_spill && sCnt[tid] > p.cap ? p.cap : sCnt[tid];
     } else if (tid < TQ) {
