@@ -260,14 +260,14 @@ struct FlatIndex::Impl {
     int64_t retryPool = 0;
     // MFLAT_STREAM_MAXQ = n: batches of up to n queries (0: none) take the
     // streaming top-k scan; MFLAT_STREAM_SPLITS = n: its split count.
-    // Default: single queries only. Measured at C4 (10M x 96, k 10): its
-    // scan runs 0.587 ms against scan_small's 0.565 at nq 1 and loses more as
-    // queries are added (each wave's bound starts unbounded, so its lists
-    // take ~k (1 + ln(rows / k)) insertions a query; 0.806 against 0.573 ms at
-    // nq 16); at nq 1 the three launches it saves against the sample path's
-    // nine make the whole search equal or slightly faster (0.650 / 0.654 ms
-    // fp32, 0.363 / 0.372 ms fp16).
-    int streamMaxQ = 1;
+    // Default: up to 2 queries with fp32 storage, 1 with fp16 / bf16. The
+    // streaming scan loses to the bound filter's as queries are added (each
+    // wave's bound starts unbounded, so its lists take ~k (1 + ln(rows / k))
+    // insertions a query) but saves the sample path's launches and selects.
+    // Whole search at C4 (10M x 96, k 10), streaming / sample path, ms: fp32
+    // nq 1 0.601 / 0.640, nq 2 0.623 / 0.643, nq 4 0.652 / 0.653, nq 8 0.703 /
+    // 0.656, nq 16 0.790 / 0.665; fp16 nq 1 0.329 / 0.372, nq 4 0.381 / 0.367.
+    int streamMaxQ = -1;   // -1: the storage type's default
     int streamSplits = 0;
     // MFLAT_QGROUP = n: query blocks co-scheduled per XCD by the MFMA scans
     // (0: each kernel's default).
@@ -307,7 +307,8 @@ struct FlatIndex::Impl {
 
     // Small batches with a small k: the streaming top-k scan.
     bool streamPath(int64_t mb, int k) const {
-        return mb <= std::min(streamMaxQ, kStreamMaxQ) && k <= kStreamTopK && small_scan_fits((int)mb, dpad, storage);
+        const int maxq = streamMaxQ >= 0 ? streamMaxQ : storage == kF32 ? 2 : 1;
+        return mb <= std::min(maxq, kStreamMaxQ) && k <= kStreamTopK && small_scan_fits((int)mb, dpad, storage);
     }
     mutable int topkConc = -1;
     int topkConcurrency() const {
