@@ -254,7 +254,7 @@ struct FlatIndex::Impl {
     PinnedInts hostCounters;
     // Diagnostics knobs, read once when the index is created: MFLAT_RETRY_WINDOW
     // = n limits a device-built retry window to n queries, MFLAT_RETRY_POOL = n
-    // the round-2 pool to n entries (0 = not set). They exercise the host's
+    // the retry pool to n entries (0 = not set). They exercise the host's
     // fallback windows; results never depend on them, only the work done.
     int retryWindow = 0;
     int64_t retryPool = 0;

@@ -68,8 +68,8 @@ def test_distance_sorted_10m_small_batches(gpu_ok, monkeypatch):
 def test_distance_sorted_large_batch(gpu_ok, monkeypatch):
     """2M x 16, rank following row order, 300 queries (the 128-query kernels):
     most queries fail the full pass. Default plan, then a 16-query window (the
-    host runs the other windows) and a 64-entry pool (round 2 drains through
-    the host's pool fallback)."""
+    host runs the other windows) and a 64-entry pool (the retry pass drains
+    through the host's pool fallback)."""
     x = sorted_db(2_000_000, 16, seed=33, block=500)
     q = queries(300, 16, seed=34)
     check(x, q, 10, {}, monkeypatch)
