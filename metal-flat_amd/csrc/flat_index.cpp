@@ -195,6 +195,7 @@ int pow2ceil(int64_t x) {
 
 struct Plan {
     bool stream = false;  // streaming top-k scan (small batch, small k): no sample, no retries
+    bool wide = false;    // every pass on the wide-tile kernel (wideBatch)
     bool direct = true;
     int64_t R0 = 0;       // sample rows
     int stride = 1;       // sample row r is database row r*stride
@@ -278,11 +279,23 @@ struct FlatIndex::Impl {
 
     // Workgroups of each pass's MFMA scan that fit the device at once (the
     // split plan's tail rule), queried once per pass.
-    mutable int conc[4] = {-1, -1, -1, -1};
-    int concurrency(int pass) const {
-        if (conc[pass] < 0) conc[pass] = scan_concurrency(dpad, storage, kernMetric(), pass);
-        return conc[pass];
+    mutable int conc[2][4] = {{-1, -1, -1, -1}, {-1, -1, -1, -1}};
+    int concurrency(int pass, bool wide = false) const {
+        int& c = conc[wide ? 1 : 0][pass];
+        if (c < 0) c = scan_concurrency(dpad, storage, kernMetric(), pass, wide);
+        return c;
     }
+    // fp16/bf16 batches of more than 128 queries at a d beyond scan_resident
+    // run the wide-tile kernel for every pass (MFLAT_WIDE=0: the 128-query
+    // tiled kernel instead, read when the index is created). Split plans then
+    // count 256-query blocks: they are given half the query count.
+    int wideKnob = 1;
+    bool wideBatch(int64_t mb) const {
+        return wideKnob && wide_scan_applies((int)std::min<int64_t>(mb, 1 << 30), dpad, storage);
+    }
+    int planQ(int64_t mb) const { return (int)(wideBatch(mb) ? (mb + 1) / 2 : mb); }
+    int planConc(int pass, int64_t mb) const { return concurrency(pass, wideBatch(mb)); }
+    bool curWide = false;   // the batch being searched runs the wide-tile kernel
 
     void setDevice() const {
         if (device >= 0) HIPC(hipSetDevice(device));
@@ -342,14 +355,16 @@ struct FlatIndex::Impl {
         // a sample level and its select.
         if (nb <= std::max<int64_t>(2 * r, kSelLds)) {
             pl.direct = true;
-            splitPlan(nb, (int)mb, dpad, storage, pl.rps1, pl.nsplit1, true, 1, concurrency(kPassFull));
+            pl.wide = wideBatch(mb);
+            splitPlan(nb, planQ(mb), dpad, storage, pl.rps1, pl.nsplit1, true, 1, planConc(kPassFull, mb));
             pl.cap1 = (int)pl.rps1;
             pl.perQuery = (size_t)pl.nsplit1 * pl.cap1;
             return pl;
         }
         pl.direct = false;
+        pl.wide = wideBatch(mb);
         setFirstSample(pl, mb, k, r);
-        splitPlan(nb, (int)mb, dpad, storage, pl.rps1, pl.nsplit1, true, 1, concurrency(kPassFull));
+        splitPlan(nb, planQ(mb), dpad, storage, pl.rps1, pl.nsplit1, true, 1, planConc(kPassFull, mb));
         const double e1 = (double)pl.j * (double)nb / (double)r;   // expected survivors
         pl.e1 = e1;
         const int64_t perSplit = (int64_t)(2.0 * e1 / pl.nsplit1) + 64;
@@ -368,7 +383,7 @@ struct FlatIndex::Impl {
         const double lambda = (double)k * (double)r / (double)nb;
         pl.j = chooseSpeculativeRank(k, lambda, mb, nb, r);
         pl.j2 = chooseJ(k, lambda, 1e-9);
-        splitPlan(r, (int)mb, dpad, storage, pl.rps0, pl.nsplit0, true, 1, concurrency(kPassSample));
+        splitPlan(r, planQ(mb), dpad, storage, pl.rps0, pl.nsplit0, true, 1, planConc(kPassSample, mb));
         pl.cap0 = (int)pl.rps0;
     }
 
@@ -485,7 +500,7 @@ struct FlatIndex::Impl {
 
     void finishSecondSample(Plan& pl, int64_t mb, int k, int64_t r) const {
         pl.strideb = (int)(nb / pl.Rb);
-        splitPlan(pl.Rb, (int)mb, dpad, storage, pl.rpsb, pl.nsplitb, true, 1, concurrency(kPassSample));
+        splitPlan(pl.Rb, planQ(mb), dpad, storage, pl.rpsb, pl.nsplitb, true, 1, planConc(kPassSample, mb));
         const double eb = (double)pl.j * (double)pl.Rb / (double)r;   // expected stored per query
         pl.capb = std::max<int>(32, pow2ceil((int64_t)(4.0 * eb / pl.nsplitb) + 16));
         // the full pass now expects jb nb / Rb survivors
@@ -582,6 +597,7 @@ struct FlatIndex::Impl {
         p.tau_key = tk; p.tau_id = ti;
         p.cand = cand.as<uint2>(); p.cnt = cnt.as<int>(); p.cap = cap;
         p.qgroup = qgroupKnob;
+        p.wide = curWide ? 1 : 0;
         return p;
     }
 
@@ -623,6 +639,7 @@ struct FlatIndex::Impl {
     // Search mb staged queries (storage type, qh or qbuf; norms in qnorm) and
     // write rows [0, mb) of the outputs.
     void searchBatch(int mb, int k, const Plan& pl, int32_t* oIds, float* oVals, hipStream_t s) {
+        curWide = pl.wide;
         const void* Q = storage == kF32 ? qbuf.p : qh.p;
         const float* qn = qnorm.as<float>();
         if (argminPath(mb, k)) {
@@ -773,8 +790,8 @@ struct FlatIndex::Impl {
         // regions do not depend on the split plan: it only spreads the work,
         // made for one block of queries (a window rarely holds more: the
         // launch covers rmax, and blocks past the device's count exit at once).
-        splitPlan(nb, std::min(rmax, kBN), dpad, storage, rr.rps, rr.nsplit, rr.batchSmall,
-                  rr.batchSmall ? 1 : kRetryMinTiles, concurrency(kPassRetry));
+        splitPlan(nb, curWide ? (std::min(rmax, 2 * kBN) + 1) / 2 : std::min(rmax, kBN), dpad, storage, rr.rps,
+                  rr.nsplit, rr.batchSmall, rr.batchSmall ? 1 : kRetryMinTiles, concurrency(kPassRetry, curWide));
         // j2 reruns, the usual kind: ~j2 nb / R0 candidates
         rr.expect = 1.5 * std::max(pl.j2, 2) * (double)nb / std::max<double>(1.0, (double)pl.R0) + 2.0 * k;
 
@@ -968,6 +985,7 @@ FlatIndex::FlatIndex(int dim, Metric metric, Storage storage) : d_(new Impl) {
     if (const char* v = std::getenv("MFLAT_STREAM_MAXQ")) d_->streamMaxQ = std::max(0, std::atoi(v));
     if (const char* v = std::getenv("MFLAT_STREAM_SPLITS")) d_->streamSplits = std::max(0, std::atoi(v));
     if (const char* v = std::getenv("MFLAT_QGROUP")) d_->qgroupKnob = std::max(0, std::atoi(v));
+    if (const char* v = std::getenv("MFLAT_WIDE")) d_->wideKnob = std::atoi(v) != 0 ? 1 : 0;
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
         (void)hipGetLastError();

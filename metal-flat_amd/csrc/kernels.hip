@@ -1092,6 +1092,279 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// scan_wide: fp16/bf16 tiles of 256 rows x 256 queries (large d)
+// ---------------------------------------------------------------------------
+//
+// For fp16/bf16 storage at a d whose 128-query tile does not fit
+// scan_resident's LDS, and batches of more than 128 queries. scan_filter's
+// 128 x 128 tile feeds each 32-cycle 16-bit MFMA one 16-byte LDS read a lane
+// (2 x 2 blocks a wave) and re-reads a query or database chunk from beyond L2
+// for every tile: operand staging and its latency bound it, not the matrix
+// cores. Here a workgroup (512 threads, one per CU: 147 KB of LDS; two
+// waves a SIMD as there) owns 256 rows x 256 queries and each of its 8
+// waves 64 rows x 128 queries as 2 x 4 blocks of 32 x 32, so an operand
+// fragment read from LDS feeds 2.7 MFMAs on average (2 there) and every
+// staged byte twice the work. Chunks, LDS layout,
+// fragment reads and the filter (MAXT, and PRE for L2) are scan_filter's, so
+// the keys are too; a search that starts on this kernel keeps it for all its
+// passes (sample, full, retry), as it does any scan family.
+// Database rows come in 128-row tiles (the split layout); a 256-row step
+// whose second half lies past the split's last tile loads zeros for it and
+// reports none of its rows. Query rows at or past nq load zeros.
+constexpr int kWT = 256;           // rows and queries of a wide tile
+constexpr int kWideThreads = 512;  // 8 waves of 64 rows x 128 queries
+
+template <int S, int METRIC, int PASS>
+__global__ void __launch_bounds__(512, 1) scan_wide_kernel(ScanParams p) {
+    static_assert(S != kF32, "the wide tile is the fp16/bf16 kernel");
+    static_assert(PASS != kPassArgmin, "k = 1 runs scan_filter");
+    constexpr int ES = 2;
+    constexpr bool PRE = METRIC == 0;
+    __shared__ __attribute__((aligned(16))) float sX[2 * kWT * kLds];
+    __shared__ __attribute__((aligned(16))) float sQ[2 * kWT * kLds];
+    __shared__ __attribute__((aligned(16))) float sXn[2 * kWT];   // PRE: -||x||^2 / 2 by step parity
+    __shared__ int sCnt[kWT];
+
+    const int nqb = (p.nq + kWT - 1) / kWT;
+    int qb, split;
+    {
+        const int nwg = gridDim.x;
+        const int bid = blockIdx.x;
+        if (PASS == kPassRetry && p.nq_dev) {   // block-major: the live blocks first
+            qb = bid / p.nsplit;
+            split = bid - qb * p.nsplit;
+        } else {   // scan_filter's XCD grouping
+            const int full = (nwg / 8) * 8;
+            const int v = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
+            const int qgrp = p.qgroup > 0 ? p.qgroup : kQGroup;
+            const int grpSize = nqb < qgrp ? nqb : qgrp;
+            const int grp = v / (grpSize * p.nsplit);
+            const int r = v - grp * grpSize * p.nsplit;
+            const int inGrp = nqb - grp * grpSize < grpSize ? nqb - grp * grpSize : grpSize;
+            split = r / inGrp;
+            qb = grp * grpSize + (r - split * inGrp);
+        }
+    }
+    const int nqv = (PASS == kPassRetry && p.nq_dev) ? *p.nq_dev : p.nq;
+    if (qb * kWT >= nqv) return;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave & 3;    // rows wm * 64 ..
+    const int wn = wave >> 2;   // queries wn * 128 ..
+    const int r32 = lane & 31;
+    const int h = lane >> 5;
+    if (tid < kWT) sCnt[tid] = 0;
+
+    // the lane's four query slots (bn: queries wn * 128 + bn * 32 + r32)
+    float tk[4], qn[4], ft[4];
+    int ti[4];
+    bool qv[4];
+    const int idb[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int bn = 0; bn < 4; ++bn) {
+        const int q = qb * kWT + wn * 128 + bn * 32 + r32;
+        qv[bn] = q < nqv;
+        tk[bn] = qv[bn] ? p.tau_key[q] : 0.0f;
+        ti[bn] = qv[bn] ? p.tau_id[q] : -1;
+        qn[bn] = (METRIC == 0 && qv[bn]) ? p.qnorm[q] : 0.0f;
+        if (METRIC == 0) {
+            const float m = 0x1p-20f * (tk[bn] + 2.0f * qn[bn] + 2.0f * p.xnorm_max);
+            ft[bn] = qv[bn] ? -0.5f * ((tk[bn] - qn[bn]) + m) : INFINITY;
+        } else {
+            ft[bn] = qv[bn] ? -tk[bn] : INFINITY;
+        }
+    }
+
+    const int64_t rowBeg = split_row(p, split);
+    const int64_t rowEnd = split_row(p, split + 1);
+    const int tiles = rowEnd > rowBeg ? (int)((rowEnd - rowBeg) / kBM) : 0;   // 128-row tiles
+    const int nsteps = (tiles + 1) / 2;
+    const int64_t rowLim = rowEnd < p.nrows ? rowEnd : p.nrows;
+    const int nk = (p.dpad + 63) / 64;
+    const bool halfTail = (p.dpad & 32) != 0;
+    const int total = nsteps * nk;
+
+    // staging as scan_filter's: database piece pc = tid % 256 of the 32-row
+    // blocks 2 i + tid / 256 (row 32 block + xRow, LDS float column xCol),
+    // query row ldRow + 64 i at float column ldCol; 4 of each a thread
+    const int pc = tid & 255;
+    const int xb = tid >> 8;
+    const int ldRow = tid >> 3;
+    const int ldCol = (tid & 7) * 4;
+    const int xRow = 16 * ((pc >> 6) & 1) + (pc & 15);
+    const int xCol = 16 * (pc >> 7) + 4 * ((pc >> 4) & 3);
+    const char* Xb = (const char*)p.X + rowBeg * p.dpad * ES;
+    const char* Qb = (const char*)p.Q + (int64_t)qb * kWT * p.dpad * ES;
+    fx4 rx[4], rq[4], rn = {0.0f, 0.0f, 0.0f, 0.0f};
+    // Every load is issued unconditionally from a valid address (an absent
+    // piece re-reads a present one: the split's first tile, query row 0, the
+    // chunk's first half) and zeroed when it is stored to LDS (validity bits
+    // in live), so the 16 loads of a chunk issue back to back instead of each
+    // behind its own branch and wait.
+    uint32_t live = 0;   // bit i: database piece i present; bit 8 + i: query piece i
+    bool whole = false;  // every piece of the chunk present (no selects at the store)
+    const bool allQ = qb * kWT + kWT <= p.nq;
+    auto gload = [&](int t, int kc) {
+        whole = allQ && 2 * t + 1 < tiles && !(halfTail && kc == nk - 1);
+        if (whole) {   // the usual case: plain loads
+            const char* xs = Xb + ((int64_t)t * 8 + xb) * 32 * p.dpad * ES + kc * 4096 + pc * 16;
+            const char* qs = Qb + (int64_t)ldRow * p.dpad * ES + kc * 128 + ldCol * 4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                rx[i] = *(const fx4*)(xs + (int64_t)i * 64 * p.dpad * ES);
+                rq[i] = *(const fx4*)(qs + (int64_t)i * 64 * p.dpad * ES);
+            }
+            if (PRE && kc == 0 && tid < kWT / 4) rn = *(const fx4*)(p.xnorm + rowBeg + (int64_t)t * kWT + tid * 4);
+            return;
+        }
+        const bool zx = halfTail && kc == nk - 1 && pc >= 128;
+        const bool zq = halfTail && kc == nk - 1 && (tid & 7) >= 4;
+        const char* xs = Xb + kc * 4096 + (zx ? pc - 128 : pc) * 16;
+        const int qo = kc * 128 + (zq ? ldCol - 16 : ldCol) * 4;
+        live = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int b = 2 * i + xb;   // 32-row block of the step (0..7)
+            const bool xv = !zx && 2 * t + (b >> 2) < tiles;
+            const bool qv8 = !zq && qb * kWT + ldRow + 64 * i < p.nq;
+            live |= (xv ? 1u : 0u) << i;
+            live |= (qv8 ? 1u : 0u) << (8 + i);
+            const int blk = 2 * t + (b >> 2) < tiles ? t * 8 + b : (b & 3);   // a 32-row block of the split
+            rx[i] = *(const fx4*)(xs + (int64_t)blk * 32 * p.dpad * ES);
+            const int qr = qb * kWT + ldRow + 64 * i < p.nq ? ldRow + 64 * i : -qb * kWT;   // else row 0
+            rq[i] = *(const fx4*)(Qb + (int64_t)qr * p.dpad * ES + qo);
+        }
+        if (PRE && kc == 0 && tid < kWT / 4) {
+            const bool nv = 2 * t + (tid >= kBM / 4 ? 1 : 0) < tiles;
+            live |= (nv ? 1u : 0u) << 16;
+            rn = *(const fx4*)(p.xnorm + rowBeg + (nv ? (int64_t)t * kWT + tid * 4 : (int64_t)(tid & 31) * 4));
+        }
+    };
+    auto lstore = [&](int t, int kc, int buf) {
+        const fx4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+        float* dx = sX + buf * (kWT * kLds);
+        float* dq = sQ + buf * (kWT * kLds);
+        if (whole) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                *(fx4*)(dx + (32 * (2 * i + xb) + xRow) * kLds + xCol) = rx[i];
+                *(fx4*)(dq + (ldRow + 64 * i) * kLds + ldCol) = rq[i];
+            }
+            if (PRE && kc == 0 && tid < kWT / 4) *(fx4*)(sXn + (t & 1) * kWT + tid * 4) = rn * -0.5f;
+            return;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            *(fx4*)(dx + (32 * (2 * i + xb) + xRow) * kLds + xCol) = (live >> i) & 1u ? rx[i] : z4;
+            *(fx4*)(dq + (ldRow + 64 * i) * kLds + ldCol) = (live >> (8 + i)) & 1u ? rq[i] : z4;
+        }
+        if (PRE && kc == 0 && tid < kWT / 4)
+            *(fx4*)(sXn + (t & 1) * kWT + tid * 4) = (live >> 16) & 1u ? rn * -0.5f : z4;
+    };
+
+    fx16 acc[2][4];
+    if (total > 0) {
+        gload(0, 0);
+        lstore(0, 0, 0);
+    }
+    __syncthreads();
+
+    const int aOff = (wm * 64 + r32) * kLds + h * 4;
+    const int bOff = (wn * 128 + r32) * kLds + h * 4;
+    // Chunk loop inside the step loop, the epilogue after it: the
+    // accumulators' only loop-carried path is MFMA to MFMA, so they stay in
+    // the accumulator registers (with the epilogue on a branch of one loop,
+    // every chunk copied all 256 of them to ordinary registers and back).
+    int it = 0;   // chunk counter over the whole split: LDS buffer it & 1
+    for (int t = 0; t < nsteps; ++t) {
+        for (int kc = 0; kc < nk; ++kc, ++it) {
+            const int buf = it & 1;
+            const bool lastK = kc == nk - 1;
+            const int nt = lastK ? t + 1 : t;
+            const int nkc = lastK ? 0 : kc + 1;
+            if (it + 1 < total) gload(nt, nkc);
+            const float* sx = sX + buf * (kWT * kLds);
+            const float* sq = sQ + buf * (kWT * kLds);
+            if (PRE && kc == 0) {
+                // acc[bm][0] = -||x||^2 / 2 of the lane's rows (register 4 g4 + i:
+                // row wm * 128 + bm * 32 + 8 g4 + 4 h + i), the C operand of the
+                // step's first MFMAs
+#pragma unroll
+                for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+                    for (int g4 = 0; g4 < 4; ++g4) {
+                        const fx4 v = *(const fx4*)(sXn + (t & 1) * kWT + wm * 64 + bm * 32 + g4 * 8 + h * 4);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[bm][0][g4 * 4 + i] = v[i];
+                    }
+            }
+            auto mma = [&](auto zeroTag) {
+                constexpr bool ZERO = decltype(zeroTag)::value;
+                const fx16 z = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f,
+                                0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    fx4 a[2], b[4];
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) a[j] = *(const fx4*)(sx + aOff + j * 32 * kLds + g * 8);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) b[j] = *(const fx4*)(sq + bOff + j * 32 * kLds + g * 8);
+                    const bool zc = ZERO && g == 0;
+#pragma unroll
+                    for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+                        for (int bn = 3; bn >= 0; --bn)
+                            acc[bm][bn] = mfma32x32x16<S>(a[bm], b[bn], zc ? (PRE ? acc[bm][0] : z) : acc[bm][bn]);
+                }
+            };
+            if (kc == 0)
+                mma(std::true_type{});
+            else
+                mma(std::false_type{});
+            if (it + 1 < total) lstore(nt, nkc, buf ^ 1);
+            __syncthreads();
+        }
+        // the step's epilogue: keys, bound test, survivors
+        const int64_t row0 = rowBeg + (int64_t)t * kWT;
+#pragma unroll
+        for (int bm = 0; bm < 2; ++bm) {
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int64_t r0 = row0 + wm * 64 + bm * 32 + g4 * 8 + h * 4;
+                const fx4 xn4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int bp = 0; bp < 2; ++bp) {
+                    // one group at a time: nothing of the next is
+                    // hoisted into this one's register budget
+                    __builtin_amdgcn_sched_barrier(0);
+                    filter_group<METRIC, PASS, 4, 2, false, true, PRE>(
+                        acc[bm], g4, 2 * bp, xn4, r0, rowLim, p.id_stride, idb, p, tk, ti, qn, ft, qv,
+                        QTab{nullptr, nullptr, nullptr, 0}, [&](int bn, float key, int id) {
+                            const int ql = wn * 128 + bn * 32 + r32;
+                            const int q = qb * kWT + ql;
+                            const uint2 v = make_uint2(__float_as_uint(key), (unsigned)id);
+                            if (PASS == kPassRetry && p.qcnt) {   // pooled region of the query
+                                const int gs = atomicAdd(&p.qcnt[(int64_t)q * kPoolCntStride], 1);
+                                if (gs < p.qcap[q]) p.cand[p.qoff[q] + gs] = v;
+                                return;
+                            }
+                            const int slot = atomicAdd(&sCnt[ql], 1);
+                            if (slot < p.cap) p.cand[((int64_t)q * p.nsplit + split) * p.cap + slot] = v;
+                        });
+                }
+            }
+        }
+    }
+    __syncthreads();   // every epilogue's slot counts
+    if (!(PASS == kPassRetry && p.qcnt) && tid < kWT) {
+        const int q = qb * kWT + tid;
+        if (q < nqv) p.cnt[(int64_t)q * p.nsplit + split] = sCnt[tid];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // scan_resident: query tile resident in LDS, database streamed per wave
 // ---------------------------------------------------------------------------
 //
@@ -2881,6 +3154,21 @@ static const void* tiled_fn(int pass) {
     if (pass == kPassArgmin) return (const void*)scan_filter_kernel<S, M, kPassArgmin>;
     return (const void*)scan_filter_kernel<S, M, kPassFull>;
 }
+template <int S, int M>
+static const void* wide_fn(int pass) {
+    if (pass == kPassSample) return (const void*)scan_wide_kernel<S, M, kPassSample>;
+    if (pass == kPassRetry) return (const void*)scan_wide_kernel<S, M, kPassRetry>;
+    return (const void*)scan_wide_kernel<S, M, kPassFull>;
+}
+template <int S>
+static const void* wide_fn_s(int metric, int pass) {
+    return metric == 0 ? wide_fn<S, 0>(pass) : wide_fn<S, 1>(pass);
+}
+
+bool wide_scan_applies(int nq, int dpad, int storage) {
+    return storage != kF32 && nq > kBN && !resident_scan_fits(dpad, storage);
+}
+
 template <int S>
 static const void* scan_fn(int dpad, int metric, int pass, size_t& lds) {
     if (resident_scan_fits(dpad, S)) {
@@ -2891,15 +3179,19 @@ static const void* scan_fn(int dpad, int metric, int pass, size_t& lds) {
     return metric == 0 ? tiled_fn<S, 0>(pass) : tiled_fn<S, 1>(pass);
 }
 
-int scan_concurrency(int dpad, int storage, int metric, int pass) {
+int scan_concurrency(int dpad, int storage, int metric, int pass, bool wide) {
     size_t lds = 0;
-    const void* f = storage == kF32 ? scan_fn<kF32>(dpad, metric, pass, lds)
+    const void* f = (wide && storage != kF32 && pass != kPassArgmin && !resident_scan_fits(dpad, storage))
+                        ? (storage == kF16 ? wide_fn_s<kF16>(metric, pass) : wide_fn_s<kBF16>(metric, pass))
+                    : storage == kF32 ? scan_fn<kF32>(dpad, metric, pass, lds)
                     : storage == kF16 ? scan_fn<kF16>(dpad, metric, pass, lds)
                                       : scan_fn<kBF16>(dpad, metric, pass, lds);
+    const int threads = (wide && storage != kF32 && pass != kPassArgmin && !resident_scan_fits(dpad, storage))
+                            ? kWideThreads : 256;
     int dev = 0, cus = 0, per = 0;
     if (!f || hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, f, 256, lds) != hipSuccess) {
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, f, threads, lds) != hipSuccess) {
         (void)hipGetLastError();
         return 0;
     }
@@ -2940,6 +3232,23 @@ void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, 
         else launch_resident_s<kBF16>(p, metric, pass, g, lds, s);
         prof_end(tok, s);
         check_launch("scan_resident");
+        return;
+    }
+    // fp16/bf16 batches the caller put on the wide tile: 256-query blocks
+    if (p.wide && storage != kF32 && pass != kPassArgmin) {
+        const int nqb2 = (p.nq + kWT - 1) / kWT;
+        const int64_t gw = (int64_t)nqb2 * p.nsplit;
+        if (gw > 0x7FFFFFFF) throw std::runtime_error("scan_wide grid too large");
+        ScanParams pw = p;
+        if (pw.qgroup <= 0) {
+            const int64_t tileBytes = (int64_t)kWT * p.dpad * 2;
+            pw.qgroup = (int)std::max<int64_t>(1, std::min<int64_t>(kQGroup, ((int64_t)5 << 19) / tileBytes));
+        }
+        const void* f = storage == kF16 ? wide_fn_s<kF16>(metric, pass) : wide_fn_s<kBF16>(metric, pass);
+        void* args[] = {(void*)&pw};
+        const hipError_t e = hipLaunchKernel(f, dim3((unsigned)gw), dim3(kWideThreads), args, 0, s);
+        prof_end(tok, s);
+        if (e != hipSuccess) throw std::runtime_error(std::string("scan_wide launch: ") + hipGetErrorString(e));
         return;
     }
     // LDS-tiled kernel: every database tile re-reads the group's query tiles

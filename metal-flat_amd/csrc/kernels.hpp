@@ -139,6 +139,10 @@ struct ScanParams {
     const float* qraw;
     int qdim;
     int qcos;
+    // fp16/bf16 at a d beyond scan_resident, batches of more than 128
+    // queries: 1 runs the wide-tile kernel (256 queries a block; grid
+    // ceil(nq / 256) x nsplit). The caller sets it for every pass of a batch.
+    int wide;
 };
 
 // Device-built retry work lists (flat search). After a full pass's select, a
@@ -278,7 +282,10 @@ bool resident_scan_fits(int dpad, int storage);
 bool ivf_narrow_fits(int dpad, int storage);
 // Workgroups of the scan that launch_scan_filter runs (outside scan_small's
 // range) that fit the current device at once (occupancy x CUs); 0 if unknown.
-int scan_concurrency(int dpad, int storage, int metric, int pass);
+int scan_concurrency(int dpad, int storage, int metric, int pass, bool wide = false);
+// Whether a batch of nq queries takes the wide-tile kernel (fp16/bf16, a d
+// beyond scan_resident's LDS, more than 128 queries).
+bool wide_scan_applies(int nq, int dpad, int storage);
 void launch_scan_filter(const ScanParams& p, int metric, int pass, int storage, hipStream_t s,
                         bool allowSmall = true);
 // IVF fine scan (scan_resident over the work items of ScanParams::ivf_*; the
