@@ -1124,6 +1124,11 @@ __global__ void __launch_bounds__(512, 1) scan_wide_kernel(ScanParams p) {
     __shared__ __attribute__((aligned(16))) float sQ[2 * kWT * kLds];
     __shared__ __attribute__((aligned(16))) float sXn[2 * kWT];   // PRE: -||x||^2 / 2 by step parity
     __shared__ int sCnt[kWT];
+    // survivor-only query state (bound key and id, query norm) in LDS, not
+    // registers: filter_group's LQ tables
+    __shared__ float sLTk[kWT];
+    __shared__ int sLTi[kWT];
+    __shared__ float sLQn[kWT];
 
     const int nqb = (p.nq + kWT - 1) / kWT;
     int qb, split;
@@ -1155,7 +1160,14 @@ __global__ void __launch_bounds__(512, 1) scan_wide_kernel(ScanParams p) {
     const int wn = wave >> 2;   // queries wn * 128 ..
     const int r32 = lane & 31;
     const int h = lane >> 5;
-    if (tid < kWT) sCnt[tid] = 0;
+    if (tid < kWT) {
+        sCnt[tid] = 0;
+        const int q = qb * kWT + tid;
+        const bool v = q < nqv;
+        sLTk[tid] = v ? p.tau_key[q] : 0.0f;
+        sLTi[tid] = v ? p.tau_id[q] : -1;
+        sLQn[tid] = (METRIC == 0 && v) ? p.qnorm[q] : 0.0f;
+    }
 
     // the lane's four query slots (bn: queries wn * 128 + bn * 32 + r32)
     float tk[4], qn[4], ft[4];
@@ -1339,9 +1351,9 @@ __global__ void __launch_bounds__(512, 1) scan_wide_kernel(ScanParams p) {
                     // one group at a time: nothing of the next is
                     // hoisted into this one's register budget
                     __builtin_amdgcn_sched_barrier(0);
-                    filter_group<METRIC, PASS, 4, 2, false, true, PRE>(
+                    filter_group<METRIC, PASS, 4, 2, true, true, PRE>(
                         acc[bm], g4, 2 * bp, xn4, r0, rowLim, p.id_stride, idb, p, tk, ti, qn, ft, qv,
-                        QTab{nullptr, nullptr, nullptr, 0}, [&](int bn, float key, int id) {
+                        QTab{sLTk + wn * 128, sLTi + wn * 128, sLQn + wn * 128, r32}, [&](int bn, float key, int id) {
                             const int ql = wn * 128 + bn * 32 + r32;
                             const int q = qb * kWT + ql;
                             const uint2 v = make_uint2(__float_as_uint(key), (unsigned)id);
