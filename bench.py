@@ -585,10 +585,14 @@ def flat_bench(cfg, nq_override, storage_name, steps, warmup, cpu=True, host_api
 
 # The other BASELINE.json configurations, measured in the default run beside the
 # C2 headline: (key, config, query count, storage). C4 is measured at each of
-# its batch sizes, with fp32 and fp16 storage.
+# its batch sizes, with fp32 and fp16 storage; C2 and C3 also with 16-bit
+# storage (their reduced-precision kernels: scan_resident, scan_wide).
 EXTRA_CONFIGS = [
     ("C1", "C1", 0, "f32"),
+    ("C2_f16", "C2", 0, "f16"),
+    ("C2_bf16", "C2", 0, "bf16"),
     ("C3", "C3", 0, "f32"),
+    ("C3_bf16", "C3", 0, "bf16"),
     ("C4_nq1", "C4", 1, "f32"),
     ("C4_nq16", "C4", 16, "f32"),
     ("C4_nq64", "C4", 64, "f32"),
@@ -606,9 +610,9 @@ def extra_configs(args):
     entry and does not drop the others or the headline."""
     out = {}
     cache = {}
-    # steps per workload: about 0.2 s or more of timed searches (C1, C4 run
-    # 0.4-1.3 ms a search; C3 ~120 ms; C5 ~250 ms)
-    steps_of = {"C1": 200, "C3": 5, "C4": 200, "C5": 5}
+    # steps per workload: about 0.1 s or more of timed searches (C1, C4 run
+    # 0.3-1.3 ms a search; C2 at 16-bit storage ~3.4 ms; C3 ~20-120 ms; C5 ~250 ms)
+    steps_of = {"C1": 200, "C2": 40, "C3": 5, "C4": 200, "C5": 5}
     for key, cfg, nq, storage in EXTRA_CONFIGS:
         steps = steps_of[cfg]
         try:
@@ -642,7 +646,8 @@ def main():
                     help="element type of the stored database and the queries")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
-                    help="default run: skip the extra_configs (C1, C3, C4 nq 1/16/64 fp32 and fp16, C5)")
+                    help="default run: skip the extra_configs (C1, C2 fp16/bf16, C3 fp32/bf16, "
+                         "C4 nq 1/16/64 fp32 and fp16, C5)")
     ap.add_argument("--kmeans", type=int, default=0, metavar="ITERS",
                     help="time the device k-means loop (mflat_kmeans_train) on C5's points and centroid "
                          "count instead: one JSON line with ms per training iteration")
