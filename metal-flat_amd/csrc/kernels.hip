@@ -1100,19 +1100,61 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
 // 128 x 128 tile feeds each 32-cycle 16-bit MFMA one 16-byte LDS read a lane
 // (2 x 2 blocks a wave) and re-reads a query or database chunk from beyond L2
 // for every tile: operand staging and its latency bound it, not the matrix
-// cores. Here a workgroup (512 threads, one per CU: 147 KB of LDS; two
-// waves a SIMD as there) owns 256 rows x 256 queries and each of its 8
-// waves 64 rows x 128 queries as 2 x 4 blocks of 32 x 32, so an operand
-// fragment read from LDS feeds 2.7 MFMAs on average (2 there) and every
-// staged byte twice the work. Chunks, LDS layout,
-// fragment reads and the filter (MAXT, and PRE for L2) are scan_filter's, so
-// the keys are too; a search that starts on this kernel keeps it for all its
-// passes (sample, full, retry), as it does any scan family.
+// cores. Here a workgroup (512 threads, one per CU; two waves a SIMD as
+// there) owns 256 rows x 256 queries and each of its 8 waves 64 rows x 128
+// queries as 2 x 4 blocks of 32 x 32, so an operand fragment read from LDS
+// feeds 2.7 MFMAs on average (2 there) and every staged byte twice the work.
+//
+// Staging: 32-column stages, copied from global memory straight into LDS
+// (global_load_lds_dwordx4: no staging registers, no LDS write
+// instructions), four stages in LDS and three in flight while one is
+// consumed. A stage holds, for each of the 8 database row blocks and 8 query
+// blocks of 32, one 2 KB unit in the chunked layout of blk_off_h: piece
+// ((r / 16) * 4 + c / 8) * 16 + r % 16 for row r and column c of the unit,
+// which is the database's own order in HBM (a unit is copied verbatim) and
+// the order a 32 x 16 MFMA fragment reads in runs of 16 pieces (no bank
+// conflicts). Query rows are row-major in HBM; each lane copies the piece of
+// that order. One barrier a stage, preceded by a wait for this wave's copies
+// of the stage (vector-memory counter, in order) but none of the later ones;
+// __syncthreads' fence would wait for all of them.
+//
+// The MFMA sequence per (query, row) pair is scan_filter's, so the keys are
+// too: columns in ascending 16-column steps, the L2 accumulators starting
+// from -||x||^2 / 2 (PRE), and for dpad = 64 c + 32 two more steps over
+// zero operands at the end of each row block, the zero half of scan_filter's
+// last 64-column chunk. A search that starts on this kernel keeps it for all
+// its passes (sample, full, retry), as it does any scan family.
 // Database rows come in 128-row tiles (the split layout); a 256-row step
-// whose second half lies past the split's last tile loads zeros for it and
-// reports none of its rows. Query rows at or past nq load zeros.
-constexpr int kWT = 256;           // rows and queries of a wide tile
-constexpr int kWideThreads = 512;  // 8 waves of 64 rows x 128 queries
+// whose second half lies past the split's last tile copies the split's first
+// tile for it and reports none of its rows; query rows at or past nq copy the
+// block's first query and are masked (no bound admits them).
+constexpr int kWT = 256;                        // rows and queries of a wide tile
+constexpr int kWideThreads = 512;               // 8 waves of 64 rows x 128 queries
+constexpr int kWideStages = 4;                  // 32-column LDS stages
+constexpr int kWideStageBytes = 2 * kWT * 64;   // both operands, 64 bytes a row
+
+// 16 bytes a lane from global memory straight into LDS: lane l's piece lands
+// at lds + 16 l (the LDS address is the wave's, the same for every lane). In
+// asm, so the compiler does not see an LDS write in flight: it would wait for
+// every copy (vmcnt(0)) before any LDS atomic of the epilogue; the kernel
+// waits for its copies itself (wide_sync). M0 holds the LDS address; the nop
+// is the M0-write-to-use wait state.
+__device__ __forceinline__ void lds_copy16(const void* g, void* lds) {
+    const uint32_t l = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(l) : "memory", "m0");
+}
+
+// Wait until at most N of this wave's vector-memory operations are still
+// outstanding and its LDS operations are done, then the workgroup barrier.
+template <int N>
+__device__ __forceinline__ void wide_sync() {
+    static_assert(N >= 0 && N < 16, "the low vmcnt field");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0x0070 | N);   // vmcnt(N) expcnt(7) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 
 template <int S, int METRIC, int PASS>
 __global__ void __launch_bounds__(512, 1) scan_wide_kernel(ScanParams p) {
@@ -1120,9 +1162,8 @@ __global__ void __launch_bounds__(512, 1) scan_wide_kernel(ScanParams p) {
     static_assert(PASS != kPassArgmin, "k = 1 runs scan_filter");
     constexpr int ES = 2;
     constexpr bool PRE = METRIC == 0;
-    __shared__ __attribute__((aligned(16))) float sX[2 * kWT * kLds];
-    __shared__ __attribute__((aligned(16))) float sQ[2 * kWT * kLds];
-    __shared__ __attribute__((aligned(16))) float sXn[2 * kWT];   // PRE: -||x||^2 / 2 by step parity
+    __shared__ __attribute__((aligned(16))) char sOp[kWideStages * kWideStageBytes];
+    __shared__ __attribute__((aligned(16))) float sXn[2 * kWT];   // PRE: ||x||^2 of the step, by step parity
     __shared__ int sCnt[kWT];
     // survivor-only query state (bound key and id, query norm) in LDS, not
     // registers: filter_group's LQ tables
@@ -1194,114 +1235,76 @@ __global__ void __launch_bounds__(512, 1) scan_wide_kernel(ScanParams p) {
     const int tiles = rowEnd > rowBeg ? (int)((rowEnd - rowBeg) / kBM) : 0;   // 128-row tiles
     const int nsteps = (tiles + 1) / 2;
     const int64_t rowLim = rowEnd < p.nrows ? rowEnd : p.nrows;
-    const int nk = (p.dpad + 63) / 64;
-    const bool halfTail = (p.dpad & 32) != 0;
+    const int nk = p.dpad / 32;              // 32-column units of a row
+    const bool halfTail = (nk & 1) != 0;     // dpad = 64 c + 32
     const int total = nsteps * nk;
 
-    // staging as scan_filter's: database piece pc = tid % 256 of the 32-row
-    // blocks 2 i + tid / 256 (row 32 block + xRow, LDS float column xCol),
-    // query row ldRow + 64 i at float column ldCol; 4 of each a thread
-    const int pc = tid & 255;
-    const int xb = tid >> 8;
-    const int ldRow = tid >> 3;
-    const int ldCol = (tid & 7) * 4;
-    const int xRow = 16 * ((pc >> 6) & 1) + (pc & 15);
-    const int xCol = 16 * (pc >> 7) + 4 * ((pc >> 4) & 3);
+    // Copies of a stage (step t, unit u): wave w brings database row block w
+    // of the step (two 1 KB halves of its 2 KB unit) and query block w (rows
+    // 32 w + 16 r + lane % 16, the lane's 16 bytes at column 8 (lane / 16)
+    // of the unit), plus, at u = 0, wave 0 the step's 256 row norms.
     const char* Xb = (const char*)p.X + rowBeg * p.dpad * ES;
-    const char* Qb = (const char*)p.Q + (int64_t)qb * kWT * p.dpad * ES;
-    fx4 rx[4], rq[4], rn = {0.0f, 0.0f, 0.0f, 0.0f};
-    // Every load is issued unconditionally from a valid address (an absent
-    // piece re-reads a present one: the split's first tile, query row 0, the
-    // chunk's first half) and zeroed when it is stored to LDS (validity bits
-    // in live), so the 16 loads of a chunk issue back to back instead of each
-    // behind its own branch and wait.
-    uint32_t live = 0;   // bit i: database piece i present; bit 8 + i: query piece i
-    bool whole = false;  // every piece of the chunk present (no selects at the store)
-    const bool allQ = qb * kWT + kWT <= p.nq;
-    auto gload = [&](int t, int kc) {
-        whole = allQ && 2 * t + 1 < tiles && !(halfTail && kc == nk - 1);
-        if (whole) {   // the usual case: plain loads
-            const char* xs = Xb + ((int64_t)t * 8 + xb) * 32 * p.dpad * ES + kc * 4096 + pc * 16;
-            const char* qs = Qb + (int64_t)ldRow * p.dpad * ES + kc * 128 + ldCol * 4;
+    const int64_t xBlk = (int64_t)32 * p.dpad * ES;
+    const char* qsrc[2];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                rx[i] = *(const fx4*)(xs + (int64_t)i * 64 * p.dpad * ES);
-                rq[i] = *(const fx4*)(qs + (int64_t)i * 64 * p.dpad * ES);
-            }
-            if (PRE && kc == 0 && tid < kWT / 4) rn = *(const fx4*)(p.xnorm + rowBeg + (int64_t)t * kWT + tid * 4);
-            return;
-        }
-        const bool zx = halfTail && kc == nk - 1 && pc >= 128;
-        const bool zq = halfTail && kc == nk - 1 && (tid & 7) >= 4;
-        const char* xs = Xb + kc * 4096 + (zx ? pc - 128 : pc) * 16;
-        const int qo = kc * 128 + (zq ? ldCol - 16 : ldCol) * 4;
-        live = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int b = 2 * i + xb;   // 32-row block of the step (0..7)
-            const bool xv = !zx && 2 * t + (b >> 2) < tiles;
-            const bool qv8 = !zq && qb * kWT + ldRow + 64 * i < p.nq;
-            live |= (xv ? 1u : 0u) << i;
-            live |= (qv8 ? 1u : 0u) << (8 + i);
-            const int blk = 2 * t + (b >> 2) < tiles ? t * 8 + b : (b & 3);   // a 32-row block of the split
-            rx[i] = *(const fx4*)(xs + (int64_t)blk * 32 * p.dpad * ES);
-            const int qr = qb * kWT + ldRow + 64 * i < p.nq ? ldRow + 64 * i : -qb * kWT;   // else row 0
-            rq[i] = *(const fx4*)(Qb + (int64_t)qr * p.dpad * ES + qo);
-        }
-        if (PRE && kc == 0 && tid < kWT / 4) {
-            const bool nv = 2 * t + (tid >= kBM / 4 ? 1 : 0) < tiles;
-            live |= (nv ? 1u : 0u) << 16;
-            rn = *(const fx4*)(p.xnorm + rowBeg + (nv ? (int64_t)t * kWT + tid * 4 : (int64_t)(tid & 31) * 4));
+    for (int r = 0; r < 2; ++r) {
+        const int row = qb * kWT + wave * 32 + r * 16 + (lane & 15);
+        qsrc[r] = (const char*)p.Q + (int64_t)(row < p.nq ? row : qb * kWT) * p.dpad * ES + (lane >> 4) * 16;
+    }
+    auto copyStage = [&](int t, int u, int buf) {
+        char* dst = sOp + buf * kWideStageBytes + wave * 2048;
+        const int blk = 2 * t + (wave >> 2) < tiles ? t * 8 + wave : (wave & 3);
+        const char* xs = Xb + blk * xBlk + u * 2048 + lane * 16;
+        lds_copy16(xs, dst);
+        lds_copy16(xs + 1024, dst + 1024);
+        lds_copy16(qsrc[0] + u * 64, dst + kWideStageBytes / 2);
+        lds_copy16(qsrc[1] + u * 64, dst + kWideStageBytes / 2 + 1024);
+        if (PRE && u == 0 && wave == 0) {
+            const bool nv = 2 * t + (lane >= 32 ? 1 : 0) < tiles;
+            lds_copy16(p.xnorm + rowBeg + (nv ? (int64_t)t * kWT + lane * 4 : (int64_t)(lane & 31) * 4),
+                       sXn + (t & 1) * kWT);
         }
     };
-    auto lstore = [&](int t, int kc, int buf) {
-        const fx4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
-        float* dx = sX + buf * (kWT * kLds);
-        float* dq = sQ + buf * (kWT * kLds);
-        if (whole) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                *(fx4*)(dx + (32 * (2 * i + xb) + xRow) * kLds + xCol) = rx[i];
-                *(fx4*)(dq + (ldRow + 64 * i) * kLds + ldCol) = rq[i];
-            }
-            if (PRE && kc == 0 && tid < kWT / 4) *(fx4*)(sXn + (t & 1) * kWT + tid * 4) = rn * -0.5f;
-            return;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            *(fx4*)(dx + (32 * (2 * i + xb) + xRow) * kLds + xCol) = (live >> i) & 1u ? rx[i] : z4;
-            *(fx4*)(dq + (ldRow + 64 * i) * kLds + ldCol) = (live >> (8 + i)) & 1u ? rq[i] : z4;
-        }
-        if (PRE && kc == 0 && tid < kWT / 4)
-            *(fx4*)(sXn + (t & 1) * kWT + tid * 4) = (live >> 16) & 1u ? rn * -0.5f : z4;
-    };
+
+    // fragment of 32 rows (or queries) x 16 columns, step g of the stage:
+    // unit piece ((r32 / 16) * 4 + 2 g + h) * 16 + r32 % 16
+    const int laneOff = (r32 >> 4) * 1024 + h * 256 + (r32 & 15) * 16;
+    const int aOff = wm * 2 * 2048 + laneOff;                          // + bm * 2048
+    const int bOff = kWideStageBytes / 2 + wn * 4 * 2048 + laneOff;    // + bn * 2048
 
     fx16 acc[2][4];
-    if (total > 0) {
-        gload(0, 0);
-        lstore(0, 0, 0);
-    }
-    __syncthreads();
-
-    const int aOff = (wm * 64 + r32) * kLds + h * 4;
-    const int bOff = (wn * 128 + r32) * kLds + h * 4;
-    // Chunk loop inside the step loop, the epilogue after it: the
+    if (total > 0) copyStage(0, 0, 0);
+    if (total > 1) copyStage(1 / nk, 1 % nk, 1);
+    if (total > 2) copyStage(2 / nk, 2 % nk, 2);
+    int ct = 3 / nk, cu = 3 % nk;   // the next stage to copy
+    // Unit loop inside the step loop, the epilogue after it: the
     // accumulators' only loop-carried path is MFMA to MFMA, so they stay in
-    // the accumulator registers (with the epilogue on a branch of one loop,
-    // every chunk copied all 256 of them to ordinary registers and back).
-    int it = 0;   // chunk counter over the whole split: LDS buffer it & 1
+    // the accumulator registers.
+    int it = 0;   // stage counter over the whole split: LDS buffer it % 4
     for (int t = 0; t < nsteps; ++t) {
-        for (int kc = 0; kc < nk; ++kc, ++it) {
-            const int buf = it & 1;
-            const bool lastK = kc == nk - 1;
-            const int nt = lastK ? t + 1 : t;
-            const int nkc = lastK ? 0 : kc + 1;
-            if (it + 1 < total) gload(nt, nkc);
-            const float* sx = sX + buf * (kWT * kLds);
-            const float* sq = sQ + buf * (kWT * kLds);
-            if (PRE && kc == 0) {
+        for (int u = 0; u < nk; ++u, ++it) {
+            // stage it is here once this wave's copies of it are (later
+            // stages' copies may stay in flight) and every wave's are: the
+            // barrier; after it, every wave is done with stage it - 1, whose
+            // buffer the copy of stage it + 3 takes
+            const int after = total - 1 - it;
+            if (after >= 2)
+                wide_sync<8>();
+            else if (after == 1)
+                wide_sync<4>();
+            else
+                wide_sync<0>();
+            if (it + 3 < total) {
+                copyStage(ct, cu, (it + 3) & 3);
+                if (++cu == nk) {
+                    cu = 0;
+                    ++ct;
+                }
+            }
+            const char* st = sOp + (it & 3) * kWideStageBytes;
+            if (PRE && u == 0) {
                 // acc[bm][0] = -||x||^2 / 2 of the lane's rows (register 4 g4 + i:
-                // row wm * 128 + bm * 32 + 8 g4 + 4 h + i), the C operand of the
+                // row wm * 64 + bm * 32 + 8 g4 + 4 h + i), the C operand of the
                 // step's first MFMAs
 #pragma unroll
                 for (int bm = 0; bm < 2; ++bm)
@@ -1309,7 +1312,7 @@ __global__ void __launch_bounds__(512, 1) scan_wide_kernel(ScanParams p) {
                     for (int g4 = 0; g4 < 4; ++g4) {
                         const fx4 v = *(const fx4*)(sXn + (t & 1) * kWT + wm * 64 + bm * 32 + g4 * 8 + h * 4);
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) acc[bm][0][g4 * 4 + i] = v[i];
+                        for (int i = 0; i < 4; ++i) acc[bm][0][g4 * 4 + i] = v[i] * -0.5f;
                     }
             }
             auto mma = [&](auto zeroTag) {
@@ -1317,12 +1320,12 @@ __global__ void __launch_bounds__(512, 1) scan_wide_kernel(ScanParams p) {
                 const fx16 z = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f,
                                 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
+                for (int g = 0; g < 2; ++g) {
                     fx4 a[2], b[4];
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) a[j] = *(const fx4*)(sx + aOff + j * 32 * kLds + g * 8);
+                    for (int j = 0; j < 2; ++j) a[j] = *(const fx4*)(st + aOff + j * 2048 + g * 512);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) b[j] = *(const fx4*)(sq + bOff + j * 32 * kLds + g * 8);
+                    for (int j = 0; j < 4; ++j) b[j] = *(const fx4*)(st + bOff + j * 2048 + g * 512);
                     const bool zc = ZERO && g == 0;
 #pragma unroll
                     for (int bm = 0; bm < 2; ++bm)
@@ -1331,12 +1334,19 @@ __global__ void __launch_bounds__(512, 1) scan_wide_kernel(ScanParams p) {
                             acc[bm][bn] = mfma32x32x16<S>(a[bm], b[bn], zc ? (PRE ? acc[bm][0] : z) : acc[bm][bn]);
                 }
             };
-            if (kc == 0)
+            if (u == 0)
                 mma(std::true_type{});
             else
                 mma(std::false_type{});
-            if (it + 1 < total) lstore(nt, nkc, buf ^ 1);
-            __syncthreads();
+            if (halfTail && u == nk - 1) {   // scan_filter's zero half-chunk: acc + 0
+                const fx4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int g = 0; g < 2; ++g)
+#pragma unroll
+                    for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+                        for (int bn = 3; bn >= 0; --bn) acc[bm][bn] = mfma32x32x16<S>(z4, z4, acc[bm][bn]);
+            }
         }
         // the step's epilogue: keys, bound test, survivors
         const int64_t row0 = rowBeg + (int64_t)t * kWT;
