@@ -1116,7 +1116,9 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
 // conflicts). Query rows are row-major in HBM; each lane copies the piece of
 // that order. One barrier a stage, preceded by a wait for this wave's copies
 // of the stage (vector-memory counter, in order) but none of the later ones;
-// __syncthreads' fence would wait for all of them.
+// __syncthreads' fence would wait for all of them. The next copy is issued
+// after the stage's first 16-column step (fragment reads first: 3% faster
+// than issuing it right after the barrier).
 //
 // The MFMA sequence per (query, row) pair is scan_filter's, so the keys are
 // too: columns in ascending 16-column steps, the L2 accumulators starting
@@ -1286,7 +1288,7 @@ __global__ void __launch_bounds__(512, 1) scan_wide_kernel(ScanParams p) {
             // stage it is here once this wave's copies of it are (later
             // stages' copies may stay in flight) and every wave's are: the
             // barrier; after it, every wave is done with stage it - 1, whose
-            // buffer the copy of stage it + 3 takes
+            // buffer the copy of stage it + 3 takes (issued below)
             const int after = total - 1 - it;
             if (after >= 2)
                 wide_sync<8>();
@@ -1294,13 +1296,6 @@ __global__ void __launch_bounds__(512, 1) scan_wide_kernel(ScanParams p) {
                 wide_sync<4>();
             else
                 wide_sync<0>();
-            if (it + 3 < total) {
-                copyStage(ct, cu, (it + 3) & 3);
-                if (++cu == nk) {
-                    cu = 0;
-                    ++ct;
-                }
-            }
             const char* st = sOp + (it & 3) * kWideStageBytes;
             if (PRE && u == 0) {
                 // acc[bm][0] = -||x||^2 / 2 of the lane's rows (register 4 g4 + i:
@@ -1332,6 +1327,16 @@ __global__ void __launch_bounds__(512, 1) scan_wide_kernel(ScanParams p) {
 #pragma unroll
                         for (int bn = 3; bn >= 0; --bn)
                             acc[bm][bn] = mfma32x32x16<S>(a[bm], b[bn], zc ? (PRE ? acc[bm][0] : z) : acc[bm][bn]);
+                    // the copy of stage it + 3 (into stage it - 1's buffer, free
+                    // since the barrier) after the first step's MFMAs: the
+                    // fragment reads go first
+                    if (g == 0 && it + 3 < total) {
+                        copyStage(ct, cu, (it + 3) & 3);
+                        if (++cu == nk) {
+                            cu = 0;
+                            ++ct;
+                        }
+                    }
                 }
             };
             if (u == 0)
