@@ -786,12 +786,15 @@ struct FlatIndex::Impl {
         rr.rowBytes = dpad * esize;
         // Retries run the kernel family of the passes their bounds came from
         // (the whole batch's), so every bound is compared with keys computed
-        // the same way (a guaranteed bound must admit its own rows). Pooled
-        // regions do not depend on the split plan: it only spreads the work,
-        // made for one block of queries (a window rarely holds more: the
-        // launch covers rmax, and blocks past the device's count exit at once).
-        splitPlan(nb, curWide ? (std::min(rmax, 2 * kBN) + 1) / 2 : std::min(rmax, kBN), dpad, storage, rr.rps,
-                  rr.nsplit, rr.batchSmall, rr.batchSmall ? 1 : kRetryMinTiles, concurrency(kPassRetry, curWide));
+        // the same way (a guaranteed bound must admit its own rows); a wide
+        // batch's window runs the 128-query tiled kernel, whose keys are the
+        // wide kernel's, so a window of up to 128 queries costs one 128-query
+        // block. Pooled regions do not depend on the split plan: it only
+        // spreads the work, made for one block of queries (a window rarely
+        // holds more: the launch covers rmax, and blocks past the device's
+        // count exit at once).
+        splitPlan(nb, std::min(rmax, kBN), dpad, storage, rr.rps, rr.nsplit, rr.batchSmall,
+                  rr.batchSmall ? 1 : kRetryMinTiles, concurrency(kPassRetry, false));
         // j2 reruns, the usual kind: ~j2 nb / R0 candidates
         rr.expect = 1.5 * std::max(pl.j2, 2) * (double)nb / std::max<double>(1.0, (double)pl.R0) + 2.0 * k;
 
@@ -839,6 +842,7 @@ struct FlatIndex::Impl {
                                       L.tk, L.ti, 1);
             p.nq_dev = L.counters + 1;
             p.qcnt = L.qcnt; p.qoff = L.qoff; p.qcap = L.qcap;
+            p.wide = 0;   // the tiled kernel (same keys as the wide one)
             launch_scan_filter(p, kernMetric(), kPassRetry, storage, s, rr.batchSmall);
             SelectParams sp = selectParams(rr.rmax, 1, 1, k, k);
             sp.cnt = L.qcnt;

@@ -1124,8 +1124,9 @@ __global__ void __launch_bounds__(256, 2) scan_filter_kernel(ScanParams p) {
 // too: columns in ascending 16-column steps, the L2 accumulators starting
 // from -||x||^2 / 2 (PRE), and for dpad = 64 c + 32 two more steps over
 // zero operands at the end of each row block, the zero half of scan_filter's
-// last 64-column chunk. A search that starts on this kernel keeps it for all
-// its passes (sample, full, retry), as it does any scan family.
+// last 64-column chunk. A search that starts on this kernel runs its sample
+// and full passes on it and its retry window (usually under 128 queries) on
+// scan_filter: the keys agree, so every bound meets keys computed the same way.
 // Database rows come in 128-row tiles (the split layout); a 256-row step
 // whose second half lies past the split's last tile copies the split's first
 // tile for it and reports none of its rows; query rows at or past nq copy the
