@@ -1142,10 +1142,12 @@ constexpr int kWideStageBytes = 2 * kWT * 64;   // both operands, 64 bytes a row
 // every copy (vmcnt(0)) before any LDS atomic of the epilogue; the kernel
 // waits for its copies itself (wide_sync). M0 holds the LDS address; the nop
 // is the M0-write-to-use wait state.
-__device__ __forceinline__ void lds_copy16(const void* g, void* lds) {
-    const uint32_t l = __builtin_amdgcn_readfirstlane(
-        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(l) : "memory", "m0");
+__device__ __forceinline__ void lds_copy16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds) : "memory", "m0");
+}
+// LDS address of a shared-memory object, as a wave-uniform (scalar) value
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
 }
 
 // Wait until at most N of this wave's vector-memory operations are still
@@ -1246,26 +1248,32 @@ __global__ void __launch_bounds__(512, 1) scan_wide_kernel(ScanParams p) {
     // of the step (two 1 KB halves of its 2 KB unit) and query block w (rows
     // 32 w + 16 r + lane % 16, the lane's 16 bytes at column 8 (lane / 16)
     // of the unit), plus, at u = 0, wave 0 the step's 256 row norms.
-    const char* Xb = (const char*)p.X + rowBeg * p.dpad * ES;
+    // (addresses: the lane's piece of block w of step 0, of the split's first
+    // tile, and of its two query rows; LDS addresses scalar)
     const int64_t xBlk = (int64_t)32 * p.dpad * ES;
+    const int64_t xStep = 8 * xBlk;
+    const char* xw = (const char*)p.X + rowBeg * p.dpad * ES + wave * xBlk + lane * 16;
+    const char* xr = (const char*)p.X + rowBeg * p.dpad * ES + (wave & 3) * xBlk + lane * 16;
     const char* qsrc[2];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         const int row = qb * kWT + wave * 32 + r * 16 + (lane & 15);
         qsrc[r] = (const char*)p.Q + (int64_t)(row < p.nq ? row : qb * kWT) * p.dpad * ES + (lane >> 4) * 16;
     }
+    const int waveS = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t dOp = lds_addr(sOp) + waveS * 2048;
+    const uint32_t dXn = lds_addr(sXn);
     auto copyStage = [&](int t, int u, int buf) {
-        char* dst = sOp + buf * kWideStageBytes + wave * 2048;
-        const int blk = 2 * t + (wave >> 2) < tiles ? t * 8 + wave : (wave & 3);
-        const char* xs = Xb + blk * xBlk + u * 2048 + lane * 16;
+        const uint32_t dst = dOp + buf * kWideStageBytes;
+        const char* xs = (2 * t + (waveS >> 2) < tiles ? xw + t * xStep : xr) + u * 2048;
         lds_copy16(xs, dst);
         lds_copy16(xs + 1024, dst + 1024);
         lds_copy16(qsrc[0] + u * 64, dst + kWideStageBytes / 2);
         lds_copy16(qsrc[1] + u * 64, dst + kWideStageBytes / 2 + 1024);
-        if (PRE && u == 0 && wave == 0) {
+        if (PRE && u == 0 && waveS == 0) {
             const bool nv = 2 * t + (lane >= 32 ? 1 : 0) < tiles;
             lds_copy16(p.xnorm + rowBeg + (nv ? (int64_t)t * kWT + lane * 4 : (int64_t)(lane & 31) * 4),
-                       sXn + (t & 1) * kWT);
+                       dXn + (t & 1) * kWT * 4);
         }
     };
 
