@@ -286,9 +286,10 @@ struct FlatIndex::Impl {
         return c;
     }
     // fp16/bf16 batches of more than 128 queries at a d beyond scan_resident
-    // run the wide-tile kernel for every pass (MFLAT_WIDE=0: the 128-query
-    // tiled kernel instead, read when the index is created). Split plans then
-    // count 256-query blocks: they are given half the query count.
+    // run their sample and full passes on the wide-tile kernel, their retry
+    // window on the 128-query tiled kernel (same keys); MFLAT_WIDE=0 (read
+    // when the index is created) keeps every pass on the tiled kernel. Split
+    // plans of wide passes count 256-query blocks: they get half the query count.
     int wideKnob = 1;
     bool wideBatch(int64_t mb) const {
         return wideKnob && wide_scan_applies((int)std::min<int64_t>(mb, 1 << 30), dpad, storage);
