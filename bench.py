@@ -55,7 +55,7 @@ MEASURED_TRAFFIC_BYTES = {
     ("C2", 10_000, "f32"): 4.636e9,
     ("C2", 10_000, "f16"): 2.090e9,
     ("C3", 10_000, "f32"): 239.84e9,
-    ("C3", 10_000, "bf16"): 22.1e9,
+    ("C3", 10_000, "bf16"): 22.0e9,
     ("C4", 1, "f32"): 3.881e9,
     ("C4", 1, "f16"): 1.961e9,
     ("C4", 64, "f16"): 1.970e9,
