@@ -54,10 +54,14 @@ MEASURED_TRAFFIC_BYTES = {
     ("C1", 1_000, "f32"): 61.9e6,
     ("C2", 10_000, "f32"): 4.636e9,
     ("C2", 10_000, "f16"): 2.090e9,
+    ("C2", 10_000, "bf16"): 2.084e9,
     ("C3", 10_000, "f32"): 239.84e9,
     ("C3", 10_000, "bf16"): 22.0e9,
     ("C4", 1, "f32"): 3.881e9,
     ("C4", 1, "f16"): 1.961e9,
+    ("C4", 16, "f32"): 3.882e9,
+    ("C4", 16, "f16"): 1.963e9,
+    ("C4", 64, "f32"): 3.890e9,
     ("C4", 64, "f16"): 1.970e9,
     ("C5", 2_000_000, "f32"): 30.7e9,
     # IVF fine scan (both launches of a search), C2's data, nlist 1000, nprobe 62
