@@ -208,6 +208,8 @@ struct Plan {
     int64_t Rb = 0;
     int strideb = 1;
     int jb = 1;
+    int jb2 = 0;          // its looser rank (0: none): the retries' first bound, with j2's
+
     int64_t rpsb = 0;
     int nsplitb = 1, capb = 1;
     int64_t rps1 = 0;
@@ -248,7 +250,7 @@ struct FlatIndex::Impl {
     // per-search workspace
     DevBuf stage, inv, qin, outIds, outVals;
     DevBuf qbuf, qh, qnorm, cand, cnt;
-    DevBuf tauSk, tauSi, tauS2k, tauS2i, tauGk, tauGi, tauKk, tauKi, tauBk, tauBi, status;
+    DevBuf tauSk, tauSi, tauS2k, tauS2i, tauGk, tauGi, tauKk, tauKi, tauBk, tauBi, tauB2k, tauB2i, status;
     DevBuf cQ, cQn;
     DevBuf best, total;
     RetryStore rl;
@@ -508,6 +510,12 @@ struct FlatIndex::Impl {
         const double e1 = (double)pl.jb * (double)nb / (double)pl.Rb;
         pl.e1 = e1;
         pl.cap1 = std::max<int>({2 * k, 64, pow2ceil((int64_t)(2.0 * e1 / pl.nsplit1) + 64)});
+        // A query with too few rows under the jb-th best reruns first under
+        // the tighter of the first sample's j2-th best (~j2 nb / R0 rows) and
+        // this sample's jb2-th best (~jb2 nb / Rb rows, where it stored that
+        // many), both at a 1e-9 miss rate.
+        const int jb2 = chooseJ(k, (double)k * (double)pl.Rb / (double)nb, 1e-9);
+        pl.jb2 = jb2 > pl.jb && pl.j2 > pl.j ? jb2 : 0;
     }
 
     void growRows(int64_t need, hipStream_t s) {
@@ -703,12 +711,20 @@ struct FlatIndex::Impl {
             scan(smp[1].X.p, smp[1].xn.as<float>(), pl.Rb, pl.rpsb, pl.nsplitb, pl.strideb, Q, qn, mb,
                  tauSk.as<float>(), tauSi.as<int>(), pl.capb, s, kPassSample);
             tauBk.ensure((size_t)mb * 4); tauBi.ensure((size_t)mb * 4);
-            SelectParams sp = selectParams(mb, pl.nsplitb, pl.capb, pl.jb, pl.jb);
-            sp.tau_k_key = tauBk.as<float>(); sp.tau_k_id = tauBi.as<int>();
+            SelectParams sp = selectParams(mb, pl.nsplitb, pl.capb, pl.jb2 ? pl.jb2 : pl.jb, pl.jb);
+            if (pl.jb2) {
+                tauB2k.ensure((size_t)mb * 4); tauB2i.ensure((size_t)mb * 4);
+                sp.tau_j_key = tauBk.as<float>(); sp.tau_j_id = tauBi.as<int>();
+                sp.tau_k_key = tauB2k.as<float>(); sp.tau_k_id = tauB2i.as<int>();
+            } else {
+                sp.tau_k_key = tauBk.as<float>(); sp.tau_k_id = tauBi.as<int>();
+            }
             // ~j Rb / R0 candidates a query, spread as an order statistic
             sp.expect = (int)std::min(3.0 * (double)pl.j * (double)pl.Rb / (double)pl.R0 + 64.0, 1e9);
             launch_select(sp, s);
             launch_tau_min(tauSk.as<float>(), tauSi.as<int>(), tauBk.as<float>(), tauBi.as<int>(), mb, s);
+            if (pl.jb2)
+                launch_tau_min(tauS2k.as<float>(), tauS2i.as<int>(), tauB2k.as<float>(), tauB2i.as<int>(), mb, s);
         }
         // L1: full database with the speculative bound
         scan(X.p, xn.as<float>(), nb, pl.rps1, pl.nsplit1, 1, Q, qn, mb,
@@ -798,6 +814,7 @@ struct FlatIndex::Impl {
                   rr.batchSmall ? 1 : kRetryMinTiles, concurrency(kPassRetry, false));
         // j2 reruns, the usual kind: ~j2 nb / R0 candidates
         rr.expect = 1.5 * std::max(pl.j2, 2) * (double)nb / std::max<double>(1.0, (double)pl.R0) + 2.0 * k;
+        if (pl.jb2) rr.expect = 1.5 * pl.jb2 * (double)nb / (double)pl.Rb + 2.0 * k;
 
         rl.ensure(mb, rmax, s);
         cQ.ensure((size_t)rr.rowsPad * rr.rowBytes);
@@ -1020,7 +1037,7 @@ FlatIndex::~FlatIndex() {
     for (auto& sm : d_->smp) sm.release();
     for (DevBuf* b : {&d_->X, &d_->xn, &d_->stage, &d_->inv, &d_->qin, &d_->outIds,
                       &d_->outVals, &d_->qbuf, &d_->qh, &d_->qnorm, &d_->cand, &d_->cnt, &d_->tauSk, &d_->tauSi, &d_->tauS2k, &d_->tauS2i, &d_->maxBits,
-                      &d_->tauGk, &d_->tauGi, &d_->tauKk, &d_->tauKi, &d_->tauBk, &d_->tauBi, &d_->status, &d_->cQ, &d_->cQn,
+                      &d_->tauGk, &d_->tauGi, &d_->tauKk, &d_->tauKi, &d_->tauBk, &d_->tauBi, &d_->tauB2k, &d_->tauB2i, &d_->status, &d_->cQ, &d_->cQn,
                       &d_->best, &d_->total})
         b->release();
     d_->rl.release();
