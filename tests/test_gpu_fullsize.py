@@ -67,6 +67,28 @@ def test_c3_full(gpu_ok):
     compare("C3", gi, gd, x, q, np.arange(0, q.shape[0], 31), 100, IP)
 
 
+def test_c2_full_fp16(gpu_ok):
+    """C2 with fp16 storage: the second sample level, the full pass and the
+    retry round with the second sample's looser rank (about 90 queries rerun);
+    every 20th query (500) checked against the oracle on the rounded inputs."""
+    x, q = datagen.gmm()
+    gi, gd = gpu_search(x, q, 100, L2, mflat.MFLAT_STORAGE_F16)
+    xs, qs, m = oracle.storage_inputs(x, q, L2, mflat.MFLAT_STORAGE_F16)
+    del x, q
+    compare("C2 fp16", gi, gd, xs, qs, np.arange(0, qs.shape[0], 20), 100, m)
+
+
+def test_c3_full_bf16(gpu_ok):
+    """C3 with bf16 storage: the wide-tile kernel (sample and full passes) and
+    the retry window on the 128-query tiled kernel; every 50th query (200)
+    checked against the oracle on the rounded inputs."""
+    x, q = datagen.unit_normal()
+    gi, gd = gpu_search(x, q, 100, IP, mflat.MFLAT_STORAGE_BF16)
+    xs, qs, m = oracle.storage_inputs(x, q, IP, mflat.MFLAT_STORAGE_BF16)
+    del x, q
+    compare("C3 bf16", gi, gd, xs, qs, np.arange(0, qs.shape[0], 50), 100, m)
+
+
 @pytest.fixture(scope="module")
 def c4_data():
     t0 = time.perf_counter()
